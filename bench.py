@@ -1,0 +1,212 @@
+"""Benchmark of the 800h decode path on one MI355X: BASELINE config 3, one layer of paged split-K decode attention
+over 64 sequences x 32,768 tokens (127 quantized 256-token sub-blocks + 256 exact tokens per sequence, permuted page
+tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape; same bytes and flops per token as
+32 / 8 / 64).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--calib]
+
+A step = one kv800.decode call (decode_quant + decode_exact + decode_merge kernels) over one layer. Inputs are
+resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one JSON line.
+roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average duration, timed
+with HIP events on its own stream; cpu_baseline: the CPU oracle (a C restatement of torch_decode.py) on a bounded
+sample of the same workload. --calib runs a plain copy of known size instead (for rocprof FETCH/WRITE calibration)."""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+B, N_CTX, EBS = 64, 32768, 128
+NQ = (N_CTX - 128) // 256                           # 127 flushed sub-blocks per sequence
+QBYTES = B * NQ * 51200                             # compressed bytes read by the quantized-split kernel
+XBYTES = B * (N_CTX - NQ * 256) * 2048              # exact tail bytes (256 tokens x 4 heads x (K + V) bf16)
+ALG_BYTES = QBYTES + XBYTES                         # the reference's accounting (nvidia/check_nvidia.py:563)
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def build_layer(torch, kh, seed, dev):
+    """One layer's cache for the 64 x 32K workload: sub-blocks quantized on the GPU by the HIP quantizer from seeded
+    bf16 N(0,1) K / V, written through a random permutation of the quant pool; exact pages permuted likewise."""
+    import lfm3_kv800_amd.kv800 as kv
+    g = torch.Generator(device=dev).manual_seed(seed)
+    boff = (torch.randperm(B * NQ, generator=g, device=dev).view(B, NQ) * 51200).to(torch.int64)
+    qpool = torch.empty(B * NQ * 51200, dtype=torch.uint8, device=dev)
+    for b0 in range(0, B, 8):
+        k = torch.randn(8 * NQ, 256, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(8 * NQ, 256, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+        sb = kh.quantize_blocks(k, v)
+        idx = boff[b0:b0 + 8].reshape(-1)[:, None] + torch.arange(51200, device=dev)
+        qpool[idx.reshape(-1)] = sb.reshape(-1)
+        del k, v, sb, idx
+    pages = N_CTX // EBS
+    ex0 = NQ * 256 // EBS
+    npg = B * (pages - ex0)
+    eoff = torch.zeros(B, pages, dtype=torch.int64, device=dev)
+    eoff[:, ex0:] = torch.randperm(npg, generator=g, device=dev).view(B, pages - ex0) * (4 * EBS * 256)
+    epool = torch.randn(npg, 4, EBS, 256, generator=g, device=dev).to(torch.bfloat16)
+    N = torch.full((B,), N_CTX, dtype=torch.int32, device=dev)
+    NQt = torch.full((B,), NQ, dtype=torch.int32, device=dev)
+    return kv.Paged(qpool=qpool, boff=boff, epool=epool, eoff=eoff, ebs=EBS, e_hs=EBS * 256, e_ts=256, e_v=128,
+                    sk=None, sv=None, skoff=None, svoff=None, N=N, NQ=NQt, nqmax=NQ, win=0)
+
+
+def rope_tables(torch, n, dev):
+    """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
+    inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
+    fr = torch.arange(n, dtype=torch.float32)[:, None] * inv[None]
+    return fr.cos().to(torch.bfloat16).to(dev), fr.sin().to(torch.bfloat16).to(dev)
+
+
+def cpu_baseline(torch, P, q, cos, sin, rows):
+    """Oracle decode (oracle/kv800_oracle.c, torch_decode.py semantics) of `rows` rows, on this host's cores."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    C = lambda t: t.detach().cpu().contiguous().numpy()
+    B16 = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    sel = list(range(rows))
+    # the rows' sub-blocks only, re-addressed into a compact pool
+    boff = C(P.boff)[sel]
+    qp = P.qpool.view(-1, 51200)
+    blocks = torch.from_numpy((boff // 51200).reshape(-1)).to(P.qpool.device)
+    qpool = C(qp.index_select(0, blocks))
+    boff_c = (np.arange(rows * NQ, dtype=np.int64) * 51200).reshape(rows, NQ)
+    case = oracle.PagedCase(qpool=qpool, boff=boff_c, epool=B16(P.epool), eoff=C(P.eoff)[sel], ebs=P.ebs, e_hs=P.e_hs,
+                            e_ts=P.e_ts, e_v=P.e_v, sk=np.zeros(1, np.uint16), sv=np.zeros(1, np.uint16),
+                            skoff=np.zeros(rows, np.int64), svoff=np.zeros(rows, np.int64), sinks=False,
+                            N=C(P.N)[sel], NQ=C(P.NQ)[sel], nqmax=NQ, win=0, B=rows)
+    qb, cb, sb = B16(q)[sel], B16(cos), B16(sin)
+    oracle.decode(case, qb[:1], cb, sb) if rows > 1 else None        # page in
+    t0 = time.perf_counter()
+    oracle.decode(case, qb, cb, sb)
+    dt = time.perf_counter() - t0
+    return dt, oracle.num_threads()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=8)
+    ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the 800h path shards by "
+              "sequence with no exchange, so N GPUs would run N independent copies of this workload", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import lfm3_kv800_amd.kv800_hip as kh
+    kh.ops()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    if a.calib:
+        x = torch.empty(1 << 28, dtype=torch.int32, device=dev)      # 1 GiB
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(a.steps):
+            y.copy_(x)
+        e1.record(); e1.synchronize()
+        ms = e0.elapsed_time(e1) / a.steps
+        print(json.dumps({"calib": "copy", "bytes_read": x.numel() * 4, "bytes_written": x.numel() * 4,
+                          "ms": ms, "gbps": 2 * x.numel() * 4 / ms / 1e6}))
+        return
+
+    t_build = time.perf_counter()
+    layers = [build_layer(torch, kh, seed, dev) for seed in (1, 2)]
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(B, 16, 128, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = rope_tables(torch, N_CTX, dev)
+    kh.rope_table16(cos, sin)                                          # model-constant table, built once
+    torch.cuda.synchronize()
+    log(f"built 2 cache copies in {time.perf_counter() - t_build:.1f} s")
+
+    # ---- whole-layer timing: W warmup + K timed steps, synchronized on both sides
+    for i in range(a.warmup):
+        kh.decode(layers[i & 1], q, cos, sin)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        kh.decode(layers[i & 1], q, cos, sin)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / a.steps
+
+    # ---- dominant kernel alone (decode_quant), HIP events on the stream it runs on
+    import ctypes
+    L = kh.ops()
+    s = torch.cuda.Stream(device=dev)
+    ns, spb = kh.plan(B, NQ)
+    MO = torch.empty(B, ns + 1, 16, dtype=torch.float32, device=dev)
+    LO = torch.empty_like(MO)
+    AO = torch.empty(B, ns + 1, 16, 128, dtype=torch.float32, device=dev)
+    cs16 = kh.rope_table16(cos, sin)
+    scale = 128 ** -0.5 * 1.4426950408889634
+    structs = [kh.paged_struct(P, B) for P in layers]
+
+    def quant(i):
+        P, (st, qbytes, _, _) = layers[i & 1], structs[i & 1]
+        rc = L.kv800_hip_decode_quant_sized(ctypes.c_void_p(q.data_ptr()), st.qpool, qbytes, st.boff, st.boff_stride,
+                                            ctypes.c_void_p(P.NQ.data_ptr()), ctypes.c_void_p(cs16.data_ptr()),
+                                            cos.shape[0], ctypes.c_void_p(MO.data_ptr()), ctypes.c_void_p(LO.data_ptr()),
+                                            ctypes.c_void_p(AO.data_ptr()), B, ns, spb, scale,
+                                            ctypes.c_void_p(s.cuda_stream))
+        assert rc == 0, L.kv800_hip_last_error()
+
+    with torch.cuda.stream(s):
+        for i in range(a.warmup):
+            quant(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(a.steps):
+            quant(i)
+        e1.record(s)
+    e1.synchronize()
+    ms_quant = e0.elapsed_time(e1) / a.steps
+    torch.cuda.synchronize()
+
+    out = kh.decode(layers[0], q, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+
+    achieved = QBYTES / (ms_quant * 1e-3) / 1e9
+    layer_gbps = ALG_BYTES / (ms_step * 1e-3) / 1e9
+    cpu = None
+    if not a.no_cpu:
+        rows = max(1, min(B, a.cpu_rows))
+        dt, cores = cpu_baseline(torch, layers[0], q, cos, sin, rows)
+        cpu = {"value": dt * 1e3 * B / rows, "unit": "ms/layer (64x32K, extrapolated from the sample)", "cores": cores,
+               "kind": "port", "sample": f"oracle decode of rows 0..{rows - 1} of the 64 x 32768 layer "
+                                         f"({dt:.2f} s), scaled by 64/{rows}"}
+    res = {
+        "metric": "800h decode ms/layer @64x32K",
+        "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8 codes / fp16 MFMA / fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "C3: one layer paged decode, 64 seqs x 32768 tokens, 16 q / 4 kv heads x 128, "
+                               "NQ=127 sub-blocks + 256 exact tokens per seq, permuted page tables, 2 rotating copies",
+                   "global_batch": B, "seq_len": N_CTX, "parallelism": "none (1 GPU)"},
+        "layer": {"algorithmic_bytes": ALG_BYTES, "gbps": round(layer_gbps, 1),
+                  "hbm_frac": round(layer_gbps / HBM_PEAK_GBS, 4), "decode_tok_s": round(B / (ms_step * 1e-3), 1)},
+        "roofline": {"bound": "hbm", "kernel": "decode_quant_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel_ms": round(ms_quant, 5), "bytes_per_launch": QBYTES},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/* kv800_hip.h -- C ABI of the MI355X (gfx950) backend of the lfm3-kv800 800h compressed KV-cache path.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (HIP), except `kv800_paged_t` itself, which lives on the host and is read
+ *     before launch. Offsets and strides are int64; byte offsets into the quant pool, element offsets (bf16) into
+ *     the exact pool and the sink buffers, as in the reference's Paged descriptor (kv800.py:239-248).
+ *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream); NULL = default stream.
+ *     Launches are asynchronous: no entry point synchronizes, allocates or frees device memory.
+ *   - Return 0 on success, otherwise a negative status; kv800_hip_last_error() returns a message for the calling
+ *     thread's most recent failure. Invalid arguments are rejected on the host before any launch.
+ *   - Layouts: quantized sub-block = 51,200 bytes (kv800.py:3-10): kc [256,4,32] | vb [256,4,16] | vlo [256,2] |
+ *     vsc [256,2] | klo [4,128] | ksc [4,128]; exact token rows bf16 pre-RoPE K | unrotated V (V at +e_v elements).
+ *   - Head shape is fixed by the format: 16 query heads over 4 KV heads, head_dim 128.
+ */
+#ifndef KV800_HIP_H
+#define KV800_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KV800_OK 0
+#define KV800_EINVAL (-1)   /* bad argument (checked on the host) */
+#define KV800_EHIP (-2)     /* HIP runtime error at launch */
+
+/* Paged descriptor of one layer; field for field kv800.Paged (kv800.py:239-248). */
+typedef struct kv800_paged {
+  const uint8_t* qpool;        /* quant pool base (bytes) */
+  const int64_t* boff;         /* (B, boff_stride) byte offsets of sub-block j of row b */
+  int64_t boff_stride;
+  const uint16_t* epool;       /* exact pool base (bf16 elements) */
+  const int64_t* eoff;         /* (B, eoff_stride) element offsets of the exact page holding position p (p / ebs) */
+  int64_t eoff_stride;
+  int64_t ebs, e_hs, e_ts, e_v;/* tokens per exact page; element strides of head, token; V offset from K */
+  const uint16_t* sk;          /* sink K base (bf16) or NULL: no sinks (kv800.py:378-382) */
+  const uint16_t* sv;          /* sink V base (bf16) */
+  const int64_t* skoff;        /* (B,) element offsets of the [4 sinks, 4 heads, 128] K block of row b */
+  const int64_t* svoff;        /* (B,) same for V */
+  const int32_t* N;            /* (B,) sequence length including the current token */
+  const int32_t* NQ;           /* (B,) flushed sub-blocks */
+  int64_t nqmax;               /* host bound >= max(NQ) (0 on window layers) */
+  int64_t win;                 /* 0: quantized layer; 256: window + sinks layer */
+} kv800_paged_t;
+
+/* Version of this ABI (major * 100 + minor). */
+int kv800_hip_version(void);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char* kv800_hip_last_error(void);
+
+/* Quantize M dense sub-blocks. Replaces kv800.quantize_blocks (kv800.py:56-76).
+ * k, v: (M, 256, 4, 128) bf16 (pre-RoPE K, unrotated V), contiguous. out: (M, 51200) bytes.
+ * Bit-identical to the reference on CPU torch (fp8 e4m3fn RNE encode, IEEE division, v @ H as the sequential
+ * fused multiply-add chain torch-CPU evaluates). */
+int kv800_hip_quantize_blocks(const uint16_t* k, const uint16_t* v, int64_t M, uint8_t* out, void* stream);
+
+/* Paged flush of the sub-blocks that became eligible. Replaces the flush plan + quantize of vllm_attn.py:297-317
+ * (and the PagedStore flush loop, kv800.py:433-440) with one launch and no host loop:
+ *   for every row r < R and sub-block j in [nq_prev[r], nq_new[r]) (at most max_new per row):
+ *     gather tokens [256 j, 256 j + 256) of row r from the exact pool (K at eoff[r, p / ebs] + h e_hs + (p % ebs) e_ts,
+ *     V at + e_v), quantize, and write the 51,200-byte sub-block to
+ *     qpool + qbt[r, (256 j) / bsq] * qs0 + ((256 j) % bsq) / 256 * 51200.
+ * vLLM geometry: qbt = the quant layer's block table, bsq = 1280 tokens per quant page, qs0 = 262144 bytes.
+ * PagedStore geometry: qbt = boff (byte offsets), bsq = 256, qs0 = 1. */
+int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_stride, int64_t ebs, int64_t e_hs,
+                    int64_t e_ts, int64_t e_v, uint8_t* qpool, const int64_t* qbt, int64_t qbt_stride, int64_t bsq,
+                    int64_t qs0, const int32_t* nq_prev, const int32_t* nq_new, int64_t R, int64_t max_new,
+                    void* stream);
+
+/* Dequantize M sub-blocks. Replaces kv800.dequantize_blocks (kv800.py:79-92).
+ * k_out: (M, 256, 4, 128) bf16 = bf16(code * ksc + klo); v_out: (M, 256, 4, 128) f32 = (bit * vsc + vlo) @ H. */
+int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, float* v_out, void* stream);
+
+/* fp16 (cos, sin) pair table used by the quantized-decode kernel: cs16[p * 32 + j] = fp16(cos[p, j]) |
+ * fp16(sin[p, j]) << 16 for p < P. cos_t, sin_t: (>= P, 32) bf16. No reference counterpart (it reads the bf16
+ * tables per token, kv800.py:146-147); the conversion is exact for every value the tables can hold above 2^-17. */
+int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs16, void* stream);
+
+/* Split-K partial attention over the flushed sub-blocks. Replaces torch.ops.kv800.qdecode (kv800_sycl.sycl:510-526,
+ * Triton _qdec kv800.py:120-170). For each row b and split s < ns: sub-blocks [s spb, min((s+1) spb, nq[b])) ->
+ * mo, lo (B, ns+1, 16) and ao (B, ns+1, 16, 128) at slot s, V in the Hadamard domain (acc + sum p vlo).
+ * q: (B, 16, 128) bf16 post-RoPE; cs16: kv800_hip_rope_table of rows >= max(nq) * 256; scale = log2(e)/sqrt(128). */
+int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
+                           const int32_t* nq, const uint32_t* cs16, float* mo, float* lo, float* ao, int64_t B,
+                           int64_t ns, int64_t spb, float scale, void* stream);
+
+/* Sinks + exact tail. Replaces torch.ops.kv800.xdecode (kv800_sycl.sycl:528-542, Triton _xdec kv800.py:197-228):
+ * positions [lo_e, N[b]) with lo_e = NQ[b] * 256 (window layers: max(lo_e, N - win)) and, when P->sk != NULL,
+ * sinks at positions < min(4, lo_e, N) -> slot ns of mo / lo / ao. cos_t, sin_t: (>= max(N), 32) bf16. */
+int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                           float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream);
+
+/* LSE merge of the ns + 1 slots. Replaces torch.ops.kv800.combine (kv800_sycl.sycl:544-551, kv800.combine
+ * kv800.py:231-236): H (FWHT) on the quantized slots, exact slot as is, bf16 (B, 16, 128) out. */
+int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, int64_t B, int64_t ns, uint16_t* out,
+                           void* stream);
+
+/* Split plan used by kv800_hip_decode when spb <= 0 (kv800.py:366-367 plans for the reference kernels). */
+int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb);
+
+/* Workspace bytes kv800_hip_decode needs for B rows, ns splits and rope rows (0 if cs16 is passed in). */
+int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows);
+
+/* Fused decode of one layer. Replaces kv800.decode's backend body (kv800.py:352-383): plan, [rope table],
+ * decode_quant, decode_exact, decode_merge, all on `stream`. cs16 may be NULL (then it is built in the
+ * workspace from cos_t / sin_t for the nqmax * 256 rows the quantized kernel reads). spb <= 0: kv800_hip_plan. */
+int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                     const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
+                     int64_t workspace_bytes, int64_t spb, void* stream);
+
+/* Bounds-checked forms used by the Python layer. They take the extent of every pool the kernels read, measured from
+ * the pointer passed in: qpool_bytes (bytes), epool_elems / sink_elems (bf16 elements), rope_rows (rows of cos_t /
+ * sin_t and of cs16). A sub-block, page or row whose offset falls outside its pool is skipped instead of read, so a
+ * malformed table yields a wrong (finite) result rather than a memory fault. The unsized forms above pass
+ * INT64_MAX / 2 for every extent. No reference counterpart: the reference's kernels read unchecked. */
+int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
+                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows,
+                                 float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
+                                 void* stream);
+int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t,
+                                 const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
+                                 float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream);
+int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs16, int64_t qpool_bytes,
+                           int64_t epool_elems, int64_t sink_elems, uint16_t* out, void* workspace,
+                           int64_t workspace_bytes, int64_t spb, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KV800_HIP_H */

@@ -1,0 +1,692 @@
+// kv800_decode.hip -- paged split-K decode attention over the 800h cache for gfx950, and its C-ABI entry points.
+//
+// Semantics (kv800.py:120-236, kv800_sycl.sycl:48-504, torch_decode.py:16-80): for each row b, 16 query rows over
+// 4 KV heads (GQA 4), head_dim 128, scores q . RoPE(K) with RoPE on the dim pairs (d, d + 64), d < 32, fp32 online
+// softmax in log2 units (scale = log2(e) / sqrt(128)); flushed sub-blocks contribute 2-bit K and 1-bit
+// Hadamard-domain V, the exact tail / sinks bf16 K (rotated, rounded to bf16) and V; splits are merged by
+// log-sum-exp, with the 128-point Hadamard applied once to the merged quantized part.
+//
+// Kernels
+//   rope_table_kernel   bf16 (cos, sin) tables -> packed fp16 pairs (exact for every table value above 2^-17).
+//   decode_quant_kernel one workgroup (4 waves) per (row b, split s); each wave owns whole 256-token sub-blocks and
+//                       reads them with 16-byte coalesced loads of all 4 heads at once.
+//     QK on MFMA f32_16x16x32_f16: M = 16 tokens, N = the 16 query rows, K = per-token features of head g supplied
+//       by lane group g (block-diagonal weights). With f = 1 + code / 4 (exact in fp16 from the code bits) and
+//       per-channel k = 4 ksc f + (klo - 4 ksc), RoPE is moved onto exact fp16 features:
+//         rope dims: (cos f0, sin f0, cos f2, sin f2) x weights (q0 S0, q2 S0, q2 S2, -q0 S2), S = 4 ksc scale
+//         nope dims: (f1, f3)                         x weights (q1 S1, q3 S3)
+//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2) (all 16 rows)
+//       and the per-row constant sum(q1 T1 + q3 T3) initialises the accumulator. Weights are rebuilt per sub-block.
+//     PV on the same MFMA: M = 16 dims (one bit plane), N = the 16 rows, K = 32 tokens. The bit feature is the
+//       fp16 subnormal bit 2^(i - 24) (one AND per two tokens; MFMA keeps fp16 subnormal inputs exactly), the
+//       weights fp16(p vsc); plane i is scaled back by 2^(24 - i) at the end.
+//     Softmax with a lazy running max (rescale only when a tile max exceeds it by more than 8 log2 units).
+//   decode_exact_kernel one workgroup per (row b, KV head h): sinks + exact positions, SIMT fp32.
+//   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT.
+#include <math.h>
+
+#include "kv800_common.h"
+#include "../../include/kv800_hip.h"
+
+namespace kv800 {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+constexpr float NEG_BIG = -1e30f;
+constexpr float LAZY = 8.f;   // log2 units a tile max may exceed the running max before the state is rescaled
+
+__device__ __forceinline__ uint32_t hbits(h2 x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+__device__ __forceinline__ h8 pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u4v v = {a, b, c, d};
+  return __builtin_bit_cast(h8, v);
+}
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ uint32_t pk2(float a, float b) {   // two floats -> packed fp16 (round to nearest even)
+  h2 v = {(_Float16)a, (_Float16)b};
+  return hbits(v);
+}
+
+// ---------------------------------------------------------------- rope table
+__global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int64_t n,
+                                  uint32_t* __restrict__ cs16) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  cs16[i] = pk2(bf2f(cos_t[i]), bf2f(sin_t[i]));
+}
+
+// ---------------------------------------------------------------- quantized sub-blocks
+constexpr int QWAVES = 4;
+struct QWaveLds {
+  uint8_t kls[1024];          // klo [4][128] | ksc [4][128] of the current sub-block
+  float vs[2][256];           // decoded vsc per (head group, token)
+  float vl[2][256];           // decoded vlo
+  uint8_t vb[2][32 * 64];     // vb bytes of a 32-token chunk (double buffer)
+  uint32_t cs[2][32 * 32];    // fp16 (cos, sin) rows of the chunk's 32 positions (double buffer)
+};
+struct QLds {
+  float q[16][128];
+  QWaveLds wv[QWAVES];
+};
+struct QFinLds {              // end-of-split merge of the 4 waves (reuses the LDS)
+  float m[QWAVES][16], l[QWAVES][16], lv[QWAVES][16];
+  float acc[QWAVES][16][128];
+};
+static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
+
+__device__ __forceinline__ float f8b(const uint8_t* p, int i) { return f8d(p[i]); }
+
+__global__ void __launch_bounds__(256, 2)
+decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
+                    const int64_t* __restrict__ boff, int64_t bstride, const int32_t* __restrict__ nq,
+                    const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
+                    float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale) {
+  __shared__ __align__(16) char lds_raw[sizeof(QLds)];
+  QLds& L = *reinterpret_cast<QLds*>(lds_raw);
+  const int b = blockIdx.x / ns, s = blockIdx.x % ns;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, n = lane & 15, hn = n >> 2;
+  QWaveLds& W = L.wv[w];
+
+  for (int i = tid; i < 16 * 128; i += 256) L.q[i >> 7][i & 127] = bf2f(q[(int64_t)b * 2048 + i]);
+  __syncthreads();
+
+  float m = NEG_BIG, lsum = 0.f, lvs = 0.f;
+  f4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+
+  int j1 = min((s + 1) * spb, nq[b]);
+  if (j1 > bstride) j1 = (int)bstride;
+  const int j0 = s * spb;
+  for (int jb = j0 + w; jb < j1; jb += QWAVES) {
+    const int64_t base = boff[(int64_t)b * bstride + jb];
+    if (base < 0 || base + SUB > qpool_bytes || (int64_t)(jb + 1) * BLK > rope_rows) continue;   // guard
+    const uint8_t* sb = qpool + base;
+    const uint32_t* csb = cs16 + (int64_t)jb * BLK * 32;
+
+    // ---- stage per-sub-block scales: klo / ksc (1 KB), vlo / vsc decoded (256 tokens x 2 groups)
+    *reinterpret_cast<uint4*>(W.kls + 16 * lane) = *reinterpret_cast<const uint4*>(sb + KLO_O + 16 * lane);
+    {
+      const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
+      const uint2 vs2 = *reinterpret_cast<const uint2*>(sb + VSC_O + 8 * lane);
+      // bytes 8 lane + e -> token (8 lane + e) / 2, group (8 lane + e) & 1
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lb = ((e < 4 ? vl2.x : vl2.y) >> (8 * (e & 3))) & 0xFFu;
+        const uint32_t sbt = ((e < 4 ? vs2.x : vs2.y) >> (8 * (e & 3))) & 0xFFu;
+        const int t = 4 * lane + (e >> 1), gg = e & 1;
+        W.vl[gg][t] = f8d(lb);
+        W.vs[gg][t] = f8d(sbt);
+      }
+    }
+    // ---- prefetch chunk 0 (vb bytes, rope rows, kc rows of tiles 0 / 1)
+    uint4 vbn0 = *reinterpret_cast<const uint4*>(sb + VB_O + 32 * lane);
+    uint4 vbn1 = *reinterpret_cast<const uint4*>(sb + VB_O + 32 * lane + 16);
+    uint4 csn[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const uint4*>(csb + 256 * u + 4 * lane);
+    const uint8_t* kcb = sb + KC_O + g * 32;
+    uint4 kn[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint8_t* p = kcb + (int64_t)(16 * u + n) * 128;
+      kn[u][0] = *reinterpret_cast<const uint4*>(p);
+      kn[u][1] = *reinterpret_cast<const uint4*>(p + 16);
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- weights of this sub-block (B operands), scaled by `scale` so the accumulator is in log2 units
+    const bool act = (hn == g);
+    const uint8_t* ksc_g = W.kls + 512 + g * 128;
+    const uint8_t* klo_n = W.kls + hn * 128;
+    const uint8_t* ksc_n = W.kls + 512 + hn * 128;
+    const float* qn = L.q[n];
+    h8 wr[16], wnp[8], wt[2];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        uint32_t hw[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int j = 4 * d + 2 * e2 + u;
+          const float s0 = act ? 4.f * scale * f8b(ksc_g, j) : 0.f;
+          const float s2 = act ? 4.f * scale * f8b(ksc_g, j + 64) : 0.f;
+          const float q0 = qn[j], q2 = qn[j + 64];
+          hw[2 * u] = pk2(q0 * s0, q2 * s0);
+          hw[2 * u + 1] = pk2(q2 * s2, -q0 * s2);
+        }
+        wr[2 * d + e2] = pack8(hw[0], hw[1], hw[2], hw[3]);
+      }
+      uint32_t hn4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = 4 * d + u;
+        const float s1 = act ? 4.f * scale * f8b(ksc_g, 32 + j) : 0.f;
+        const float s3 = act ? 4.f * scale * f8b(ksc_g, 96 + j) : 0.f;
+        hn4[u] = pk2(qn[32 + j] * s1, qn[96 + j] * s3);
+      }
+      wnp[d] = pack8(hn4[0], hn4[1], hn4[2], hn4[3]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      uint32_t ht[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = 16 * kk + 4 * g + u;
+        const float t0 = f8b(klo_n, j) - 4.f * f8b(ksc_n, j);
+        const float t2 = f8b(klo_n, j + 64) - 4.f * f8b(ksc_n, j + 64);
+        const float q0 = qn[j], q2 = qn[j + 64];
+        ht[u] = pk2(scale * (q0 * t0 + q2 * t2), scale * (q2 * t0 - q0 * t2));
+      }
+      wt[kk] = pack8(ht[0], ht[1], ht[2], ht[3]);
+    }
+    float c13 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = 8 * g + u;
+      const float t1 = f8b(klo_n, 32 + j) - 4.f * f8b(ksc_n, 32 + j);
+      const float t3 = f8b(klo_n, 96 + j) - 4.f * f8b(ksc_n, 96 + j);
+      c13 += qn[32 + j] * t1 + qn[96 + j] * t3;
+    }
+    c13 += __shfl_xor(c13, 16);
+    c13 += __shfl_xor(c13, 32);
+    c13 *= scale;
+
+    // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
+    for (int c = 0; c < 8; ++c) {
+      const int cb = c & 1;
+      *reinterpret_cast<uint4*>(W.vb[cb] + 32 * lane) = vbn0;
+      *reinterpret_cast<uint4*>(W.vb[cb] + 32 * lane + 16) = vbn1;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(W.cs[cb] + 256 * u + 4 * lane) = csn[u];
+      uint4 kc[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) { kc[u][0] = kn[u][0]; kc[u][1] = kn[u][1]; }
+      if (c + 1 < 8) {   // prefetch the next chunk
+        const uint8_t* vbp = sb + VB_O + (c + 1) * 32 * 64 + 32 * lane;
+        vbn0 = *reinterpret_cast<const uint4*>(vbp);
+        vbn1 = *reinterpret_cast<const uint4*>(vbp + 16);
+        const uint32_t* csp = csb + (c + 1) * 32 * 32;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const uint4*>(csp + 256 * u + 4 * lane);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint8_t* p = kcb + (int64_t)(32 * (c + 1) + 16 * u + n) * 128;
+          kn[u][0] = *reinterpret_cast<const uint4*>(p);
+          kn[u][1] = *reinterpret_cast<const uint4*>(p + 16);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+      uint32_t bpv[4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {   // QK tile u: tokens 32 c + 16 u + (0..15)
+        const uint32_t* csrow = W.cs[cb] + (16 * u + n) * 32;
+        const uint32_t kw[8] = {kc[u][0].x, kc[u][0].y, kc[u][0].z, kc[u][0].w,
+                                kc[u][1].x, kc[u][1].y, kc[u][1].z, kc[u][1].w};
+        f4 sacc = {c13, c13, c13, c13};
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          const uint32_t x = kw[d];
+          const uint32_t Q0 = (x & 0x03030303u) | 0x3C3C3C3Cu;
+          const uint32_t Q2 = ((x >> 4) & 0x03030303u) | 0x3C3C3C3Cu;
+          const uint32_t Q1 = ((x >> 2) & 0x03030303u) | 0x3C3C3C3Cu;
+          const uint32_t Q3 = ((x >> 6) & 0x03030303u) | 0x3C3C3C3Cu;
+          const uint4 cs4 = *reinterpret_cast<const uint4*>(csrow + 4 * d);
+          const uint32_t csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+          uint32_t ga[4], gb[4], f13[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t sel = 0x0Cu | ((uint32_t)e << 8) | (0x0Cu << 16) | ((uint32_t)(4 + e) << 24);
+            const h2 F = as_h2(__builtin_amdgcn_perm(Q2, Q0, sel));
+            const h2 CS = as_h2(csv[e]);
+            ga[e] = hbits(CS * h2{F.x, F.x});
+            gb[e] = hbits(CS * h2{F.y, F.y});
+            f13[e] = __builtin_amdgcn_perm(Q3, Q1, sel);
+          }
+          sacc = mfma16(pack8(ga[0], gb[0], ga[1], gb[1]), wr[2 * d], sacc);
+          sacc = mfma16(pack8(ga[2], gb[2], ga[3], gb[3]), wr[2 * d + 1], sacc);
+          sacc = mfma16(pack8(f13[0], f13[1], f13[2], f13[3]), wnp[d], sacc);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const uint4 t4 = *reinterpret_cast<const uint4*>(csrow + 16 * kk + 4 * g);
+          sacc = mfma16(pack8(t4.x, t4.y, t4.z, t4.w), wt[kk], sacc);
+        }
+        // ---- online softmax (lazy max); rows are columns n, tokens 4 g + i of this tile
+        float tmax = fmaxf(fmaxf(sacc[0], sacc[1]), fmaxf(sacc[2], sacc[3]));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        if (__any(tmax > m + LAZY)) {
+          const float mn = fmaxf(m, tmax);
+          const float al = exp2f(m - mn);
+          m = mn; lsum *= al; lvs *= al;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] *= al;
+        }
+        const int t0 = 32 * c + 16 * u + 4 * g;
+        const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
+        const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);
+        const float p0 = exp2f(sacc[0] - m), p1 = exp2f(sacc[1] - m), p2 = exp2f(sacc[2] - m), p3 = exp2f(sacc[3] - m);
+        lsum += (p0 + p1) + (p2 + p3);
+        lvs += (p0 * vl4.x + p1 * vl4.y) + (p2 * vl4.z + p3 * vl4.w);
+        const h2 w01 = {(_Float16)(p0 * vs4.x), (_Float16)(p1 * vs4.y)};
+        const h2 w23 = {(_Float16)(p2 * vs4.z), (_Float16)(p3 * vs4.w)};
+        bpv[2 * u] = hbits(w01);
+        bpv[2 * u + 1] = hbits(w23);
+      }
+      // ---- PV: per head hh, plane i. Lane (g, jj = n): bytes jj of tokens 32 c + {4 g + (0..3), 16 + 4 g + (0..3)}
+      const uint8_t* vbc = W.vb[cb];
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        const bool mine = (hn == hh);
+        const h8 B = mine ? pack8(bpv[0], bpv[1], bpv[2], bpv[3]) : pack8(0u, 0u, 0u, 0u);
+        uint32_t D[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int ta = 16 * (v >> 1) + 4 * g + 2 * (v & 1);
+          D[v] = (uint32_t)vbc[ta * 64 + hh * 16 + n] | ((uint32_t)vbc[(ta + 1) * 64 + hh * 16 + n] << 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t msk = (1u << i) | (1u << (16 + i));
+          const h8 A = pack8(D[0] & msk, D[1] & msk, D[2] & msk, D[3] & msk);
+          acc[i] = mfma16(A, B, acc[i]);
+        }
+      }
+    }
+  }
+
+  // ---- combine the 4 waves of the split
+  lsum += __shfl_xor(lsum, 16); lsum += __shfl_xor(lsum, 32);
+  lvs += __shfl_xor(lvs, 16);   lvs += __shfl_xor(lvs, 32);
+  __syncthreads();
+  QFinLds& F = *reinterpret_cast<QFinLds*>(lds_raw);
+  if (g == 0) { F.m[w][n] = m; F.l[w][n] = lsum; F.lv[w][n] = lvs; }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) F.acc[w][n][16 * i + 4 * g + r] = acc[i][r];
+  __syncthreads();
+  // thread -> (row rr = tid / 16, dims 8 (tid % 16) .. + 7)
+  const int rr = tid >> 4, d0 = 8 * (tid & 15);
+  float M = NEG_BIG;
+#pragma unroll
+  for (int ww = 0; ww < QWAVES; ++ww) M = fmaxf(M, F.m[ww][rr]);
+  float Ls = 0.f, LV = 0.f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int ww = 0; ww < QWAVES; ++ww) {
+    const float sc = exp2f(F.m[ww][rr] - M);
+    Ls += sc * F.l[ww][rr]; LV += sc * F.lv[ww][rr];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += sc * F.acc[ww][rr][d0 + e];
+  }
+  const int64_t row = ((int64_t)b * (ns + 1) + s) * 16 + rr;
+  if ((tid & 15) == 0) { mo[row] = M; lo_out[row] = Ls; }
+  const float pscale = __uint_as_float((uint32_t)(127 + 24 - (d0 >> 4)) << 23);   // 2^(24 - i), plane i = d / 16
+  float4 r0, r1;
+  r0.x = o[0] * pscale + LV; r0.y = o[1] * pscale + LV; r0.z = o[2] * pscale + LV; r0.w = o[3] * pscale + LV;
+  r1.x = o[4] * pscale + LV; r1.y = o[5] * pscale + LV; r1.z = o[6] * pscale + LV; r1.w = o[7] * pscale + LV;
+  *reinterpret_cast<float4*>(ao + row * 128 + d0) = r0;
+  *reinterpret_cast<float4*>(ao + row * 128 + d0 + 4) = r1;
+}
+
+// ---------------------------------------------------------------- exact tail + sinks (SIMT)
+struct XLds {
+  float4 q[128];                       // q rows r = 0..3 of this head at dim d
+  float m[4][4], l[4][4];              // per wave, per row
+  float acc[4][4][128];                // per wave, row, dim
+};
+
+__global__ void __launch_bounds__(256)
+decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
+                    const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
+                    float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
+                    int nsink) {
+  __shared__ XLds X;
+  const int b = blockIdx.x >> 2, h = blockIdx.x & 3;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  if (tid < 128) {
+    float4 a;
+    a.x = bf2f(q[((int64_t)b * 16 + h * 4 + 0) * 128 + tid]);
+    a.y = bf2f(q[((int64_t)b * 16 + h * 4 + 1) * 128 + tid]);
+    a.z = bf2f(q[((int64_t)b * 16 + h * 4 + 2) * 128 + tid]);
+    a.w = bf2f(q[((int64_t)b * 16 + h * 4 + 3) * 128 + tid]);
+    X.q[tid] = a;
+  }
+  __syncthreads();
+  const int n = P.N[b];
+  int lo_e = P.NQ[b] * BLK;
+  if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
+  lo_e = max(lo_e, 0);
+  const int cnt = (nsink > 0) ? max(0, min(min(nsink, lo_e), n)) : 0;
+  const int T = cnt + max(0, n - lo_e);
+  const int64_t* et = P.eoff + (int64_t)b * P.eoff_stride;
+
+  // element offset of token i's K row (sink or exact page) and of its V row; -1 if out of range
+  auto rows = [&](int i, int64_t& ko, int64_t& vo, int& pos) {
+    if (i < cnt) {
+      pos = i;
+      ko = P.skoff[b] + ((int64_t)i * 4 + h) * 128;
+      vo = P.svoff[b] + ((int64_t)i * 4 + h) * 128;
+      if (ko < 0 || vo < 0 || ko + 128 > sink_elems || vo + 128 > sink_elems) { ko = vo = -1; }
+    } else {
+      pos = lo_e + (i - cnt);
+      const int64_t pg = pos / P.ebs;
+      if (pg >= P.eoff_stride) { ko = vo = -1; return; }
+      ko = et[pg] + h * P.e_hs + (pos % P.ebs) * P.e_ts;
+      vo = ko + P.e_v;
+      if (ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) { ko = vo = -1; }
+    }
+  };
+
+  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0}, acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  for (int c0 = 64 * w; c0 < T; c0 += 256) {
+    asm volatile("" ::: "memory");   // keep the q reads below inside the loop (no 512-register hoist)
+    const int i = c0 + lane;
+    int64_t ko = -1, vo = -1;
+    int pos = 0;
+    if (i < T) rows(i, ko, vo, pos);
+    const bool valid = (i < T) && ko >= 0 && pos < rope_rows;
+    const uint16_t* Kb = (i < cnt) ? P.sk : P.epool;
+    float sc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+      const uint16_t* kr = Kb + ko;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const uint4 w0 = *reinterpret_cast<const uint4*>(kr + 8 * gq);
+        const uint4 w1 = *reinterpret_cast<const uint4*>(kr + 32 + 8 * gq);
+        const uint4 w2 = *reinterpret_cast<const uint4*>(kr + 64 + 8 * gq);
+        const uint4 w3 = *reinterpret_cast<const uint4*>(kr + 96 + 8 * gq);
+        const uint4 c4 = *reinterpret_cast<const uint4*>(cos_t + (int64_t)pos * 32 + 8 * gq);
+        const uint4 s4 = *reinterpret_cast<const uint4*>(sin_t + (int64_t)pos * 32 + 8 * gq);
+        const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
+        const uint32_t a2[4] = {w2.x, w2.y, w2.z, w2.w}, a3[4] = {w3.x, w3.y, w3.z, w3.w};
+        const uint32_t cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          asm volatile("" ::: "memory");
+          const int j = 8 * gq + e;
+          const uint32_t sh = 16 * (e & 1);
+          const float k0 = bf2f((a0[e >> 1] >> sh) & 0xFFFFu), k1 = bf2f((a1[e >> 1] >> sh) & 0xFFFFu);
+          const float k2 = bf2f((a2[e >> 1] >> sh) & 0xFFFFu), k3 = bf2f((a3[e >> 1] >> sh) & 0xFFFFu);
+          const float cs = bf2f((cc[e >> 1] >> sh) & 0xFFFFu), sn = bf2f((ss[e >> 1] >> sh) & 0xFFFFu);
+          const float kr0 = bfround(__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)));
+          const float kr2 = bfround(__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn)));
+          const float4 qa = X.q[j], qb = X.q[32 + j], qc = X.q[64 + j], qd = X.q[96 + j];
+          sc[0] += qa.x * kr0 + qb.x * k1 + qc.x * kr2 + qd.x * k3;
+          sc[1] += qa.y * kr0 + qb.y * k1 + qc.y * kr2 + qd.y * k3;
+          sc[2] += qa.z * kr0 + qb.z * k1 + qc.z * kr2 + qd.z * k3;
+          sc[3] += qa.w * kr0 + qb.w * k1 + qc.w * kr2 + qd.w * k3;
+        }
+      }
+    }
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = valid ? sc[r] * scale : -INFINITY;
+      float cm = x;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+      const float mn = fmaxf(m[r], cm);
+      const float al = exp2f(m[r] - mn);
+      m[r] = mn;
+      p[r] = valid ? exp2f(x - mn) : 0.f;
+      lsum[r] = lsum[r] * al + p[r];
+      acc[r][0] *= al; acc[r][1] *= al;
+    }
+    // PV: lane owns dims 2 lane, 2 lane + 1; walk the chunk's tokens
+    const int cntc = min(64, T - c0);
+    for (int tt = 0; tt < cntc; ++tt) {
+      const float p0 = __shfl(p[0], tt), p1 = __shfl(p[1], tt), p2 = __shfl(p[2], tt), p3 = __shfl(p[3], tt);
+      const int64_t vrow = __shfl(vo, tt);
+      if (vrow < 0) continue;   // uniform: masked token
+      const uint16_t* Vb = (c0 + tt < cnt) ? P.sv : P.epool;
+      const uint32_t vv = *reinterpret_cast<const uint32_t*>(Vb + vrow + 2 * lane);
+      const float v0 = bf2f_lo(vv), v1 = bf2f_hi(vv);
+      acc[0][0] += p0 * v0; acc[0][1] += p0 * v1;
+      acc[1][0] += p1 * v0; acc[1][1] += p1 * v1;
+      acc[2][0] += p2 * v0; acc[2][1] += p2 * v1;
+      acc[3][0] += p3 * v0; acc[3][1] += p3 * v1;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float l = lsum[r];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) { X.m[w][r] = m[r]; X.l[w][r] = l; }
+    X.acc[w][r][2 * lane] = acc[r][0];
+    X.acc[w][r][2 * lane + 1] = acc[r][1];
+  }
+  __syncthreads();
+  // thread -> (row r = tid / 64, dims 2 (tid % 64), +1)
+  const int r = tid >> 6, dd = 2 * (tid & 63);
+  float M = NEG_BIG;
+#pragma unroll
+  for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, X.m[ww][r]);
+  float Ls = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < 4; ++ww) {
+    const float sc = exp2f(X.m[ww][r] - M);
+    Ls += sc * X.l[ww][r];
+    o0 += sc * X.acc[ww][r][dd];
+    o1 += sc * X.acc[ww][r][dd + 1];
+  }
+  const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
+  if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
+  ao[row * 128 + dd] = o0;
+  ao[row * 128 + dd + 1] = o1;
+}
+
+// ---------------------------------------------------------------- split merge
+__global__ void __launch_bounds__(256)
+decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
+                    uint16_t* __restrict__ out) {
+  const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
+  const int S = ns + 1;
+  float M = NEG_BIG;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, mo[((int64_t)b * S + s) * 16 + r]);
+  float Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, xe[8];
+  for (int s = 0; s < S; ++s) {
+    const int64_t row = ((int64_t)b * S + s) * 16 + r;
+    const float wgt = exp2f(mo[row] - M);
+    Ls += wgt * lo[row];
+    const float4 a0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
+    const float4 a1 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
+    const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    if (s < ns) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
+    }
+  }
+  if (ns > 0) {   // y = H x, d = 8 l16 + e: three in-lane stages, four across the 16-lane group
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (!(e & (1 << k))) {
+          const float a = xq[e], c = xq[e | (1 << k)];
+          xq[e] = a + c; xq[e | (1 << k)] = a - c;
+        }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int msk = 1 << k;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pv = __shfl_xor(xq[e], msk);
+        xq[e] = (l16 & msk) ? pv - xq[e] : xq[e] + pv;
+      }
+    }
+  }
+  const float hn = __uint_as_float(0x3DB504F3u);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float y0 = (ns > 0 ? xq[e] * hn : 0.f) + xe[e];
+    float y1 = (ns > 0 ? xq[e + 1] * hn : 0.f) + xe[e + 1];
+    y0 = Ls > 0.f ? y0 / Ls : 0.f;
+    y1 = Ls > 0.f ? y1 / Ls : 0.f;
+    o[e >> 1] = f2bf(y0) | (f2bf(y1) << 16);
+  }
+  *reinterpret_cast<uint4*>(out + ((int64_t)b * 16 + r) * 128 + 8 * l16) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+}  // namespace
+}  // namespace kv800
+
+using namespace kv800;
+
+extern "C" {
+
+int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs16, void* stream) {
+  KV800_REQUIRE(P >= 0, "rope_table: P < 0");
+  if (P == 0) return KV800_OK;
+  KV800_REQUIRE(cos_t && sin_t && cs16, "rope_table: null pointer");
+  const int64_t n = P * 32;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, cos_t,
+                     sin_t, n, cs16);
+  return check_launch("rope_table");
+}
+
+int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb) {
+  KV800_REQUIRE(B >= 0 && nqmax >= 0 && ns && spb, "plan: bad arguments");
+  if (nqmax == 0 || B == 0) { *ns = 0; *spb = 1; return KV800_OK; }
+  // ~512 workgroups (2 per CU), each wave owning whole sub-blocks
+  const int64_t want = (512 + B - 1) / B;
+  const int64_t cap = (nqmax + QWAVES - 1) / QWAVES;
+  int64_t n_s = want < cap ? want : cap;
+  if (n_s < 1) n_s = 1;
+  const int64_t sp = (nqmax + n_s - 1) / n_s;
+  *spb = sp;
+  *ns = (nqmax + sp - 1) / sp;
+  return KV800_OK;
+}
+
+int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
+                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows,
+                                 float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
+                                 void* stream) {
+  KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
+  if (B == 0 || ns == 0) return KV800_OK;
+  KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
+  KV800_REQUIRE(B * ns <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
+  KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
+                "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
+  hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(B * ns)), dim3(256), 0, (hipStream_t)stream, q, qpool,
+                     qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale);
+  return check_launch("decode_quant");
+}
+
+int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
+                           const int32_t* nq, const uint32_t* cs16, float* mo, float* lo, float* ao, int64_t B,
+                           int64_t ns, int64_t spb, float scale, void* stream) {
+  return kv800_hip_decode_quant_sized(q, qpool, INT64_MAX / 2, boff, boff_stride, nq, cs16, INT64_MAX / 2, mo, lo, ao,
+                                      B, ns, spb, scale, stream);
+}
+
+int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t,
+                                 const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
+                                 float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream) {
+  KV800_REQUIRE(P && B >= 0 && ns >= 0, "decode_exact: bad arguments");
+  if (B == 0) return KV800_OK;
+  KV800_REQUIRE(q && cos_t && sin_t && mo && lo && ao && P->epool && P->eoff && P->N && P->NQ,
+                "decode_exact: null pointer");
+  KV800_REQUIRE(P->ebs > 0 && P->win >= 0, "decode_exact: ebs must be > 0");
+  KV800_REQUIRE(P->e_hs % 8 == 0 && P->e_ts % 8 == 0 && ((uintptr_t)P->epool % 16) == 0,
+                "decode_exact: exact strides must be multiples of 8 elements and the pool 16-byte aligned");
+  const int nsink = P->sk ? NSINK : 0;
+  KV800_REQUIRE(!nsink || (P->sv && P->skoff && P->svoff), "decode_exact: sinks need sv, skoff and svoff");
+  KV800_REQUIRE(B * 4 <= 0x7FFFFFFF, "decode_exact: grid too large");
+  hipLaunchKernelGGL(decode_exact_kernel, dim3((unsigned)(B * 4)), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
+                     sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink);
+  return check_launch("decode_exact");
+}
+
+int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                           float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream) {
+  return kv800_hip_decode_exact_sized(P, q, cos_t, sin_t, INT64_MAX / 2, INT64_MAX / 2, INT64_MAX / 2, mo, lo, ao, B, ns,
+                                      scale, stream);
+}
+
+int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, int64_t B, int64_t ns, uint16_t* out,
+                           void* stream) {
+  KV800_REQUIRE(B >= 0 && ns >= 0, "decode_merge: bad arguments");
+  if (B == 0) return KV800_OK;
+  KV800_REQUIRE(mo && lo && ao && out, "decode_merge: null pointer");
+  KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, out);
+  return check_launch("decode_merge");
+}
+
+int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows) {
+  const int64_t S = ns + 1;
+  return align256(B * S * 16 * 4) * 2 + align256(B * S * 16 * 128 * 4) + align256(rope_rows * 32 * 4);
+}
+
+int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs16, int64_t qpool_bytes,
+                           int64_t epool_elems, int64_t sink_elems, uint16_t* out, void* workspace,
+                           int64_t workspace_bytes, int64_t spb, void* stream) {
+  KV800_REQUIRE(P && B >= 0, "decode: bad arguments");
+  if (B == 0) return KV800_OK;
+  KV800_REQUIRE(q && out && workspace && cos_t && sin_t, "decode: null pointer");
+  const int64_t nqmax = P->win ? 0 : P->nqmax;
+  KV800_REQUIRE(nqmax >= 0, "decode: nqmax < 0");
+  KV800_REQUIRE(!nqmax || (P->qpool && P->boff && nqmax <= P->boff_stride), "decode: nqmax exceeds the boff table");
+  int64_t ns = 0, sp = 1;
+  if (nqmax) {
+    if (spb > 0) { sp = spb; ns = (nqmax + sp - 1) / sp; }
+    else if (kv800_hip_plan(B, nqmax, &ns, &sp) != KV800_OK) return KV800_EINVAL;
+  }
+  const int64_t rows = nqmax * BLK;
+  KV800_REQUIRE(rows <= rope_rows, "decode: rope tables hold %lld rows, the quantized part needs %lld",
+                (long long)rope_rows, (long long)rows);
+  const int64_t need = kv800_hip_decode_workspace(B, ns, cs16 ? 0 : rows);
+  KV800_REQUIRE(workspace_bytes >= need, "decode: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  KV800_REQUIRE(((uintptr_t)workspace % 256) == 0, "decode: workspace must be 256-byte aligned");
+  const int64_t S = ns + 1;
+  char* ws = (char*)workspace;
+  float* mo = (float*)ws;
+  float* lo = (float*)(ws + align256(B * S * 16 * 4));
+  float* ao = (float*)(ws + 2 * align256(B * S * 16 * 4));
+  uint32_t* cst = (uint32_t*)(ws + 2 * align256(B * S * 16 * 4) + align256(B * S * 16 * 128 * 4));
+  const float scale = (float)(1.4426950408889634 / sqrt(128.0));
+  int rc;
+  if (ns) {
+    if (!cs16) {
+      if ((rc = kv800_hip_rope_table(cos_t, sin_t, rows, cst, stream)) != KV800_OK) return rc;
+      cs16 = cst;
+    }
+    if ((rc = kv800_hip_decode_quant_sized(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo,
+                                           ao, B, ns, sp, scale, stream)) != KV800_OK)
+      return rc;
+  }
+  if ((rc = kv800_hip_decode_exact_sized(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns,
+                                         scale, stream)) != KV800_OK)
+    return rc;
+  return kv800_hip_decode_merge(mo, lo, ao, B, ns, out, stream);
+}
+
+int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                     const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
+                     int64_t workspace_bytes, int64_t spb, void* stream) {
+  const int64_t rows = P ? (P->win ? 0 : P->nqmax) * BLK : 0;
+  return kv800_hip_decode_sized(P, q, B, cos_t, sin_t, rows > 0 ? rows : INT64_MAX / 2, cs16, INT64_MAX / 2,
+                                INT64_MAX / 2, INT64_MAX / 2, out, workspace, workspace_bytes, spb, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,389 @@
+// kv800_quant.hip -- 800h quantize / paged flush / dequantize kernels for gfx950 and their C-ABI entry points.
+//
+// Reference semantics: kv800.py:56-76 (quantize_blocks), kv800.py:79-92 (dequantize_blocks), the flush plan of
+// vllm_attn.py:297-317 and the PagedStore flush loop kv800.py:433-440. Output bytes are bit-identical to the
+// reference quantizer on CPU torch:
+//   * K: per (head, channel) min / max over the 256 tokens; lo8 = fp8(lo), sc8 = fp8(max((hi - lo) / 3, 1e-8));
+//     code = clamp(rne((x - f32(lo8)) / max(f32(sc8), 1e-8)), 0, 3) with IEEE division;
+//   * V: y = f32(v) @ H per (token, head) as the sequential fma chain over k = 0..127 that torch-CPU's sgemm
+//     evaluates for this shape, then per (token, 2-head group) lo8 / sc8 and 1-bit codes the same way.
+// One workgroup (8 waves) quantizes one 256-token sub-block of all 4 KV heads; the input is gathered straight from
+// the exact pages (paged flush) or from dense (M, 256, 4, 128) tensors, and the 51,200-byte result is written
+// through the quant block table, so a flush is one launch with no host loop and no intermediate copies.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "kv800_common.h"
+#include "../../include/kv800_hip.h"
+
+namespace kv800 {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return KV800_EHIP;
+  }
+  return KV800_OK;
+}
+
+namespace {
+
+constexpr int QTHREADS = 512;    // 8 waves per sub-block, 32 tokens each
+constexpr int QW = QTHREADS / 64, TPW = BLK / QW;
+
+// ---------------------------------------------------------------- token-row sources
+struct DenseSrc {   // (M, 256, 4, 128) contiguous K and V
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t m;
+  __device__ const uint16_t* krow(int t, int h) const { return k + ((m * BLK + t) * 4 + h) * 128; }
+  __device__ const uint16_t* vrow(int t, int h) const { return v + ((m * BLK + t) * 4 + h) * 128; }
+};
+
+struct PagedSrc {   // exact pages: K of (position p, head h) at eoff[r, p / ebs] + h e_hs + (p % ebs) e_ts; V at + e_v
+  const uint16_t* ep;
+  const int64_t* et;   // this row's page table
+  int64_t ebs, e_hs, e_ts, e_v, p0;
+  __device__ const uint16_t* krow(int t, int h) const {
+    const int64_t p = p0 + t;
+    return ep + et[p / ebs] + h * e_hs + (p % ebs) * e_ts;
+  }
+  __device__ const uint16_t* vrow(int t, int h) const { return krow(t, h) + e_v; }
+};
+
+// Per-lane column of the normalized Sylvester Hadamard for k < 64: H[k][lane] (H[k][lane + 64] is the same for
+// k < 64 and its negation for k >= 64; H[k][d] = H[k - 64][d] for d < 64).
+__device__ __forceinline__ void hadamard_column(float (&hc)[64], int lane) {
+  const float c = __uint_as_float(0x3DB504F3u);   // fp32(1 / sqrt(128)), the entries of kv800.hadamard
+#pragma unroll
+  for (int k = 0; k < 64; ++k) hc[k] = (__builtin_popcount(k & lane) & 1) ? -c : c;
+}
+
+// y[d] = sum_k x[k] H[k][d], the sequential fma chain of torch-CPU, for d = lane (ya) and d = lane + 64 (yb).
+// x is read from LDS (uniform across the wave). The first 64 steps are shared by both outputs.
+__device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)[64], float& ya, float& yb) {
+  float a = 0.f;
+#pragma unroll
+  for (int k = 0; k < 64; k += 4) {
+    if ((k & 15) == 0) __builtin_amdgcn_sched_barrier(0);   // bound the LDS loads in flight
+    const float4 v4 = *reinterpret_cast<const float4*>(x + k);
+    a = __builtin_fmaf(v4.x, hc[k], a);
+    a = __builtin_fmaf(v4.y, hc[k + 1], a);
+    a = __builtin_fmaf(v4.z, hc[k + 2], a);
+    a = __builtin_fmaf(v4.w, hc[k + 3], a);
+  }
+  float b = a;
+#pragma unroll
+  for (int k = 64; k < 128; k += 4) {
+    if ((k & 15) == 0) __builtin_amdgcn_sched_barrier(0);
+    const float4 v4 = *reinterpret_cast<const float4*>(x + k);
+    a = __builtin_fmaf(v4.x, hc[k - 64], a);     b = __builtin_fmaf(v4.x, -hc[k - 64], b);
+    a = __builtin_fmaf(v4.y, hc[k - 63], a);     b = __builtin_fmaf(v4.y, -hc[k - 63], b);
+    a = __builtin_fmaf(v4.z, hc[k - 62], a);     b = __builtin_fmaf(v4.z, -hc[k - 62], b);
+    a = __builtin_fmaf(v4.w, hc[k - 61], a);     b = __builtin_fmaf(v4.w, -hc[k - 61], b);
+  }
+  ya = a;
+  yb = b;
+}
+
+typedef const __attribute__((address_space(4))) uint32_t* cu32p;   // read-only scalar-cache view
+
+// Same chain with x = a bf16 row in global memory at a wave-uniform address: the row is read with scalar loads
+// and converted on the scalar unit, so the x operand of every fma is an SGPR and no VGPRs hold the row.
+__device__ __forceinline__ void hadamard_chain_row(const uint16_t* row, const float (&hc)[64], float& ya, float& yb) {
+  const uint64_t ad = (uint64_t)(uintptr_t)row;
+  const uint32_t lo32 = __builtin_amdgcn_readfirstlane((uint32_t)ad), hi32 = __builtin_amdgcn_readfirstlane((uint32_t)(ad >> 32));
+  const cu32p r = (cu32p)(uintptr_t)(((uint64_t)hi32 << 32) | lo32);
+  float a = 0.f;
+#pragma unroll
+  for (int k = 0; k < 64; k += 2) {
+    if ((k & 31) == 0) __builtin_amdgcn_sched_barrier(0);   // at most a quarter row in SGPRs
+    const uint32_t wd = r[k >> 1];
+    a = __builtin_fmaf(__uint_as_float(wd << 16), hc[k], a);
+    a = __builtin_fmaf(__uint_as_float(wd & 0xFFFF0000u), hc[k + 1], a);
+  }
+  float b = a;
+#pragma unroll
+  for (int k = 64; k < 128; k += 2) {
+    if ((k & 31) == 0) __builtin_amdgcn_sched_barrier(0);
+    const uint32_t wd = r[k >> 1];
+    const float x0 = __uint_as_float(wd << 16), x1 = __uint_as_float(wd & 0xFFFF0000u);
+    a = __builtin_fmaf(x0, hc[k - 64], a);     b = __builtin_fmaf(x0, -hc[k - 64], b);
+    a = __builtin_fmaf(x1, hc[k - 63], a);     b = __builtin_fmaf(x1, -hc[k - 63], b);
+  }
+  ya = a;
+  yb = b;
+}
+
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// bits jj, jj + 16, jj + 32, jj + 48 of m gathered into bits 0..3
+__device__ __forceinline__ uint32_t gather4(uint64_t m, int jj) {
+  const uint64_t x = (m >> jj) & 0x0001000100010001ull;
+  return (uint32_t)((x | (x >> 15) | (x >> 30) | (x >> 45)) & 0xFull);
+}
+
+constexpr int LDS_BYTES = 2 * 8 * 512 * 4 + 2 * 512 * 4;   // K-path min/max partials + lo / den; V path reuses it
+
+template <typename Src>
+__device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* lds) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  float* red_min = reinterpret_cast<float*>(lds);               // [QW][512]
+  float* red_max = red_min + QW * 512;                          // [QW][512]
+  float* col_lo = red_max + 16 * 512;                           // [512]
+  float* col_den = col_lo + 512;                                // [512]
+
+  // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16)
+  const int h = lane >> 4, c0 = 8 * (lane & 15);
+  uint4 kx[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + tt, h) + c0);
+  float mn[8], mx[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { mn[e] = INFINITY; mx[e] = -INFINITY; }
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+      mn[e] = fminf(mn[e], x);
+      mx[e] = fmaxf(mx[e], x);
+    }
+  }
+  const int hc0 = h * 128 + c0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { red_min[w * 512 + hc0 + e] = mn[e]; red_max[w * 512 + hc0 + e] = mx[e]; }
+  // the code pass re-derives the floats from the packed bf16 registers instead of keeping 128 converted values live
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) asm volatile("" : "+v"(kx[tt].x), "+v"(kx[tt].y), "+v"(kx[tt].z), "+v"(kx[tt].w));
+  __syncthreads();
+  if (tid < 512) {
+    float lo = red_min[tid], hi = red_max[tid];
+#pragma unroll
+    for (int ww = 1; ww < QW; ++ww) { lo = fminf(lo, red_min[ww * 512 + tid]); hi = fmaxf(hi, red_max[ww * 512 + tid]); }
+    const uint32_t lo8 = f8e(lo);
+    const uint32_t sc8 = f8e(clamp_min_1e8(__fdiv_rn(__fsub_rn(hi, lo), 3.0f)));
+    out[KLO_O + tid] = (uint8_t)lo8;
+    out[KSC_O + tid] = (uint8_t)sc8;
+    col_lo[tid] = f8d(lo8);
+    col_den[tid] = clamp_min_1e8(f8d(sc8));
+  }
+  __syncthreads();
+  {
+    float lof[8], den[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { lof[e] = col_lo[hc0 + e]; den[e] = col_den[hc0 + e]; }
+    const int p = (lane & 15) >> 2, q = lane & 3;   // plane of these 8 channels, byte quarter 8q .. 8q + 7
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      __builtin_amdgcn_sched_barrier(0);   // one token row at a time: keeps the division temporaries bounded
+      const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
+      uint32_t d0 = 0, d1 = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+        float c = __builtin_rintf(__fdiv_rn(__fsub_rn(x, lof[e]), den[e]));
+        c = fminf(fmaxf(c, 0.f), 3.f);
+        const uint32_t code = (uint32_t)c << (2 * p);
+        if (e < 4) d0 |= code << (8 * e); else d1 |= code << (8 * (e - 4));
+      }
+      d0 |= __shfl_xor(d0, 4); d1 |= __shfl_xor(d1, 4);
+      d0 |= __shfl_xor(d0, 8); d1 |= __shfl_xor(d1, 8);
+      if (p == 0) {
+        const int t = TPW * w + tt;
+        *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + h) * 32 + 8 * q) = make_uint2(d0, d1);
+      }
+    }
+  }
+  __syncthreads();   // the K scratch is reused below
+
+  // ---------------- V: wave w = tokens 32w .. 32w + 31; per token the 4 head rows, lane = dims lane, lane + 64
+  float hcol[64];
+  hadamard_column(hcol, lane);
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int t = TPW * w + tt;
+    float ya[4], yb[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_barrier(0);
+      hadamard_chain_row(src.vrow(t, r), hcol, ya[r], yb[r]);
+    }
+    uint64_t ma[4], mb[4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const float lo = wave_min(fminf(fminf(ya[2 * g], yb[2 * g]), fminf(ya[2 * g + 1], yb[2 * g + 1])));
+      const float hi = wave_max(fmaxf(fmaxf(ya[2 * g], yb[2 * g]), fmaxf(ya[2 * g + 1], yb[2 * g + 1])));
+      const uint32_t lo8 = f8e(lo);
+      const uint32_t sc8 = f8e(clamp_min_1e8(__fsub_rn(hi, lo)));
+      const float lof = f8d(lo8), den = clamp_min_1e8(f8d(sc8));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 2 * g + u;
+        const float ba = __builtin_rintf(__fdiv_rn(__fsub_rn(ya[r], lof), den));
+        const float bb = __builtin_rintf(__fdiv_rn(__fsub_rn(yb[r], lof), den));
+        ma[r] = __ballot(ba >= 1.f);
+        mb[r] = __ballot(bb >= 1.f);
+      }
+      if (lane == 0) { out[VLO_O + t * 2 + g] = (uint8_t)lo8; out[VSC_O + t * 2 + g] = (uint8_t)sc8; }
+    }
+    {
+      const int hh = lane >> 4, jj = lane & 15;
+      const uint64_t a = hh == 0 ? ma[0] : hh == 1 ? ma[1] : hh == 2 ? ma[2] : ma[3];
+      const uint64_t b = hh == 0 ? mb[0] : hh == 1 ? mb[1] : hh == 2 ? mb[2] : mb[3];
+      out[VB_O + t * 64 + lane] = (uint8_t)(gather4(a, jj) | (gather4(b, jj) << 4));
+    }
+  }
+}
+
+__global__ void __launch_bounds__(QTHREADS) quantize_dense_kernel(const uint16_t* __restrict__ k,
+                                                                   const uint16_t* __restrict__ v,
+                                                                   uint8_t* __restrict__ out) {
+  __shared__ __align__(16) char lds[LDS_BYTES];
+  const int64_t m = blockIdx.x;
+  DenseSrc src{k, v, m};
+  quantize_sub(src, out + m * SUB, lds);
+}
+
+__global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restrict__ ep, const int64_t* __restrict__ eoff,
+                                                         int64_t es, int64_t ebs, int64_t e_hs, int64_t e_ts, int64_t e_v,
+                                                         uint8_t* __restrict__ qpool, const int64_t* __restrict__ qbt,
+                                                         int64_t qs, int64_t bsq, int64_t qs0,
+                                                         const int32_t* __restrict__ nq_prev,
+                                                         const int32_t* __restrict__ nq_new, int max_new) {
+  __shared__ __align__(16) char lds[LDS_BYTES];
+  const int64_t r = blockIdx.x / max_new;
+  const int j = nq_prev[r] + (int)(blockIdx.x % max_new);
+  if (j >= nq_new[r]) return;   // uniform over the workgroup
+  const int64_t tok0 = (int64_t)j * BLK;
+  uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
+  PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
+  quantize_sub(src, dst, lds);
+}
+
+// ---------------------------------------------------------------- dequantize (kv800.py:79-92)
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ sb, uint16_t* __restrict__ kout,
+                                                      float* __restrict__ vout) {
+  __shared__ __align__(16) float xbuf[4][2][512];
+  const int64_t m = blockIdx.x;
+  const uint8_t* s = sb + m * SUB;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // K: bf16(code * ksc + klo) (product and sum rounded separately, as the reference's torch ops)
+  for (int i = tid; i < BLK * 512 / 8; i += 256) {
+    const int t = i / 64, hc0 = (i % 64) * 8, hh = hc0 >> 7, d0 = hc0 & 127;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      uint32_t pr = 0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int d = d0 + e + u;
+        const uint32_t code = (s[KC_O + (t * 4 + hh) * 32 + (d & 31)] >> (2 * (d >> 5))) & 3u;
+        const float kv = __fadd_rn(__fmul_rn((float)code, f8d(s[KSC_O + hh * 128 + d])), f8d(s[KLO_O + hh * 128 + d]));
+        pr |= f2bf(kv) << (16 * u);
+      }
+      o[e >> 1] = pr;
+    }
+    *reinterpret_cast<uint4*>(kout + (m * BLK + t) * 512 + hc0) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  // V: (bit * vsc + vlo) @ H, wave w = tokens 64w .. 64w + 63, per token its 4 head rows
+  float hcol[64];
+  hadamard_column(hcol, lane);
+  const int rr = lane >> 4, e0 = 8 * (lane & 15);
+  for (int tt = 0; tt < 64; ++tt) {
+    const int t = 64 * w + tt;
+    float* xb = xbuf[w][tt & 1];
+    {
+      const float vsc = f8d(s[VSC_O + t * 2 + (rr >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (rr >> 1)]);
+      const uint8_t* vb = s + VB_O + (t * 4 + rr) * 16;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = e0 + e;
+        const float bit = (float)((vb[d & 15] >> (d >> 4)) & 1u);
+        xb[rr * 128 + d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float ya, yb;
+      hadamard_chain(xb + r * 128, hcol, ya, yb);
+      float* vo = vout + ((m * BLK + t) * 4 + r) * 128;
+      vo[lane] = ya;
+      vo[lane + 64] = yb;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace kv800
+
+using namespace kv800;
+
+extern "C" {
+
+int kv800_hip_version(void) { return 100; }
+
+const char* kv800_hip_last_error(void) { return g_err; }
+
+int kv800_hip_quantize_blocks(const uint16_t* k, const uint16_t* v, int64_t M, uint8_t* out, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(M >= 0, "quantize_blocks: M = %lld < 0", (long long)M);
+  if (M == 0) return KV800_OK;
+  KV800_REQUIRE(k && v && out, "quantize_blocks: null pointer");
+  KV800_REQUIRE(M <= 0x7FFFFFFF, "quantize_blocks: M = %lld too large", (long long)M);
+  KV800_REQUIRE(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && ((uintptr_t)out % 8) == 0,
+                "quantize_blocks: k / v must be 16-byte aligned and out 8-byte aligned");
+  hipLaunchKernelGGL(quantize_dense_kernel, dim3((unsigned)M), dim3(QTHREADS), 0, (hipStream_t)stream, k, v, out);
+  return check_launch("quantize_blocks");
+}
+
+int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_stride, int64_t ebs, int64_t e_hs,
+                    int64_t e_ts, int64_t e_v, uint8_t* qpool, const int64_t* qbt, int64_t qbt_stride, int64_t bsq,
+                    int64_t qs0, const int32_t* nq_prev, const int32_t* nq_new, int64_t R, int64_t max_new,
+                    void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(R >= 0 && max_new >= 0, "flush: R and max_new must be >= 0");
+  if (R == 0 || max_new == 0) return KV800_OK;
+  KV800_REQUIRE(epool && eoff && qpool && qbt && nq_prev && nq_new, "flush: null pointer");
+  KV800_REQUIRE(ebs > 0 && bsq > 0 && bsq % BLK == 0, "flush: ebs must be > 0 and bsq a positive multiple of 256");
+  KV800_REQUIRE(e_hs % 8 == 0 && e_ts % 8 == 0 && e_v % 8 == 0 && ((uintptr_t)epool % 16) == 0,
+                "flush: exact-pool strides must be multiples of 8 elements and the pool 16-byte aligned");
+  KV800_REQUIRE(R * max_new <= 0x7FFFFFFF && max_new <= 0x7FFFFFFF, "flush: grid too large");
+  hipLaunchKernelGGL(flush_kernel, dim3((unsigned)(R * max_new)), dim3(QTHREADS), 0, (hipStream_t)stream, epool, eoff,
+                     eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq, qs0, nq_prev, nq_new, (int)max_new);
+  return check_launch("flush");
+}
+
+int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, float* v_out, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(M >= 0, "dequantize_blocks: M = %lld < 0", (long long)M);
+  if (M == 0) return KV800_OK;
+  KV800_REQUIRE(sb && k_out && v_out, "dequantize_blocks: null pointer");
+  KV800_REQUIRE(M <= 0x7FFFFFFF, "dequantize_blocks: M too large");
+  KV800_REQUIRE(((uintptr_t)k_out % 16) == 0, "dequantize_blocks: k_out must be 16-byte aligned");
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, sb, k_out, v_out);
+  return check_launch("dequantize_blocks");
+}
+
+}  // extern "C"

@@ -1,0 +1,297 @@
+"""HIP backend of kv800.decode / quantize_blocks / dequantize_blocks / flush for MI355X (gfx950).
+
+Binds the C ABI of _lib/libkv800_hip.so (include/kv800_hip.h) with ctypes: no torch C++ extension, so the library
+is independent of the torch build. Load contract, as the reference's SYCL loader (kv800_sycl.py:68-91): the first
+call to ops() loads the library; any failure (no ROCm torch, no GPU, library missing or not loadable) raises
+ImportError, which kv800 reports as "backend not available". There is no fallback inside this module: every entry
+point either runs the HIP kernels or raises.
+
+Tensors are passed by data_ptr(); launches go on torch's current stream of the tensors' device. Extents of every
+pool (from its data_ptr to the end of its storage) are passed to the bounds-checked entry points."""
+import ctypes
+import math
+import os
+from collections import OrderedDict
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "_lib", "libkv800_hip.so")
+SOURCE = None        # how the library was obtained (for the backend log line)
+_L = None
+_ERR = None
+
+BLK, LAG, NSINK, SUB = 256, 128, 4, 51200
+LOG2E = 1.4426950408889634
+
+
+class Paged(ctypes.Structure):
+    """kv800_paged_t (include/kv800_hip.h)."""
+    _fields_ = [("qpool", ctypes.c_void_p), ("boff", ctypes.c_void_p), ("boff_stride", ctypes.c_int64),
+                ("epool", ctypes.c_void_p), ("eoff", ctypes.c_void_p), ("eoff_stride", ctypes.c_int64),
+                ("ebs", ctypes.c_int64), ("e_hs", ctypes.c_int64), ("e_ts", ctypes.c_int64), ("e_v", ctypes.c_int64),
+                ("sk", ctypes.c_void_p), ("sv", ctypes.c_void_p), ("skoff", ctypes.c_void_p), ("svoff", ctypes.c_void_p),
+                ("N", ctypes.c_void_p), ("NQ", ctypes.c_void_p), ("nqmax", ctypes.c_int64), ("win", ctypes.c_int64)]
+
+
+# exported symbol -> (restype, argtypes); the ABI check in tests compares this list with include/kv800_hip.h
+_VP, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "kv800_hip_version": (_I32, []),
+    "kv800_hip_last_error": (ctypes.c_char_p, []),
+    "kv800_hip_quantize_blocks": (_I32, [_VP, _VP, _I64, _VP, _VP]),
+    "kv800_hip_flush": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _I64, _I64,
+                               _VP]),
+    "kv800_hip_dequantize_blocks": (_I32, [_VP, _I64, _VP, _VP, _VP]),
+    "kv800_hip_rope_table": (_I32, [_VP, _VP, _I64, _VP, _VP]),
+    "kv800_hip_decode_quant": (_I32, [_VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _F32, _VP]),
+    "kv800_hip_decode_exact": (_I32, [ctypes.POINTER(Paged), _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP]),
+    "kv800_hip_decode_merge": (_I32, [_VP, _VP, _VP, _I64, _I64, _VP, _VP]),
+    "kv800_hip_plan": (_I32, [_I64, _I64, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "kv800_hip_decode_workspace": (_I64, [_I64, _I64, _I64]),
+    "kv800_hip_decode": (_I32, [ctypes.POINTER(Paged), _VP, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _VP]),
+    "kv800_hip_decode_quant_sized": (_I32, [_VP, _VP, _I64, _VP, _I64, _VP, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64,
+                                            _F32, _VP]),
+    "kv800_hip_decode_exact_sized": (_I32, [ctypes.POINTER(Paged), _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _I64,
+                                            _I64, _F32, _VP]),
+    "kv800_hip_decode_sized": (_I32, [ctypes.POINTER(Paged), _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP,
+                                      _I64, _I64, _VP]),
+}
+
+
+def load_library(path=LIB):
+    """ctypes handle of the library with every signature set (no GPU needed; used by the ABI tests too)."""
+    if not os.path.isfile(path):
+        raise ImportError(f"{path} is not built (run __graft_entry__.build() or python lfm3-kv800_amd/build.py)")
+    try:
+        L = ctypes.CDLL(path)
+    except OSError as e:
+        raise ImportError(f"loading {path} failed: {e}") from e
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+    return L
+
+
+def ops():
+    """The loaded library; raises ImportError when the HIP backend cannot run in this process."""
+    global _L, _ERR, SOURCE
+    if _L is not None:
+        return _L
+    if _ERR is not None:
+        raise ImportError(_ERR)
+    if getattr(torch.version, "hip", None) is None:
+        _ERR = "this torch is not a ROCm build"
+        raise ImportError(_ERR)
+    if not torch.cuda.is_available():
+        _ERR = "torch sees no ROCm GPU"
+        raise ImportError(_ERR)
+    try:
+        _L = load_library()
+    except ImportError as e:
+        _ERR = str(e)
+        raise
+    SOURCE = f"{LIB} (ABI {_L.kv800_hip_version()})"
+    return _L
+
+
+def _check(rc):
+    if rc != 0:
+        raise RuntimeError(f"kv800 HIP: {ops().kv800_hip_last_error().decode(errors='replace')} (status {rc})")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _extent(t):
+    """Elements from t's first element to the end of its storage (what the kernels may address from data_ptr)."""
+    return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
+def _need(t, name, dtype, dev):
+    if t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+# ---------------------------------------------------------------- codec
+def quantize_blocks(k, v):
+    """(M, 256, 4, 128) bf16 K (pre-RoPE) and V -> (M, 51200) uint8, bit-identical to kv800.py:56-76 on CPU torch."""
+    L = ops()
+    dev = k.device
+    _need(k, "k", torch.bfloat16, dev); _need(v, "v", torch.bfloat16, dev)
+    if k.shape != v.shape or k.dim() != 4 or tuple(k.shape[1:]) != (BLK, 4, 128):
+        raise ValueError(f"k, v must be (M, 256, 4, 128), got {tuple(k.shape)} / {tuple(v.shape)}")
+    k, v = k.contiguous(), v.contiguous()
+    out = torch.empty(k.shape[0], SUB, dtype=torch.uint8, device=dev)
+    _check(L.kv800_hip_quantize_blocks(_ptr(k), _ptr(v), k.shape[0], _ptr(out), _stream(dev)))
+    return out
+
+
+def dequantize_blocks(sb):
+    """(M, 51200) uint8 -> K (M, 256, 4, 128) bf16, V (M, 256, 4, 128) fp32 (kv800.py:79-92)."""
+    L = ops()
+    dev = sb.device
+    _need(sb, "sb", torch.uint8, dev)
+    if sb.dim() != 2 or sb.shape[1] != SUB:
+        raise ValueError(f"sb must be (M, 51200), got {tuple(sb.shape)}")
+    sb = sb.contiguous()
+    M = sb.shape[0]
+    k = torch.empty(M, BLK, 4, 128, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(M, BLK, 4, 128, dtype=torch.float32, device=dev)
+    _check(L.kv800_hip_dequantize_blocks(_ptr(sb), M, _ptr(k), _ptr(v), _stream(dev)))
+    return k, v
+
+
+def flush(epool, eoff, ebs, e_hs, e_ts, e_v, qpool, qbt, bsq, qs0, nq_prev, nq_new, max_new):
+    """Quantize sub-blocks j in [nq_prev[r], nq_new[r]) of every row r from the exact pages into the quant pool
+    (one launch; see kv800_hip_flush). epool bf16 (any shape, element offsets), eoff (R, pages) int64 element
+    offsets, qpool uint8 (byte offsets), qbt (R, >= 1) int64 quant block table, nq_prev / nq_new (R,) int32."""
+    L = ops()
+    dev = epool.device
+    _need(epool, "epool", torch.bfloat16, dev); _need(qpool, "qpool", torch.uint8, dev)
+    _need(eoff, "eoff", torch.int64, dev); _need(qbt, "qbt", torch.int64, dev)
+    _need(nq_prev, "nq_prev", torch.int32, dev); _need(nq_new, "nq_new", torch.int32, dev)
+    if eoff.stride(-1) != 1 or qbt.stride(-1) != 1:
+        raise ValueError("eoff and qbt rows must be contiguous")
+    R = nq_prev.shape[0]
+    nq_prev, nq_new = nq_prev.contiguous(), nq_new.contiguous()
+    _check(L.kv800_hip_flush(_ptr(epool), _ptr(eoff), eoff.stride(0), int(ebs), int(e_hs), int(e_ts), int(e_v),
+                             _ptr(qpool), _ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(nq_prev), _ptr(nq_new),
+                             R, int(max_new), _stream(dev)))
+
+
+def combine(MO, LO, AO, ns):
+    """LSE merge of (B, ns+1, 16[, 128]) partials -> (B, 16, 128) bf16 (kv800.py:231-236)."""
+    L = ops()
+    dev = MO.device
+    for t, nm in ((MO, "MO"), (LO, "LO"), (AO, "AO")):
+        _need(t, nm, torch.float32, dev)
+    MO, LO, AO = MO.contiguous(), LO.contiguous(), AO.contiguous()
+    out = torch.empty(MO.shape[0], 16, 128, dtype=torch.bfloat16, device=dev)
+    _check(L.kv800_hip_decode_merge(_ptr(MO), _ptr(LO), _ptr(AO), MO.shape[0], int(ns), _ptr(out), _stream(dev)))
+    return out
+
+
+# ---------------------------------------------------------------- decode
+_CS16 = OrderedDict()      # (device, cos ptr, sin ptr, rows, versions) -> fp16 pair table; tables are model constants
+
+
+def rope_table16(cos_t, sin_t):
+    """Packed fp16 (cos, sin) table of every row of the bf16 tables, cached per table tensors (re-built when either
+    tensor is modified in place)."""
+    key = (str(cos_t.device), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0], cos_t._version, sin_t._version)
+    t = _CS16.get(key)
+    if t is None:
+        L = ops()
+        P = cos_t.shape[0]
+        t = torch.empty(P, 32, dtype=torch.int32, device=cos_t.device)
+        _check(L.kv800_hip_rope_table(_ptr(cos_t), _ptr(sin_t), P, _ptr(t), _stream(cos_t.device)))
+        _CS16[key] = t
+        while len(_CS16) > 8:
+            _CS16.popitem(last=False)
+    else:
+        _CS16.move_to_end(key)
+    return t
+
+
+def plan(B, nqmax, spb=None, target=None):
+    """(ns, spb) of a decode call: explicit spb; or the reference's target rule (kv800.py:366-367); or the library
+    plan (about two workgroups per CU)."""
+    if not nqmax:
+        return 0, 1
+    if spb is None and target:
+        spb = max(1, math.ceil(nqmax * B * 4 / target))
+    if spb is not None:
+        spb = max(1, int(spb))
+        return math.ceil(nqmax / spb), spb
+    ns, sp = ctypes.c_int64(), ctypes.c_int64()
+    _check(ops().kv800_hip_plan(B, nqmax, ctypes.byref(ns), ctypes.byref(sp)))
+    return ns.value, sp.value
+
+
+def paged_struct(P, B):
+    """kv800_paged_t of a kv800.Paged, plus the extents of its pools."""
+    dev = P.epool.device
+    _need(P.epool, "epool", torch.bfloat16, dev); _need(P.eoff, "eoff", torch.int64, dev)
+    _need(P.N, "N", torch.int32, dev); _need(P.NQ, "NQ", torch.int32, dev)
+    if P.eoff.stride(-1) != 1:
+        raise ValueError("eoff rows must be contiguous")
+    s = Paged()
+    nqmax = 0 if P.win else int(P.nqmax or 0)
+    if nqmax:
+        _need(P.qpool, "qpool", torch.uint8, dev); _need(P.boff, "boff", torch.int64, dev)
+        if P.boff.stride(-1) != 1:
+            raise ValueError("boff rows must be contiguous")
+        s.qpool, s.boff, s.boff_stride = P.qpool.data_ptr(), P.boff.data_ptr(), P.boff.stride(0)
+        qbytes = _extent(P.qpool)
+    else:
+        qbytes = 0
+    s.epool, s.eoff, s.eoff_stride = P.epool.data_ptr(), P.eoff.data_ptr(), P.eoff.stride(0)
+    s.ebs, s.e_hs, s.e_ts, s.e_v = int(P.ebs), int(P.e_hs), int(P.e_ts), int(P.e_v)
+    sink_elems = 0
+    if P.win and P.sk is not None:
+        _need(P.sk, "sk", torch.bfloat16, dev); _need(P.sv, "sv", torch.bfloat16, dev)
+        _need(P.skoff, "skoff", torch.int64, dev); _need(P.svoff, "svoff", torch.int64, dev)
+        s.sk, s.sv, s.skoff, s.svoff = P.sk.data_ptr(), P.sv.data_ptr(), P.skoff.data_ptr(), P.svoff.data_ptr()
+        sink_elems = min(_extent(P.sk), _extent(P.sv))
+    s.N, s.NQ = P.N.data_ptr(), P.NQ.data_ptr()
+    s.nqmax, s.win = nqmax, int(P.win or 0)
+    if P.N.shape[0] < B or P.NQ.shape[0] < B:
+        raise ValueError("N / NQ have fewer rows than q")
+    return s, qbytes, _extent(P.epool), sink_elems
+
+
+def decode(P, q, cos_t, sin_t, spb=None, target=None):
+    """q (B, 16, 128) bf16 post-RoPE -> (B, 16, 128) bf16: the fused HIP decode of one layer (kv800_hip_decode)."""
+    L = ops()
+    dev = q.device
+    _need(q, "q", torch.bfloat16, dev); _need(cos_t, "cos_t", torch.bfloat16, dev); _need(sin_t, "sin_t", torch.bfloat16, dev)
+    B = q.shape[0]
+    if q.dim() != 3 or tuple(q.shape[1:]) != (16, 128):
+        raise ValueError(f"q must be (B, 16, 128), got {tuple(q.shape)}")
+    if cos_t.shape != sin_t.shape or cos_t.dim() != 2 or cos_t.shape[1] != 32:
+        raise ValueError("cos_t / sin_t must be (P, 32)")
+    q, cos_t, sin_t = q.contiguous(), cos_t.contiguous(), sin_t.contiguous()
+    s, qbytes, eelems, selems = paged_struct(P, B)
+    out = torch.empty(B, 16, 128, dtype=torch.bfloat16, device=dev)
+    if B == 0:
+        return out
+    ns, sp = plan(B, s.nqmax, spb, target)
+    cs16 = rope_table16(cos_t, sin_t) if ns else None
+    wsb = int(L.kv800_hip_decode_workspace(B, ns, 0))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    _check(L.kv800_hip_decode_sized(ctypes.byref(s), _ptr(q), B, _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], _ptr(cs16),
+                                    qbytes, eelems, selems, _ptr(out), _ptr(ws), wsb, sp if ns else 0, _stream(dev)))
+    return out
+
+
+def decode_parts(P, q, cos_t, sin_t, spb=None, target=None):
+    """The three stages separately (decode_quant, decode_exact, decode_merge) with the partials returned:
+    (out, MO, LO, AO, ns). Same result as decode(); used by tests of each stage."""
+    L = ops()
+    dev = q.device
+    q, cos_t, sin_t = q.contiguous(), cos_t.contiguous(), sin_t.contiguous()
+    B = q.shape[0]
+    s, qbytes, eelems, selems = paged_struct(P, B)
+    ns, sp = plan(B, s.nqmax, spb, target)
+    MO = torch.empty(B, ns + 1, 16, dtype=torch.float32, device=dev)
+    LO = torch.empty_like(MO)
+    AO = torch.empty(B, ns + 1, 16, 128, dtype=torch.float32, device=dev)
+    scale = 128 ** -0.5 * LOG2E
+    st = _stream(dev)
+    if ns:
+        cs16 = rope_table16(cos_t, sin_t)
+        _check(L.kv800_hip_decode_quant_sized(_ptr(q), s.qpool, qbytes, s.boff, s.boff_stride, _ptr(P.NQ), _ptr(cs16),
+                                              cos_t.shape[0], _ptr(MO), _ptr(LO), _ptr(AO), B, ns, sp, scale, st))
+    _check(L.kv800_hip_decode_exact_sized(ctypes.byref(s), _ptr(q), _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], eelems,
+                                          selems, _ptr(MO), _ptr(LO), _ptr(AO), B, ns, scale, st))
+    out = torch.empty(B, 16, 128, dtype=torch.bfloat16, device=dev)
+    _check(L.kv800_hip_decode_merge(_ptr(MO), _ptr(LO), _ptr(AO), B, ns, _ptr(out), st))
+    return out, MO, LO, AO, ns

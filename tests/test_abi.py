@@ -1,0 +1,61 @@
+"""The C-ABI library (CPU, no GPU calls): it loads, exports every entry point include/kv800_hip.h declares, the Python
+binding's signature table covers exactly those, and host-side argument checks reject bad input before any launch."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import lfm3_kv800_amd.kv800_hip as kh
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kv800_hip.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(kv800_hip_\w+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.isfile(kh.LIB):
+        pytest.fail(f"{kh.LIB} not built: run __graft_entry__.build()")
+    return kh.load_library()
+
+
+def test_header_symbols_exported(lib):
+    names = declared()
+    assert len(names) >= 14
+    out = subprocess.run(["nm", "-D", "--defined-only", kh.LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (kv800_hip_\w+)", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for n in names:
+        getattr(lib, n)
+
+
+def test_binding_covers_header():
+    assert sorted(kh.SIGNATURES) == declared()
+
+
+def test_host_checks_reject_bad_arguments(lib):
+    # rejected on the host: no device memory is touched
+    assert lib.kv800_hip_quantize_blocks(None, None, -1, None, None) == -1
+    assert b"M" in lib.kv800_hip_last_error()
+    assert lib.kv800_hip_quantize_blocks(None, None, 2, None, None) == -1
+    assert lib.kv800_hip_flush(None, None, 0, 0, 0, 0, 0, None, None, 0, 256, 1, None, None, 1, 1, None) == -1
+    assert lib.kv800_hip_decode_merge(None, None, None, 1, 0, None, None) == -1
+    assert lib.kv800_hip_quantize_blocks(None, None, 0, None, None) == 0        # empty: a no-op
+
+
+def test_plan(lib):
+    ns, spb = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.kv800_hip_plan(64, 127, ctypes.byref(ns), ctypes.byref(spb)) == 0
+    assert (ns.value, spb.value) == (8, 16)
+    assert lib.kv800_hip_plan(2, 19, ctypes.byref(ns), ctypes.byref(spb)) == 0
+    assert ns.value * spb.value >= 19 and (ns.value - 1) * spb.value < 19
+    assert lib.kv800_hip_plan(4, 0, ctypes.byref(ns), ctypes.byref(spb)) == 0 and ns.value == 0
+    assert lib.kv800_hip_decode_workspace(64, 8, 0) >= 64 * 9 * 16 * 4 * 2 + 64 * 9 * 16 * 128 * 4

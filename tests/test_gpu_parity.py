@@ -1,0 +1,268 @@
+"""Parity of the HIP backend (through the C ABI) with the CPU oracle and the golden fixtures, on an MI355X.
+
+Bars: quantized codes / page contents bit-exact; decode outputs within 2e-2 max-abs and 1e-3
+mean-abs of the oracle's restatement of torch_decode.py (both bf16, same cache bytes), and within the reference's
+own rel < 1e-2 of its independent check (tests/test_parity.py:104)."""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import make_golden
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+DEV = "cuda"
+
+
+def say(*a):
+    print("[gpu-parity]", *a, flush=True)
+
+
+def to_dev_bf16(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bits_of(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def upload(case):
+    """oracle PagedCase (numpy) -> kv800.Paged on the GPU."""
+    import lfm3_kv800_amd.kv800 as kv
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return kv.Paged(qpool=T(case.qpool), boff=T(case.boff), epool=to_dev_bf16(case.epool), eoff=T(case.eoff),
+                    ebs=case.ebs, e_hs=case.e_hs, e_ts=case.e_ts, e_v=case.e_v,
+                    sk=to_dev_bf16(case.sk) if case.sinks else None, sv=to_dev_bf16(case.sv) if case.sinks else None,
+                    skoff=T(case.skoff), svoff=T(case.svoff), N=T(case.N), NQ=T(case.NQ), nqmax=case.nqmax, win=case.win)
+
+
+def download(P, oracle):
+    """kv800.Paged on the GPU -> oracle PagedCase over the same bytes."""
+    C = lambda t: t.detach().cpu().contiguous().numpy()
+    sinks = P.sk is not None
+    return oracle.PagedCase(qpool=C(P.qpool), boff=C(P.boff), epool=bits_of(P.epool), eoff=C(P.eoff), ebs=P.ebs,
+                            e_hs=P.e_hs, e_ts=P.e_ts, e_v=P.e_v, sk=bits_of(P.sk) if sinks else np.zeros(1, np.uint16),
+                            sv=bits_of(P.sv) if sinks else np.zeros(1, np.uint16), skoff=C(P.skoff),
+                            svoff=C(P.svoff), sinks=sinks, N=C(P.N), NQ=C(P.NQ), nqmax=int(P.nqmax or 0),
+                            win=int(P.win or 0), B=P.N.shape[0])
+
+
+def close(out_bits, ref_bits, what):
+    o = torch.from_numpy(out_bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    r = torch.from_numpy(ref_bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    d = np.abs(o - r)
+    say(f"{what}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+    assert np.isfinite(o).all(), what
+    assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (what, d.max(), d.mean())
+
+
+# ---------------------------------------------------------------- quantizer / flush / dequantizer: bit-exact
+@pytest.mark.parametrize("case", ["parity", "outlier", "edge", "scaled"])
+def test_quantize_golden(hip, case):
+    g = np.load(os.path.join(make_golden.HERE, "quantize_golden.npz"))
+    kb, vb = make_golden.case_inputs(case)
+    say("quantize golden", case, kb.shape)
+    out = hip.quantize_blocks(to_dev_bf16(kb), to_dev_bf16(vb)).cpu().numpy()
+    if case == "scaled":
+        assert [hashlib.sha256(out[m].tobytes()).hexdigest() for m in range(out.shape[0])] == list(g["scaled_sha256"])
+    else:
+        want = g[f"{case}_out"]
+        assert np.array_equal(out, want), f"{int((out != want).sum())} of {out.size} bytes differ"
+
+
+@pytest.mark.parametrize("dist", ["normal", "offset", "outlier", "wide"])
+def test_quantize_random_vs_oracle(hip, oracle, dist):
+    rng = np.random.RandomState({"normal": 11, "offset": 12, "outlier": 13, "wide": 14}[dist])
+    M = 24
+    k = rng.standard_normal((M, 256, 4, 128)).astype(np.float32)
+    v = rng.standard_normal((M, 256, 4, 128)).astype(np.float32)
+    if dist == "offset":
+        k += 3 * rng.standard_normal((1, 1, 4, 128)).astype(np.float32)
+    if dist == "outlier":
+        k[rng.random_sample(k.shape) < 0.01] *= 8
+        v[rng.random_sample(v.shape) < 0.01] *= 8
+    if dist == "wide":
+        k *= np.exp2(rng.randint(-12, 6, size=(M, 1, 4, 128))).astype(np.float32)
+        v *= np.exp2(rng.randint(-12, 6, size=(M, 256, 4, 1))).astype(np.float32)
+    kb, vb = oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+    say("quantize random", dist, M)
+    got = hip.quantize_blocks(to_dev_bf16(kb), to_dev_bf16(vb)).cpu().numpy()
+    want = oracle.quantize_blocks(kb, vb)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} bytes differ"
+
+
+def test_flush_two_kv_groups(hip, oracle):
+    """vLLM geometry: two exact KV groups (different shuffled block tables, ebs 128, [pages, 4, 128, 256] bf16) and one
+    quant layer per group with 1280-token quant pages of 262,144 bytes. Each layer must gather from its own group's
+    pages (the 0.1.1 fix, vllm_attn.py:301); reading the other group's table must give different bytes."""
+    rng = np.random.RandomState(5)
+    R, n_tok, ebs = 6, 2048 + 384, 128
+    pages_per_row = (n_tok + ebs - 1) // ebs
+    nq_new = np.array([(n_tok - 128) // 256 - r % 3 for r in range(R)], np.int32)     # ragged: 9, 8, 7 sub-blocks
+    nq_prev = np.array([r % 2 for r in range(R)], np.int32)                             # some already flushed
+    K = [oracle.randn_bf16(rng, (R, n_tok, 4, 128)) for _ in range(2)]
+    V = [oracle.randn_bf16(rng, (R, n_tok, 4, 128)) for _ in range(2)]
+    npages = R * pages_per_row + 3
+    elems = 4 * ebs * 256
+    tables, pools = [], []
+    for gidx in range(2):
+        perm = rng.permutation(npages)[:R * pages_per_row].reshape(R, pages_per_row)
+        pool = np.zeros((npages, 4, ebs, 256), np.uint16)
+        for r in range(R):
+            for p in range(n_tok):
+                pg = perm[r, p // ebs]
+                pool[pg, :, p % ebs, :128] = K[gidx][r, p]
+                pool[pg, :, p % ebs, 128:] = V[gidx][r, p]
+        tables.append(perm.astype(np.int64))
+        pools.append(pool)
+    qpages = R * 2 + 2
+    qperm = rng.permutation(qpages)[:R * 2].reshape(R, 2).astype(np.int64)
+    outs = []
+    for gidx in range(2):
+        epool = to_dev_bf16(pools[gidx])
+        eoff = torch.from_numpy(tables[gidx] * elems).to(DEV)
+        qpool = torch.zeros(qpages * 262144, dtype=torch.uint8, device=DEV)
+        say("flush group", gidx)
+        hip.flush(epool, eoff, ebs, ebs * 256, 256, 128, qpool, torch.from_numpy(qperm).to(DEV), 1280, 262144,
+                  torch.from_numpy(nq_prev).to(DEV), torch.from_numpy(nq_new).to(DEV), int((nq_new - nq_prev).max()))
+        outs.append(qpool.cpu().numpy())
+    for gidx in range(2):
+        q = outs[gidx]
+        for r in range(R):
+            js = list(range(nq_prev[r], nq_new[r]))
+            want = oracle.quantize_blocks(np.stack([K[gidx][r, 256 * j:256 * j + 256] for j in js]),
+                                          np.stack([V[gidx][r, 256 * j:256 * j + 256] for j in js]))
+            for i, j in enumerate(js):
+                off = qperm[r, (256 * j) // 1280] * 262144 + ((256 * j) % 1280) // 256 * 51200
+                assert np.array_equal(q[off:off + 51200], want[i]), (gidx, r, j)
+                other = oracle.quantize_blocks(K[1 - gidx][r, 256 * j:256 * j + 256][None],
+                                               V[1 - gidx][r, 256 * j:256 * j + 256][None])[0]
+                assert not np.array_equal(q[off:off + 51200], other)
+            for j in range(nq_prev[r]):                   # already-flushed sub-blocks are left untouched
+                off = qperm[r, (256 * j) // 1280] * 262144 + ((256 * j) % 1280) // 256 * 51200
+                assert not q[off:off + 51200].any()
+
+
+def test_dequantize_vs_oracle(hip, oracle):
+    kb, vb = make_golden.case_inputs("outlier")
+    sb = oracle.quantize_blocks(kb, vb)
+    say("dequantize", sb.shape)
+    k, v = hip.dequantize_blocks(torch.from_numpy(sb).to(DEV))
+    kw, vw = oracle.dequantize_blocks(sb)
+    assert np.array_equal(bits_of(k), kw)
+    assert np.array_equal(v.cpu().numpy().view(np.uint32), vw.view(np.uint32))
+
+
+# ---------------------------------------------------------------- decode
+QUANT_NS = (50, 383, 384, 700, 1500, 5000)
+WINDOW_NS = (3, 10, 200, 259, 260, 1500)
+
+
+@pytest.mark.parametrize("win,n", [(0, n) for n in QUANT_NS] + [(256, n) for n in WINDOW_NS])
+def test_decode_reference_cases(hip, oracle, win, n):
+    """tests/test_parity.py's 12 cases through the product PagedStore (HIP flush) and kv800.decode."""
+    import lfm3_kv800_amd.kv800 as kv
+    import test_oracle as T
+    q, K, V = T.parity_inputs(oracle, n, win)
+    cos, sin = oracle.rope_tables(8192)
+    say("decode case", win, n)
+    st = kv.PagedStore(2, n + 8, DEV, window=win)
+    pre = max(1, n - 5)
+    st.append(to_dev_bf16(K[:, :pre]), to_dev_bf16(V[:, :pre]))
+    for i in range(pre, n):
+        st.append(to_dev_bf16(K[:, i:i + 1]), to_dev_bf16(V[:, i:i + 1]))
+    kv.set_backend("hip")
+    try:
+        out = kv.decode(st.paged(), to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), st.H)
+        assert kv.get_backend() == "hip"
+    finally:
+        kv.set_backend(None)
+    ob = bits_of(out)
+    want = oracle.decode(download(st.paged(), oracle), q, cos, sin)
+    close(ob, want, f"win={win} n={n} vs oracle")
+    ref = oracle.reference_f64(q, K, V, cos, sin, window=win)
+    o = oracle.bf16_to_f32(ob).astype(np.float64)
+    rel = np.linalg.norm(o - ref) / np.linalg.norm(ref)
+    say(f"win={win} n={n}: rel {rel:.2e} vs the independent check")
+    assert rel < 1e-2
+
+
+@pytest.mark.parametrize("win", [0, 256])
+def test_decode_shuffled_ragged(hip, oracle, win):
+    rng = np.random.RandomState(21 + win)
+    lens = [1, 127, 128, 383, 384, 385, 700, 1024, 2311, 4096]
+    K = [oracle.randn_bf16(rng, (n, 4, 128), offset=rng.standard_normal((1, 4, 128))) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (len(lens), 16, 128), scale=1.5)
+    cos, sin = oracle.rope_tables(4200)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, win=win, ebs=128, shuffle_seed=9)
+    say("decode ragged", win, lens)
+    P = upload(case)
+    for spb in (None, 1, 3):
+        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=spb)
+        close(bits_of(out), oracle.decode(case, q, cos, sin), f"ragged win={win} spb={spb}")
+
+
+def test_decode_stages_and_merge(hip, oracle):
+    rng = np.random.RandomState(31)
+    lens = [900, 3000, 1500]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (3, 16, 128))
+    cos, sin = oracle.rope_tables(3100)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, shuffle_seed=4)
+    say("decode stages")
+    P = upload(case)
+    out, MO, LO, AO, ns = hip.decode_parts(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=2)
+    assert ns == 6
+    merged = oracle.combine(MO.cpu().numpy(), LO.cpu().numpy(), AO.cpu().numpy(), ns)
+    close(bits_of(out), merged, "HIP merge vs oracle combine of the same partials")
+    close(bits_of(out), oracle.decode(case, q, cos, sin), "staged decode vs oracle")
+    fused = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=2)
+    assert torch.equal(fused, out)
+
+
+def test_decode_full_size_sampled_rows(hip, oracle):
+    """BASELINE config 3 at full size (64 x 32,768, permuted tables): cache built on the GPU by the HIP quantizer,
+    decoded by the HIP kernels; rows 0, 31 and 63 are decoded by the oracle from the downloaded pages."""
+    import lfm3_kv800_amd.kv800 as kv
+    B, n, ebs = 64, 32768, 128
+    nq = (n - 128) // 256
+    g = torch.Generator(device=DEV).manual_seed(3)
+    say("full size: building", B, n)
+    qperm = torch.randperm(B * nq, generator=g, device=DEV)
+    boff = (qperm.view(B, nq) * 51200).to(torch.int64)
+    qpool = torch.empty(B * nq * 51200, dtype=torch.uint8, device=DEV)
+    for b0 in range(0, B, 8):
+        k = torch.randn(8 * nq, 256, 4, 128, generator=g, device=DEV).to(torch.bfloat16)
+        v = torch.randn(8 * nq, 256, 4, 128, generator=g, device=DEV).to(torch.bfloat16)
+        sb = hip.quantize_blocks(k, v)
+        dst = boff[b0:b0 + 8].reshape(-1)[:, None] + torch.arange(51200, device=DEV)
+        qpool[dst.reshape(-1)] = sb.reshape(-1)
+    pages = (n + ebs - 1) // ebs
+    ex0 = nq * 256 // ebs
+    npg = B * (pages - ex0)
+    eperm = torch.randperm(npg, generator=g, device=DEV).view(B, pages - ex0)
+    eoff = torch.zeros(B, pages, dtype=torch.int64, device=DEV)
+    eoff[:, ex0:] = eperm * (4 * ebs * 256)
+    epool = torch.randn(npg, 4, ebs, 256, generator=g, device=DEV).to(torch.bfloat16)
+    N = torch.full((B,), n, dtype=torch.int32, device=DEV)
+    NQ = torch.full((B,), nq, dtype=torch.int32, device=DEV)
+    P = kv.Paged(qpool=qpool, boff=boff, epool=epool, eoff=eoff, ebs=ebs, e_hs=ebs * 256, e_ts=256, e_v=128,
+                 sk=None, sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nq, win=0)
+    q = torch.randn(B, 16, 128, generator=g, device=DEV).to(torch.bfloat16)
+    cos, sin = oracle.rope_tables(n)
+    say("full size: decode")
+    out = hip.decode(P, q, to_dev_bf16(cos), to_dev_bf16(sin))
+    torch.cuda.synchronize()
+    rows = [0, 31, 63]
+    case = download(P, oracle)
+    sub = oracle.PagedCase(**{**case.__dict__, "boff": case.boff[rows], "eoff": case.eoff[rows], "N": case.N[rows],
+                              "NQ": case.NQ[rows], "B": len(rows)})
+    say("full size: oracle rows", rows)
+    want = oracle.decode(sub, bits_of(q)[rows], cos, sin)
+    close(bits_of(out)[rows], want, "64x32768 rows 0/31/63")
