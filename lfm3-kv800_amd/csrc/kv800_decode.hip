@@ -225,7 +225,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-      uint32_t bpv[4];
+      f4 sacc2[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {   // QK tile u: tokens 32 c + 16 u + (0..15)
         const uint32_t* csrow = W.cs[cb] + (16 * u + n) * 32;
@@ -260,17 +260,24 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
           const uint4 t4 = *reinterpret_cast<const uint4*>(csrow + 16 * kk + 4 * g);
           sacc = mfma16(pack8(t4.x, t4.y, t4.z, t4.w), wt[kk], sacc);
         }
-        // ---- online softmax (lazy max); rows are columns n, tokens 4 g + i of this tile
-        float tmax = fmaxf(fmaxf(sacc[0], sacc[1]), fmaxf(sacc[2], sacc[3]));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        if (__any(tmax > m + LAZY)) {
-          const float mn = fmaxf(m, tmax);
-          const float al = exp2f(m - mn);
-          m = mn; lsum *= al; lvs *= al;
+        sacc2[u] = sacc;
+      }
+      // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
+      float tmax = fmaxf(fmaxf(fmaxf(sacc2[0][0], sacc2[0][1]), fmaxf(sacc2[0][2], sacc2[0][3])),
+                         fmaxf(fmaxf(sacc2[1][0], sacc2[1][1]), fmaxf(sacc2[1][2], sacc2[1][3])));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      if (__any(tmax > m + LAZY)) {
+        const float mn = fmaxf(m, tmax);
+        const float al = exp2f(m - mn);
+        m = mn; lsum *= al; lvs *= al;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] *= al;
-        }
+        for (int i = 0; i < 8; ++i) acc[i] *= al;
+      }
+      uint32_t bpv[4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const f4 sacc = sacc2[u];
         const int t0 = 32 * c + 16 * u + 4 * g;
         const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
         const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);

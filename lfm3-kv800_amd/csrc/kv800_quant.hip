@@ -143,15 +143,22 @@ __device__ __forceinline__ uint32_t gather4(uint64_t m, int jj) {
   return (uint32_t)((x | (x >> 15) | (x >> 30) | (x >> 45)) & 0xFull);
 }
 
-constexpr int LDS_BYTES = 2 * 8 * 512 * 4 + 2 * 512 * 4;   // K-path min/max partials + lo / den; V path reuses it
+struct QuantLds {                  // K path: per-wave min / max partials, then per-column lo and divisor
+  float red_min[QW][512];
+  float red_max[QW][512];
+  float col_lo[512];
+  float col_den[512];
+};
+constexpr int LDS_BYTES = (int)sizeof(QuantLds);
 
 template <typename Src>
 __device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  float* red_min = reinterpret_cast<float*>(lds);               // [QW][512]
-  float* red_max = red_min + QW * 512;                          // [QW][512]
-  float* col_lo = red_max + 16 * 512;                           // [512]
-  float* col_den = col_lo + 512;                                // [512]
+  QuantLds& S = *reinterpret_cast<QuantLds*>(lds);
+  float* red_min = &S.red_min[0][0];
+  float* red_max = &S.red_max[0][0];
+  float* col_lo = S.col_lo;
+  float* col_den = S.col_den;
 
   // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16)
   const int h = lane >> 4, c0 = 8 * (lane & 15);

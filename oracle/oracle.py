@@ -256,10 +256,11 @@ def _aq(x, bits, axis):
     return np.clip(np.round((x - lo8) / sc8), 0, 2 ** bits - 1) * sc8 + lo8
 
 
-def reference_f64(q_bits, K_bits, V_bits, cos_bits, sin_bits, window=0):
+def reference_f64(q_bits, K_bits, V_bits, cos_bits, sin_bits, window=0, round_k=True):
     """q (B,16,128), K/V (B,n,4,128) bf16 bits (pre-RoPE K), cos/sin (P,32) bf16 bits -> (B,16,128) float64.
     The reference's independent check, in float64 (the fake quant itself works on float32 values as the reference
-    does; everything after it is float64)."""
+    does; everything after it is float64). round_k=False skips the two bf16 roundings of K (dequantized, then
+    rotated) that the reference and torch_decode.py apply: the exact attention over the quantized cache."""
     q = bf16_to_f32(q_bits).astype(np.float64)
     Kh = bf16_to_f32(K_bits).astype(np.float64); Vh = bf16_to_f32(V_bits).astype(np.float64)
     B, n = Kh.shape[:2]
@@ -269,7 +270,7 @@ def reference_f64(q_bits, K_bits, V_bits, cos_bits, sin_bits, window=0):
     if nq:
         x = Kh[:, :nq * BLK].reshape(B, nq, BLK, 512).astype(np.float32)
         kq = _aq(x.astype(np.float64), 2, 2).reshape(B, nq * BLK, 4, 128)
-        K[:, :nq * BLK] = bf16_to_f32(f32_to_bf16(kq.astype(np.float32))).astype(np.float64)
+        K[:, :nq * BLK] = bf16_to_f32(f32_to_bf16(kq.astype(np.float32))).astype(np.float64) if round_k else kq
         y = (Vh[:, :nq * BLK] @ H).reshape(B, nq * BLK, 2, 256)
         V[:, :nq * BLK] = _aq(y, 1, -1).reshape(B, nq * BLK, 4, 128) @ H
     cs = bf16_to_f32(cos_bits[:n]).astype(np.float64)[None, :, None, :]
@@ -278,7 +279,8 @@ def reference_f64(q_bits, K_bits, V_bits, cos_bits, sin_bits, window=0):
     Kr = K.copy()
     Kr[..., :32] = K0 * cs - K2 * sn
     Kr[..., 64:96] = K2 * cs + K0 * sn
-    Kr = bf16_to_f32(f32_to_bf16(Kr.astype(np.float32))).astype(np.float64)
+    if round_k:
+        Kr = bf16_to_f32(f32_to_bf16(Kr.astype(np.float32))).astype(np.float64)
     Kr, V = np.repeat(Kr, 4, axis=2), np.repeat(V, 4, axis=2)            # (B, n, 16, 128)
     sc = np.einsum("bhd,bnhd->bhn", q, Kr) * 128 ** -0.5
     if window:
