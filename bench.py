@@ -96,7 +96,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-rows", type=int, default=8)
+    ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
     a = ap.parse_args()
     if a.gpus != 1:

@@ -29,8 +29,9 @@ __device__ __forceinline__ float bfround(float f) { return __uint_as_float(f2bf(
 // fp8 e4m3fn byte -> float, exact; no NaN handling (the scales the quantizer writes are finite for finite input)
 __device__ __forceinline__ float f8d(uint32_t b) {
   const uint32_t e = (b >> 3) & 15u, m = b & 7u;
-  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
-  return (b & 0x80u) ? -mag : mag;
+  const uint32_t nrm = ((e + 120u) << 23) | (m << 20);
+  const uint32_t sub = __float_as_uint((float)m * 0.001953125f);
+  return __uint_as_float((e ? nrm : sub) | ((b & 0x80u) << 24));   // selects, no control flow
 }
 
 // float -> fp8 e4m3fn byte with torch's .to(float8_e4m3fn) semantics (round to nearest even on the e4m3 grid,

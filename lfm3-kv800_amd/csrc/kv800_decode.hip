@@ -62,7 +62,8 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
 // ---------------------------------------------------------------- quantized sub-blocks
 constexpr int QWAVES = 4;
 struct QWaveLds {
-  uint8_t kls[1024];          // klo [4][128] | ksc [4][128] of the current sub-block
+  float s4[512];              // 4 * scale * ksc [head][channel] of the current sub-block
+  float tp[512];              // klo - 4 * ksc  [head][channel]
   float vs[2][256];           // decoded vsc per (head group, token)
   float vl[2][256];           // decoded vlo
   uint8_t vb[2][32 * 64];     // vb bytes of a 32-token chunk (double buffer)
@@ -77,8 +78,6 @@ struct QFinLds {              // end-of-split merge of the 4 waves (reuses the L
   float acc[QWAVES][16][128];
 };
 static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
-
-__device__ __forceinline__ float f8b(const uint8_t* p, int i) { return f8d(p[i]); }
 
 __global__ void __launch_bounds__(256, 2)
 decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
@@ -109,8 +108,24 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     const uint8_t* sb = qpool + base;
     const uint32_t* csb = cs16 + (int64_t)jb * BLK * 32;
 
-    // ---- stage per-sub-block scales: klo / ksc (1 KB), vlo / vsc decoded (256 tokens x 2 groups)
-    *reinterpret_cast<uint4*>(W.kls + 16 * lane) = *reinterpret_cast<const uint4*>(sb + KLO_O + 16 * lane);
+    // ---- stage per-sub-block scales as floats: S = 4 scale ksc, T = klo - 4 ksc per (head, channel); vlo / vsc
+    {
+      const uint2 lo2 = *reinterpret_cast<const uint2*>(sb + KLO_O + 8 * lane);   // channels 8 lane .. 8 lane + 7
+      const uint2 sc2 = *reinterpret_cast<const uint2*>(sb + KSC_O + 8 * lane);
+      float4 sa, sbv, ta, tb;
+      float sv[8], tv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ksc = f8d(((e < 4 ? sc2.x : sc2.y) >> (8 * (e & 3))) & 0xFFu);
+        const float klo = f8d(((e < 4 ? lo2.x : lo2.y) >> (8 * (e & 3))) & 0xFFu);
+        sv[e] = 4.f * scale * ksc;
+        tv[e] = klo - 4.f * ksc;
+      }
+      sa = make_float4(sv[0], sv[1], sv[2], sv[3]); sbv = make_float4(sv[4], sv[5], sv[6], sv[7]);
+      ta = make_float4(tv[0], tv[1], tv[2], tv[3]); tb = make_float4(tv[4], tv[5], tv[6], tv[7]);
+      *reinterpret_cast<float4*>(W.s4 + 8 * lane) = sa; *reinterpret_cast<float4*>(W.s4 + 8 * lane + 4) = sbv;
+      *reinterpret_cast<float4*>(W.tp + 8 * lane) = ta; *reinterpret_cast<float4*>(W.tp + 8 * lane + 4) = tb;
+    }
     {
       const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
       const uint2 vs2 = *reinterpret_cast<const uint2*>(sb + VSC_O + 8 * lane);
@@ -140,63 +155,64 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     }
     __builtin_amdgcn_wave_barrier();
 
-    // ---- weights of this sub-block (B operands), scaled by `scale` so the accumulator is in log2 units
-    const bool act = (hn == g);
-    const uint8_t* ksc_g = W.kls + 512 + g * 128;
-    const uint8_t* klo_n = W.kls + hn * 128;
-    const uint8_t* ksc_n = W.kls + 512 + hn * 128;
+    // ---- weights of this sub-block (B operands), scaled by `scale` so the accumulator is in log2 units.
+    // Lanes whose row n is not in head g (block-diagonal part) multiply by zero instead of branching.
+    const float actf = (hn == g) ? 1.f : 0.f;
+    const float* s4g = W.s4 + g * 128;
+    const float* s4n = W.s4 + hn * 128;
+    const float* tpn = W.tp + hn * 128;
     const float* qn = L.q[n];
     h8 wr[16], wnp[8], wt[2];
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-#pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        uint32_t hw[4];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int j = 4 * d + 2 * e2 + u;
-          const float s0 = act ? 4.f * scale * f8b(ksc_g, j) : 0.f;
-          const float s2 = act ? 4.f * scale * f8b(ksc_g, j + 64) : 0.f;
-          const float q0 = qn[j], q2 = qn[j + 64];
-          hw[2 * u] = pk2(q0 * s0, q2 * s0);
-          hw[2 * u + 1] = pk2(q2 * s2, -q0 * s2);
-        }
-        wr[2 * d + e2] = pack8(hw[0], hw[1], hw[2], hw[3]);
-      }
-      uint32_t hn4[4];
+      const float4 q0 = *reinterpret_cast<const float4*>(qn + 4 * d), q1 = *reinterpret_cast<const float4*>(qn + 32 + 4 * d);
+      const float4 q2 = *reinterpret_cast<const float4*>(qn + 64 + 4 * d), q3 = *reinterpret_cast<const float4*>(qn + 96 + 4 * d);
+      const float4 S0 = *reinterpret_cast<const float4*>(s4g + 4 * d), S1 = *reinterpret_cast<const float4*>(s4g + 32 + 4 * d);
+      const float4 S2 = *reinterpret_cast<const float4*>(s4g + 64 + 4 * d), S3 = *reinterpret_cast<const float4*>(s4g + 96 + 4 * d);
+      const float a0[4] = {q0.x, q0.y, q0.z, q0.w}, a1[4] = {q1.x, q1.y, q1.z, q1.w};
+      const float a2[4] = {q2.x, q2.y, q2.z, q2.w}, a3[4] = {q3.x, q3.y, q3.z, q3.w};
+      const float b0[4] = {S0.x * actf, S0.y * actf, S0.z * actf, S0.w * actf};
+      const float b1[4] = {S1.x * actf, S1.y * actf, S1.z * actf, S1.w * actf};
+      const float b2[4] = {S2.x * actf, S2.y * actf, S2.z * actf, S2.w * actf};
+      const float b3[4] = {S3.x * actf, S3.y * actf, S3.z * actf, S3.w * actf};
+      uint32_t hw[8], hnp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int j = 4 * d + u;
-        const float s1 = act ? 4.f * scale * f8b(ksc_g, 32 + j) : 0.f;
-        const float s3 = act ? 4.f * scale * f8b(ksc_g, 96 + j) : 0.f;
-        hn4[u] = pk2(qn[32 + j] * s1, qn[96 + j] * s3);
+        hw[2 * u] = pk2(a0[u] * b0[u], a2[u] * b0[u]);
+        hw[2 * u + 1] = pk2(a2[u] * b2[u], -a0[u] * b2[u]);
+        hnp[u] = pk2(a1[u] * b1[u], a3[u] * b3[u]);
       }
-      wnp[d] = pack8(hn4[0], hn4[1], hn4[2], hn4[3]);
+      wr[2 * d] = pack8(hw[0], hw[1], hw[2], hw[3]);
+      wr[2 * d + 1] = pack8(hw[4], hw[5], hw[6], hw[7]);
+      wnp[d] = pack8(hnp[0], hnp[1], hnp[2], hnp[3]);
     }
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
+      const int j0 = 16 * kk + 4 * g;
+      const float4 q0 = *reinterpret_cast<const float4*>(qn + j0), q2 = *reinterpret_cast<const float4*>(qn + 64 + j0);
+      const float4 T0 = *reinterpret_cast<const float4*>(tpn + j0), T2 = *reinterpret_cast<const float4*>(tpn + 64 + j0);
+      const float a0[4] = {q0.x, q0.y, q0.z, q0.w}, a2[4] = {q2.x, q2.y, q2.z, q2.w};
+      const float t0[4] = {T0.x, T0.y, T0.z, T0.w}, t2[4] = {T2.x, T2.y, T2.z, T2.w};
       uint32_t ht[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = 16 * kk + 4 * g + u;
-        const float t0 = f8b(klo_n, j) - 4.f * f8b(ksc_n, j);
-        const float t2 = f8b(klo_n, j + 64) - 4.f * f8b(ksc_n, j + 64);
-        const float q0 = qn[j], q2 = qn[j + 64];
-        ht[u] = pk2(scale * (q0 * t0 + q2 * t2), scale * (q2 * t0 - q0 * t2));
-      }
+      for (int u = 0; u < 4; ++u)
+        ht[u] = pk2(scale * (a0[u] * t0[u] + a2[u] * t2[u]), scale * (a2[u] * t0[u] - a0[u] * t2[u]));
       wt[kk] = pack8(ht[0], ht[1], ht[2], ht[3]);
     }
     float c13 = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = 8 * g + u;
-      const float t1 = f8b(klo_n, 32 + j) - 4.f * f8b(ksc_n, 32 + j);
-      const float t3 = f8b(klo_n, 96 + j) - 4.f * f8b(ksc_n, 96 + j);
-      c13 += qn[32 + j] * t1 + qn[96 + j] * t3;
+    {
+      const float4 q1a = *reinterpret_cast<const float4*>(qn + 32 + 8 * g), q1b = *reinterpret_cast<const float4*>(qn + 36 + 8 * g);
+      const float4 q3a = *reinterpret_cast<const float4*>(qn + 96 + 8 * g), q3b = *reinterpret_cast<const float4*>(qn + 100 + 8 * g);
+      const float4 t1a = *reinterpret_cast<const float4*>(tpn + 32 + 8 * g), t1b = *reinterpret_cast<const float4*>(tpn + 36 + 8 * g);
+      const float4 t3a = *reinterpret_cast<const float4*>(tpn + 96 + 8 * g), t3b = *reinterpret_cast<const float4*>(tpn + 100 + 8 * g);
+      c13 = q1a.x * t1a.x + q1a.y * t1a.y + q1a.z * t1a.z + q1a.w * t1a.w + q1b.x * t1b.x + q1b.y * t1b.y + q1b.z * t1b.z +
+            q1b.w * t1b.w + q3a.x * t3a.x + q3a.y * t3a.y + q3a.z * t3a.z + q3a.w * t3a.w + q3b.x * t3b.x +
+            q3b.y * t3b.y + q3b.z * t3b.z + q3b.w * t3b.w;
     }
     c13 += __shfl_xor(c13, 16);
     c13 += __shfl_xor(c13, 32);
     c13 *= scale;
+    (void)s4n;
 
     // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
     for (int c = 0; c < 8; ++c) {
