@@ -61,22 +61,58 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
 
 // ---------------------------------------------------------------- quantized sub-blocks
 constexpr int QWAVES = 4;
+// LDS row strides are padded (132 floats, 272 floats, 9 x 16 bytes) so that the 16 lanes of a lane group, which read
+// 16 different rows at the same column, fall into distinct banks; the vb chunk is XOR-swizzled instead (below).
+constexpr int QROW = 132, HROW = 132, VROW = 272, CSP = 9;
 struct QWaveLds {
-  float s4[512];              // 4 * scale * ksc [head][channel] of the current sub-block
-  float tp[512];              // klo - 4 * ksc  [head][channel]
-  float vs[2][256];           // decoded vsc per (head group, token)
-  float vl[2][256];           // decoded vlo
-  uint8_t vb[2][32 * 64];     // vb bytes of a 32-token chunk (double buffer)
-  uint32_t cs[2][32 * 32];    // fp16 (cos, sin) rows of the chunk's 32 positions (double buffer)
+  float s4[4 * HROW];         // 4 * scale * ksc [head][channel] of the current sub-block
+  float tp[4 * HROW];         // klo - 4 * ksc  [head][channel]
+  float vs[2][VROW];          // decoded vsc per (head group, token)
+  float vl[2][VROW];          // decoded vlo
+  u4v vb[2][32 * 4];          // vb bytes of a 32-token chunk (double buffer), 16-byte pieces placed by vb_at
+  u4v cs[2][32 * CSP];         // fp16 (cos, sin) rows of the chunk's 32 positions (double buffer), placed by cs_at
 };
 struct QLds {
-  float q[16][128];
+  float q[16][QROW];
   QWaveLds wv[QWAVES];
 };
 struct QFinLds {              // end-of-split merge of the 4 waves (reuses the LDS)
   float m[QWAVES][16], l[QWAVES][16], lv[QWAVES][16];
-  float acc[QWAVES][16][128];
+  float acc[QWAVES][16][QROW];
 };
+// 16-byte slot of (token t of the chunk, piece k = head) in a vb chunk buffer: piece k of token t is stored at slot
+// k ^ ((t >> 2) & 3) of the token's 4, so the four lane groups (tokens 4 g + ...) read four different banks
+__device__ __forceinline__ int vb_at(int t, int k) { return 4 * t + (k ^ ((t >> 2) & 3)); }
+// 16-byte slot of piece p (dwords 4 p .. 4 p + 3) of rope row r in a chunk buffer: rows are padded to 9 slots and the
+// pieces of rows with (r / 4) odd are swapped in pairs, so the 16 (row, piece) pairs a rope / nope read touches
+// (4 tokens x 4 lane groups) cover all 16 bank quads
+__device__ __forceinline__ int cs_at(int r, int p) { return r * CSP + (p ^ ((r >> 2) & 1)); }
+
+// rope + nope features of one kc dword (channels e = 0..3 of the lane's 8, cos / sin in cs4) against weight blocks
+// w0 (channels 0, 1), w1 (channels 2, 3) and wn (nope, channels 0..3). f = 1 + code / 4 is built exactly in fp16 by
+// placing the code under the exponent of 1.0 (0x3C | code in the high byte).
+// km = 0x03030303 and kc = 0x3C3C3C3C arrive in VGPRs so that each (x & km) | kc is a single v_and_or_b32 (a VALU
+// instruction may read only one literal or SGPR).
+__device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn, f4 a, uint32_t km, uint32_t kc) {
+  const uint32_t Q0 = (x & km) | kc;
+  const uint32_t Q2 = ((x >> 4) & km) | kc;
+  const uint32_t Q1 = ((x >> 2) & km) | kc;
+  const uint32_t Q3 = ((x >> 6) & km) | kc;
+  const uint32_t csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+  uint32_t ga[4], gb[4], f13[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t sel = 0x0Cu | ((uint32_t)e << 8) | (0x0Cu << 16) | ((uint32_t)(4 + e) << 24);
+    const h2 F = as_h2(__builtin_amdgcn_perm(Q2, Q0, sel));   // (f0, f2) of channel e
+    const h2 CS = as_h2(csv[e]);
+    ga[e] = hbits(CS * h2{F.x, F.x});
+    gb[e] = hbits(CS * h2{F.y, F.y});
+    f13[e] = __builtin_amdgcn_perm(Q3, Q1, sel);             // (f1, f3) of channel e
+  }
+  a = mfma16(pack8(ga[0], gb[0], ga[1], gb[1]), w0, a);
+  a = mfma16(pack8(ga[2], gb[2], ga[3], gb[3]), w1, a);
+  return mfma16(pack8(f13[0], f13[1], f13[2], f13[3]), wn, a);
+}
 static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
 
 __global__ void __launch_bounds__(256, 2)
@@ -90,8 +126,13 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
+  // kc bytes a lane reads for token group tg of a 16-token tile: token 4 (n / 4) + tg, head n % 4, channels 8 g .. + 7
+  const int kofs = (n >> 2) * 512 + (n & 3) * 32 + 8 * g;
+  uint32_t KM, KC;   // code mask and fp16 exponent bytes, opaque VGPR values (see rope_nope)
+  asm volatile("v_mov_b32 %0, 0x03030303" : "=v"(KM));
+  asm volatile("v_mov_b32 %0, 0x3c3c3c3c" : "=v"(KC));
 
-  for (int i = tid; i < 16 * 128; i += 256) L.q[i >> 7][i & 127] = bf2f(q[(int64_t)b * 2048 + i]);
+  for (int i = tid; i < 16 * 128; i += 256) L.q[i >> 7][i & 127] = bf2f(q[(int64_t)b * 2048 + i]);   // padded rows
   __syncthreads();
 
   float m = NEG_BIG, lsum = 0.f, lvs = 0.f;
@@ -123,8 +164,9 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
       }
       sa = make_float4(sv[0], sv[1], sv[2], sv[3]); sbv = make_float4(sv[4], sv[5], sv[6], sv[7]);
       ta = make_float4(tv[0], tv[1], tv[2], tv[3]); tb = make_float4(tv[4], tv[5], tv[6], tv[7]);
-      *reinterpret_cast<float4*>(W.s4 + 8 * lane) = sa; *reinterpret_cast<float4*>(W.s4 + 8 * lane + 4) = sbv;
-      *reinterpret_cast<float4*>(W.tp + 8 * lane) = ta; *reinterpret_cast<float4*>(W.tp + 8 * lane + 4) = tb;
+      const int ho = (lane >> 4) * HROW + 8 * (lane & 15);   // head lane / 16, channels 8 (lane % 16) ..
+      *reinterpret_cast<float4*>(W.s4 + ho) = sa; *reinterpret_cast<float4*>(W.s4 + ho + 4) = sbv;
+      *reinterpret_cast<float4*>(W.tp + ho) = ta; *reinterpret_cast<float4*>(W.tp + ho + 4) = tb;
     }
     {
       const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
@@ -140,52 +182,48 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
       }
     }
     // ---- prefetch chunk 0 (vb bytes, rope rows, kc rows of tiles 0 / 1)
-    uint4 vbn0 = *reinterpret_cast<const uint4*>(sb + VB_O + 32 * lane);
-    uint4 vbn1 = *reinterpret_cast<const uint4*>(sb + VB_O + 32 * lane + 16);
-    uint4 csn[4];
+    u4v vbn0 = *reinterpret_cast<const u4v*>(sb + VB_O + 32 * lane);
+    u4v vbn1 = *reinterpret_cast<const u4v*>(sb + VB_O + 32 * lane + 16);
+    u4v csn[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const uint4*>(csb + 256 * u + 4 * lane);
-    const uint8_t* kcb = sb + KC_O + g * 32;
-    uint4 kn[2][2];
+    for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const u4v*>(csb + 256 * u + 4 * lane);
+    const uint8_t* kcb = sb + KC_O + kofs;
+    uint2 kn[2][4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint8_t* p = kcb + (int64_t)(16 * u + n) * 128;
-      kn[u][0] = *reinterpret_cast<const uint4*>(p);
-      kn[u][1] = *reinterpret_cast<const uint4*>(p + 16);
-    }
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) kn[u][tg] = *reinterpret_cast<const uint2*>(kcb + (16 * u + tg) * 128);
     __builtin_amdgcn_wave_barrier();
 
     // ---- weights of this sub-block (B operands), scaled by `scale` so the accumulator is in log2 units.
-    // Lanes whose row n is not in head g (block-diagonal part) multiply by zero instead of branching.
-    const float actf = (hn == g) ? 1.f : 0.f;
-    const float* s4g = W.s4 + g * 128;
-    const float* s4n = W.s4 + hn * 128;
-    const float* tpn = W.tp + hn * 128;
+    // Rope / nope MFMAs: lane (g, n) holds the weights of query row n (head hn's scales) for channels 8 g .. 8 g + 7:
+    // block r < 4 = channels 8 g + 2 r, + 1 (4 rope features each), nope block p = channels 8 g + 4 p .. + 3.
     const float* qn = L.q[n];
-    h8 wr[16], wnp[8], wt[2];
+    const float* sh = W.s4 + hn * HROW;
+    const float* tpn = W.tp + hn * HROW;
+    h8 wr[4], wnp[2], wt[2];
+    {
+      float q0[8], q1[8], q2[8], q3[8], s0[8], s1[8], s2[8], s3[8];
+      auto ld8 = [](const float* p, float* o) {
+        const float4 x = *reinterpret_cast<const float4*>(p), y = *reinterpret_cast<const float4*>(p + 4);
+        o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+      };
+      ld8(qn + 8 * g, q0); ld8(qn + 32 + 8 * g, q1); ld8(qn + 64 + 8 * g, q2); ld8(qn + 96 + 8 * g, q3);
+      ld8(sh + 8 * g, s0); ld8(sh + 32 + 8 * g, s1); ld8(sh + 64 + 8 * g, s2); ld8(sh + 96 + 8 * g, s3);
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const float4 q0 = *reinterpret_cast<const float4*>(qn + 4 * d), q1 = *reinterpret_cast<const float4*>(qn + 32 + 4 * d);
-      const float4 q2 = *reinterpret_cast<const float4*>(qn + 64 + 4 * d), q3 = *reinterpret_cast<const float4*>(qn + 96 + 4 * d);
-      const float4 S0 = *reinterpret_cast<const float4*>(s4g + 4 * d), S1 = *reinterpret_cast<const float4*>(s4g + 32 + 4 * d);
-      const float4 S2 = *reinterpret_cast<const float4*>(s4g + 64 + 4 * d), S3 = *reinterpret_cast<const float4*>(s4g + 96 + 4 * d);
-      const float a0[4] = {q0.x, q0.y, q0.z, q0.w}, a1[4] = {q1.x, q1.y, q1.z, q1.w};
-      const float a2[4] = {q2.x, q2.y, q2.z, q2.w}, a3[4] = {q3.x, q3.y, q3.z, q3.w};
-      const float b0[4] = {S0.x * actf, S0.y * actf, S0.z * actf, S0.w * actf};
-      const float b1[4] = {S1.x * actf, S1.y * actf, S1.z * actf, S1.w * actf};
-      const float b2[4] = {S2.x * actf, S2.y * actf, S2.z * actf, S2.w * actf};
-      const float b3[4] = {S3.x * actf, S3.y * actf, S3.z * actf, S3.w * actf};
-      uint32_t hw[8], hnp[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        hw[2 * u] = pk2(a0[u] * b0[u], a2[u] * b0[u]);
-        hw[2 * u + 1] = pk2(a2[u] * b2[u], -a0[u] * b2[u]);
-        hnp[u] = pk2(a1[u] * b1[u], a3[u] * b3[u]);
+      for (int r = 0; r < 4; ++r) {
+        const int e0 = 2 * r, e1 = 2 * r + 1;
+        wr[r] = pack8(pk2(q0[e0] * s0[e0], q2[e0] * s0[e0]), pk2(q2[e0] * s2[e0], -q0[e0] * s2[e0]),
+                      pk2(q0[e1] * s0[e1], q2[e1] * s0[e1]), pk2(q2[e1] * s2[e1], -q0[e1] * s2[e1]));
       }
-      wr[2 * d] = pack8(hw[0], hw[1], hw[2], hw[3]);
-      wr[2 * d + 1] = pack8(hw[4], hw[5], hw[6], hw[7]);
-      wnp[d] = pack8(hnp[0], hnp[1], hnp[2], hnp[3]);
+#pragma unroll
+      for (int pq = 0; pq < 2; ++pq) {
+        const int e = 4 * pq;
+        wnp[pq] = pack8(pk2(q1[e] * s1[e], q3[e] * s3[e]), pk2(q1[e + 1] * s1[e + 1], q3[e + 1] * s3[e + 1]),
+                        pk2(q1[e + 2] * s1[e + 2], q3[e + 2] * s3[e + 2]), pk2(q1[e + 3] * s1[e + 3], q3[e + 3] * s3[e + 3]));
+      }
     }
+    // table part (all 16 rows, dense): lane (g, n) channels 16 kk + 4 g .. + 3, features (cos, sin)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int j0 = 16 * kk + 4 * g;
@@ -212,71 +250,64 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     c13 += __shfl_xor(c13, 16);
     c13 += __shfl_xor(c13, 32);
     c13 *= scale;
-    (void)s4n;
 
     // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
+#pragma unroll 2
     for (int c = 0; c < 8; ++c) {
-      const int cb = c & 1;
-      *reinterpret_cast<uint4*>(W.vb[cb] + 32 * lane) = vbn0;
-      *reinterpret_cast<uint4*>(W.vb[cb] + 32 * lane + 16) = vbn1;
+      const int cb = c & 1;   // constant in each of the two unrolled copies
+      // lane holds token lane / 2, pieces 2 (lane % 2) and 2 (lane % 2) + 1; rope dwords 256 u + 4 lane
+      W.vb[cb][vb_at(lane >> 1, 2 * (lane & 1))] = vbn0;
+      W.vb[cb][vb_at(lane >> 1, 2 * (lane & 1) + 1)] = vbn1;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(W.cs[cb] + 256 * u + 4 * lane) = csn[u];
-      uint4 kc[2][2];
+      for (int u = 0; u < 4; ++u) {
+        const int r = 8 * u + (lane >> 3);
+        W.cs[cb][cs_at(r, lane & 7)] = csn[u];
+      }
+      uint2 kc[2][4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) { kc[u][0] = kn[u][0]; kc[u][1] = kn[u][1]; }
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int tg = 0; tg < 4; ++tg) kc[u][tg] = kn[u][tg];
       if (c + 1 < 8) {   // prefetch the next chunk
         const uint8_t* vbp = sb + VB_O + (c + 1) * 32 * 64 + 32 * lane;
-        vbn0 = *reinterpret_cast<const uint4*>(vbp);
-        vbn1 = *reinterpret_cast<const uint4*>(vbp + 16);
+        vbn0 = *reinterpret_cast<const u4v*>(vbp);
+        vbn1 = *reinterpret_cast<const u4v*>(vbp + 16);
         const uint32_t* csp = csb + (c + 1) * 32 * 32;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const uint4*>(csp + 256 * u + 4 * lane);
+        for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const u4v*>(csp + 256 * u + 4 * lane);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint8_t* p = kcb + (int64_t)(32 * (c + 1) + 16 * u + n) * 128;
-          kn[u][0] = *reinterpret_cast<const uint4*>(p);
-          kn[u][1] = *reinterpret_cast<const uint4*>(p + 16);
-        }
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int tg = 0; tg < 4; ++tg)
+            kn[u][tg] = *reinterpret_cast<const uint2*>(kcb + (32 * (c + 1) + 16 * u + tg) * 128);
       }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-      f4 sacc2[2];
+      f4 sacc2[2];   // lane (g, n) register i: score of token 32 c + 16 u + 4 g + i, query row n
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {   // QK tile u: tokens 32 c + 16 u + (0..15)
-        const uint32_t* csrow = W.cs[cb] + (16 * u + n) * 32;
-        const uint32_t kw[8] = {kc[u][0].x, kc[u][0].y, kc[u][0].z, kc[u][0].w,
-                                kc[u][1].x, kc[u][1].y, kc[u][1].z, kc[u][1].w};
-        f4 sacc = {c13, c13, c13, c13};
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          const uint32_t x = kw[d];
-          const uint32_t Q0 = (x & 0x03030303u) | 0x3C3C3C3Cu;
-          const uint32_t Q2 = ((x >> 4) & 0x03030303u) | 0x3C3C3C3Cu;
-          const uint32_t Q1 = ((x >> 2) & 0x03030303u) | 0x3C3C3C3Cu;
-          const uint32_t Q3 = ((x >> 6) & 0x03030303u) | 0x3C3C3C3Cu;
-          const uint4 cs4 = *reinterpret_cast<const uint4*>(csrow + 4 * d);
-          const uint32_t csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-          uint32_t ga[4], gb[4], f13[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t sel = 0x0Cu | ((uint32_t)e << 8) | (0x0Cu << 16) | ((uint32_t)(4 + e) << 24);
-            const h2 F = as_h2(__builtin_amdgcn_perm(Q2, Q0, sel));
-            const h2 CS = as_h2(csv[e]);
-            ga[e] = hbits(CS * h2{F.x, F.x});
-            gb[e] = hbits(CS * h2{F.y, F.y});
-            f13[e] = __builtin_amdgcn_perm(Q3, Q1, sel);
-          }
-          sacc = mfma16(pack8(ga[0], gb[0], ga[1], gb[1]), wr[2 * d], sacc);
-          sacc = mfma16(pack8(ga[2], gb[2], ga[3], gb[3]), wr[2 * d + 1], sacc);
-          sacc = mfma16(pack8(f13[0], f13[1], f13[2], f13[3]), wnp[d], sacc);
-        }
+      for (int u = 0; u < 2; ++u) {
+        // table part: A row n = token 16 u + n
+        const int trow = 16 * u + n;
+        f4 tacc = {c13, c13, c13, c13};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const uint4 t4 = *reinterpret_cast<const uint4*>(csrow + 16 * kk + 4 * g);
-          sacc = mfma16(pack8(t4.x, t4.y, t4.z, t4.w), wt[kk], sacc);
+          const u4v t4 = W.cs[cb][cs_at(trow, 4 * kk + g)];
+          tacc = mfma16(__builtin_bit_cast(h8, t4), wt[kk], tacc);
         }
-        sacc2[u] = sacc;
+        // rope / nope part, 4 token groups: A row n = (token 16 u + 4 (n / 4) + tg, head n % 4); the result for query
+        // row n sits in output register n / 4 (the output rows of other heads are discarded)
+#pragma unroll
+        for (int tg = 0; tg < 4; ++tg) {
+          const int tok = 16 * u + 4 * (n >> 2) + tg;
+          const u4v cA = W.cs[cb][cs_at(tok, 2 * g)];
+          const u4v cB = W.cs[cb][cs_at(tok, 2 * g + 1)];
+          f4 a = {0.f, 0.f, 0.f, 0.f};
+          a = rope_nope(kc[u][tg].x, cA, wr[0], wr[1], wnp[0], a, KM, KC);
+          a = rope_nope(kc[u][tg].y, cB, wr[2], wr[3], wnp[1], a, KM, KC);
+          const float lo = (hn & 1) ? a[1] : a[0], hi = (hn & 1) ? a[3] : a[2];
+          sacc2[u][tg] = tacc[tg] + ((hn & 2) ? hi : lo);
+        }
       }
       // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
       float tmax = fmaxf(fmaxf(fmaxf(sacc2[0][0], sacc2[0][1]), fmaxf(sacc2[0][2], sacc2[0][3])),
@@ -285,7 +316,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
       if (__any(tmax > m + LAZY)) {
         const float mn = fmaxf(m, tmax);
-        const float al = exp2f(m - mn);
+        const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
         m = mn; lsum *= al; lvs *= al;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] *= al;
@@ -297,7 +328,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
         const int t0 = 32 * c + 16 * u + 4 * g;
         const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
         const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);
-        const float p0 = exp2f(sacc[0] - m), p1 = exp2f(sacc[1] - m), p2 = exp2f(sacc[2] - m), p3 = exp2f(sacc[3] - m);
+        const float p0 = __builtin_amdgcn_exp2f(sacc[0] - m), p1 = __builtin_amdgcn_exp2f(sacc[1] - m);
+        const float p2 = __builtin_amdgcn_exp2f(sacc[2] - m), p3 = __builtin_amdgcn_exp2f(sacc[3] - m);
         lsum += (p0 + p1) + (p2 + p3);
         lvs += (p0 * vl4.x + p1 * vl4.y) + (p2 * vl4.z + p3 * vl4.w);
         const h2 w01 = {(_Float16)(p0 * vs4.x), (_Float16)(p1 * vs4.y)};
@@ -306,7 +338,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
         bpv[2 * u + 1] = hbits(w23);
       }
       // ---- PV: per head hh, plane i. Lane (g, jj = n): bytes jj of tokens 32 c + {4 g + (0..3), 16 + 4 g + (0..3)}
-      const uint8_t* vbc = W.vb[cb];
+      const uint8_t* vbc = reinterpret_cast<const uint8_t*>(W.vb[cb]);
 #pragma unroll
       for (int hh = 0; hh < 4; ++hh) {
         const bool mine = (hn == hh);
@@ -315,7 +347,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int ta = 16 * (v >> 1) + 4 * g + 2 * (v & 1);
-          D[v] = (uint32_t)vbc[ta * 64 + hh * 16 + n] | ((uint32_t)vbc[(ta + 1) * 64 + hh * 16 + n] << 16);
+          D[v] = (uint32_t)vbc[16 * vb_at(ta, hh) + n] | ((uint32_t)vbc[16 * vb_at(ta + 1, hh) + n] << 16);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
