@@ -65,8 +65,6 @@ constexpr int QWAVES = 4;
 // 16 different rows at the same column, fall into distinct banks; the vb chunk is XOR-swizzled instead (below).
 constexpr int QROW = 132, HROW = 132, VROW = 272, CSP = 9;
 struct QWaveLds {
-  float s4[4 * HROW];         // 4 * scale * ksc [head][channel] of the current sub-block
-  float tp[4 * HROW];         // klo - 4 * ksc  [head][channel]
   float vs[2][VROW];          // decoded vsc per (head group, token)
   float vl[2][VROW];          // decoded vlo
   u4v vb[2][32 * 4];          // vb bytes of a 32-token chunk (double buffer), 16-byte pieces placed by vb_at
@@ -76,6 +74,11 @@ struct QLds {
   float q[16][QROW];
   QWaveLds wv[QWAVES];
 };
+// Per-sub-block scale staging, 4 * scale * ksc and klo - 4 * ksc as [head][channel] floats, lives in the wave's second
+// rope buffer: it is read only while the weights are built, before chunk 1 (the first user of that buffer) is stored,
+// and a wave's LDS instructions execute in order. This keeps a workgroup under 80 KB (two per CU).
+constexpr int SCALE_FLOATS = 8 * HROW;
+static_assert(SCALE_FLOATS * 4 <= (int)sizeof(u4v) * 32 * CSP, "scale staging must fit one rope buffer");
 struct QFinLds {              // end-of-split merge of the 4 waves (reuses the LDS)
   float m[QWAVES][16], l[QWAVES][16], lv[QWAVES][16];
   float acc[QWAVES][16][QROW];
@@ -126,6 +129,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
+  float* const s4w = reinterpret_cast<float*>(W.cs[1]);   // scale staging (see SCALE_FLOATS)
+  float* const tpw = s4w + 4 * HROW;
   // kc bytes a lane reads for token group tg of a 16-token tile: token 4 (n / 4) + tg, head n % 4, channels 8 g .. + 7
   const int kofs = (n >> 2) * 512 + (n & 3) * 32 + 8 * g;
   uint32_t KM, KC;   // code mask and fp16 exponent bytes, opaque VGPR values (see rope_nope)
@@ -165,8 +170,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
       sa = make_float4(sv[0], sv[1], sv[2], sv[3]); sbv = make_float4(sv[4], sv[5], sv[6], sv[7]);
       ta = make_float4(tv[0], tv[1], tv[2], tv[3]); tb = make_float4(tv[4], tv[5], tv[6], tv[7]);
       const int ho = (lane >> 4) * HROW + 8 * (lane & 15);   // head lane / 16, channels 8 (lane % 16) ..
-      *reinterpret_cast<float4*>(W.s4 + ho) = sa; *reinterpret_cast<float4*>(W.s4 + ho + 4) = sbv;
-      *reinterpret_cast<float4*>(W.tp + ho) = ta; *reinterpret_cast<float4*>(W.tp + ho + 4) = tb;
+      *reinterpret_cast<float4*>(s4w + ho) = sa; *reinterpret_cast<float4*>(s4w + ho + 4) = sbv;
+      *reinterpret_cast<float4*>(tpw + ho) = ta; *reinterpret_cast<float4*>(tpw + ho + 4) = tb;
     }
     {
       const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
@@ -199,8 +204,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     // Rope / nope MFMAs: lane (g, n) holds the weights of query row n (head hn's scales) for channels 8 g .. 8 g + 7:
     // block r < 4 = channels 8 g + 2 r, + 1 (4 rope features each), nope block p = channels 8 g + 4 p .. + 3.
     const float* qn = L.q[n];
-    const float* sh = W.s4 + hn * HROW;
-    const float* tpn = W.tp + hn * HROW;
+    const float* sh = s4w + hn * HROW;
+    const float* tpn = tpw + hn * HROW;
     h8 wr[4], wnp[2], wt[2];
     {
       float q0[8], q1[8], q2[8], q3[8], s0[8], s1[8], s2[8], s3[8];
@@ -250,6 +255,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     c13 += __shfl_xor(c13, 16);
     c13 += __shfl_xor(c13, 32);
     c13 *= scale;
+    asm volatile("" ::: "memory");   // the scale staging reads above stay before the chunk stores below
 
     // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
 #pragma unroll 2
