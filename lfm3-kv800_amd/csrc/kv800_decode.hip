@@ -400,17 +400,24 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------- exact tail + sinks (SIMT)
+constexpr int XW = 8;                  // waves per exact-tail workgroup (64 tokens per wave per pass)
 struct XLds {
   float4 q[128];                       // q rows r = 0..3 of this head at dim d
-  float m[4][4], l[4][4];              // per wave, per row
-  float acc[4][4][128];                // per wave, row, dim
+  float4 p[XW][64];                    // per wave: softmax weights of rows 0..3 for the chunk's 64 tokens
+  const uint16_t* vrow[XW][64];        // per wave: V row of each token of the chunk (null: masked)
+  float m[XW][4], l[XW][4];            // per wave, per row
+  float acc[XW][4][128];               // per wave, row, dim
 };
 
-__global__ void __launch_bounds__(256)
+// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into split slot ns.
+// MERGE = true : instead merges it with the ns quantized partials of those rows (written before on the same stream)
+//                and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
+template <bool MERGE>
+__global__ void __launch_bounds__(64 * XW)
 decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
                     const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
-                    int nsink) {
+                    int nsink, uint16_t* __restrict__ out) {
   __shared__ XLds X;
   const int b = blockIdx.x >> 2, h = blockIdx.x & 3;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -449,7 +456,7 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
   };
 
   float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0}, acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  for (int c0 = 64 * w; c0 < T; c0 += 256) {
+  for (int c0 = 64 * w; c0 < T; c0 += 64 * XW) {
     asm volatile("" ::: "memory");   // keep the q reads below inside the loop (no 512-register hoist)
     const int i = c0 + lane;
     int64_t ko = -1, vo = -1;
@@ -457,17 +464,32 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
     if (i < T) rows(i, ko, vo, pos);
     const bool valid = (i < T) && ko >= 0 && pos < rope_rows;
     const uint16_t* Kb = (i < cnt) ? P.sk : P.epool;
+    // V rows of the chunk's 64 tokens, exchanged through the wave's LDS slots; every lane then requests its two dims of
+    // all 64 rows at once, so these loads overlap the QK work below (masked tokens read row 0 of the exact pool and
+    // are zeroed by vmask)
+    const bool vok = valid && vo >= 0;
+    const uint64_t vmask = __ballot(vok);
+    X.vrow[w][lane] = vok ? ((i < cnt) ? P.sv : P.epool) + vo : P.epool;
+    __builtin_amdgcn_wave_barrier();
+    uint32_t vv[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) vv[j] = *reinterpret_cast<const uint32_t*>(X.vrow[w][j] + 2 * lane);
     float sc[4] = {0.f, 0.f, 0.f, 0.f};
     if (valid) {
+      // the token's whole K row and rope row are requested before any of it is used
       const uint16_t* kr = Kb + ko;
+      u4v kw[16], cw[4], sw[4];
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const uint4 w0 = *reinterpret_cast<const uint4*>(kr + 8 * gq);
-        const uint4 w1 = *reinterpret_cast<const uint4*>(kr + 32 + 8 * gq);
-        const uint4 w2 = *reinterpret_cast<const uint4*>(kr + 64 + 8 * gq);
-        const uint4 w3 = *reinterpret_cast<const uint4*>(kr + 96 + 8 * gq);
-        const uint4 c4 = *reinterpret_cast<const uint4*>(cos_t + (int64_t)pos * 32 + 8 * gq);
-        const uint4 s4 = *reinterpret_cast<const uint4*>(sin_t + (int64_t)pos * 32 + 8 * gq);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) kw[4 * gq + qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8 * gq);
+        cw[gq] = *reinterpret_cast<const u4v*>(cos_t + (int64_t)pos * 32 + 8 * gq);
+        sw[gq] = *reinterpret_cast<const u4v*>(sin_t + (int64_t)pos * 32 + 8 * gq);
+      }
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const u4v w0 = kw[4 * gq], w1 = kw[4 * gq + 1], w2 = kw[4 * gq + 2], w3 = kw[4 * gq + 3];
+        const u4v c4 = cw[gq], s4 = sw[gq];
         const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
         const uint32_t a2[4] = {w2.x, w2.y, w2.z, w2.w}, a3[4] = {w3.x, w3.y, w3.z, w3.w};
         const uint32_t cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
@@ -503,20 +525,20 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
       lsum[r] = lsum[r] * al + p[r];
       acc[r][0] *= al; acc[r][1] *= al;
     }
-    // PV: lane owns dims 2 lane, 2 lane + 1; walk the chunk's tokens
-    const int cntc = min(64, T - c0);
-    for (int tt = 0; tt < cntc; ++tt) {
-      const float p0 = __shfl(p[0], tt), p1 = __shfl(p[1], tt), p2 = __shfl(p[2], tt), p3 = __shfl(p[3], tt);
-      const int64_t vrow = __shfl(vo, tt);
-      if (vrow < 0) continue;   // uniform: masked token
-      const uint16_t* Vb = (c0 + tt < cnt) ? P.sv : P.epool;
-      const uint32_t vv = *reinterpret_cast<const uint32_t*>(Vb + vrow + 2 * lane);
-      const float v0 = bf2f_lo(vv), v1 = bf2f_hi(vv);
-      acc[0][0] += p0 * v0; acc[0][1] += p0 * v1;
-      acc[1][0] += p1 * v0; acc[1][1] += p1 * v1;
-      acc[2][0] += p2 * v0; acc[2][1] += p2 * v1;
-      acc[3][0] += p3 * v0; acc[3][1] += p3 * v1;
+    // PV: lane owns dims 2 lane, 2 lane + 1; the chunk's weights are read back from LDS as broadcasts
+    X.p[w][lane] = make_float4(p[0], p[1], p[2], p[3]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const float4 pp = X.p[w][j];   // zero for masked tokens and tokens past the chunk
+      const uint32_t vj = ((vmask >> j) & 1) ? vv[j] : 0u;
+      const float v0 = bf2f_lo(vj), v1 = bf2f_hi(vj);
+      acc[0][0] += pp.x * v0; acc[0][1] += pp.x * v1;
+      acc[1][0] += pp.y * v0; acc[1][1] += pp.y * v1;
+      acc[2][0] += pp.z * v0; acc[2][1] += pp.z * v1;
+      acc[3][0] += pp.w * v0; acc[3][1] += pp.w * v1;
     }
+    __builtin_amdgcn_wave_barrier();
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -528,23 +550,78 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
     X.acc[w][r][2 * lane + 1] = acc[r][1];
   }
   __syncthreads();
+  if (tid >= 256) return;
   // thread -> (row r = tid / 64, dims 2 (tid % 64), +1)
   const int r = tid >> 6, dd = 2 * (tid & 63);
   float M = NEG_BIG;
 #pragma unroll
-  for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, X.m[ww][r]);
+  for (int ww = 0; ww < XW; ++ww) M = fmaxf(M, X.m[ww][r]);
   float Ls = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-  for (int ww = 0; ww < 4; ++ww) {
+  for (int ww = 0; ww < XW; ++ww) {
     const float sc = exp2f(X.m[ww][r] - M);
     Ls += sc * X.l[ww][r];
     o0 += sc * X.acc[ww][r][dd];
     o1 += sc * X.acc[ww][r][dd + 1];
   }
-  const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
-  if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
-  ao[row * 128 + dd] = o0;
-  ao[row * 128 + dd + 1] = o1;
+  if constexpr (!MERGE) {
+    const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
+    if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
+    ao[row * 128 + dd] = o0;
+    ao[row * 128 + dd + 1] = o1;
+  } else {
+    // wave r = row 4 h + r; lane owns dims dd, dd + 1 (same combination as decode_merge_kernel)
+    const int64_t rq = (int64_t)b * (ns + 1) * 16 + h * 4 + r;   // row of split 0; split s adds 16 s
+    // splits are visited 8 at a time with all of their loads issued together
+    float Mq = M;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mv[k] = (s0 + k < ns) ? mo[rq + 16 * (s0 + k)] : NEG_BIG;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) Mq = fmaxf(Mq, mv[k]);
+    }
+    const float we = exp2f(M - Mq);
+    float L = Ls * we, x0 = 0.f, x1 = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8], lv[8];
+      float2 av[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const bool in = s0 + k < ns;
+        const int64_t row = rq + 16 * (in ? s0 + k : 0);
+        mv[k] = in ? mo[row] : NEG_BIG;
+        lv[k] = lo_out[row];
+        av[k] = *reinterpret_cast<const float2*>(ao + row * 128 + dd);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float wq = exp2f(mv[k] - Mq);   // 0 for the padding entries
+        L += wq * lv[k];
+        x0 += wq * av[k].x;
+        x1 += wq * av[k].y;
+      }
+    }
+    // y = H x over the 128 dims: bit 0 of the dim in-lane, bits 1..6 across the wave's lanes
+    {
+      const float a = x0, c = x1;
+      x0 = a + c;
+      x1 = a - c;
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int msk = 1 << k;
+      const float p0 = __shfl_xor(x0, msk), p1 = __shfl_xor(x1, msk);
+      x0 = (lane & msk) ? p0 - x0 : x0 + p0;
+      x1 = (lane & msk) ? p1 - x1 : x1 + p1;
+    }
+    const float hn = __uint_as_float(0x3DB504F3u);
+    float y0 = (ns > 0 ? x0 * hn : 0.f) + o0 * we;
+    float y1 = (ns > 0 ? x1 * hn : 0.f) + o1 * we;
+    y0 = L > 0.f ? y0 / L : 0.f;
+    y1 = L > 0.f ? y1 / L : 0.f;
+    *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
+  }
 }
 
 // ---------------------------------------------------------------- split merge
@@ -553,23 +630,46 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
                     uint16_t* __restrict__ out) {
   const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
   const int S = ns + 1;
+  const int64_t r0 = (int64_t)b * S * 16 + r;   // row of split 0; split s adds 16 s
   float M = NEG_BIG;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, mo[((int64_t)b * S + s) * 16 + r]);
+  for (int s0 = 0; s0 < S; s0 += 4) {   // 4 splits at a time, loads issued together
+    float mv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mv[k] = (s0 + k < S) ? mo[r0 + 16 * (s0 + k)] : NEG_BIG;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) M = fmaxf(M, mv[k]);
+  }
   float Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, xe[8];
-  for (int s = 0; s < S; ++s) {
-    const int64_t row = ((int64_t)b * S + s) * 16 + r;
+  for (int s0 = 0; s0 < ns; s0 += 4) {   // quantized splits
+    float mv[4], lv[4];
+    float4 a0[4], a1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool in = s0 + k < ns;
+      const int64_t row = r0 + 16 * (in ? s0 + k : 0);
+      mv[k] = in ? mo[row] : NEG_BIG;
+      lv[k] = lo[row];
+      a0[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
+      a1[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float wgt = exp2f(mv[k] - M);   // 0 for the padding entries
+      const float a[8] = {a0[k].x, a0[k].y, a0[k].z, a0[k].w, a1[k].x, a1[k].y, a1[k].z, a1[k].w};
+      Ls += wgt * lv[k];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
+    }
+  }
+  {   // exact split
+    const int64_t row = r0 + 16 * (int64_t)ns;
     const float wgt = exp2f(mo[row] - M);
     Ls += wgt * lo[row];
     const float4 a0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
     const float4 a1 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
     const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    if (s < ns) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
-    }
+    for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
   }
   if (ns > 0) {   // y = H x, d = 8 l16 + e: three in-lane stages, four across the 16-lane group
 #pragma unroll
@@ -604,6 +704,34 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// Validates the exact-tail arguments and launches decode_exact_kernel; with out != null the fused variant that also
+// merges the quantized splits and writes the bf16 rows.
+int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                 int64_t rope_rows, int64_t epool_elems, int64_t sink_elems, float* mo, float* lo, float* ao, int64_t B,
+                 int64_t ns, float scale, uint16_t* out, void* stream) {
+  KV800_REQUIRE(P && B >= 0 && ns >= 0, "decode_exact: bad arguments");
+  if (B == 0) return KV800_OK;
+  KV800_REQUIRE(q && cos_t && sin_t && mo && lo && ao && P->epool && P->eoff && P->N && P->NQ,
+                "decode_exact: null pointer");
+  KV800_REQUIRE(P->ebs > 0 && P->win >= 0, "decode_exact: ebs must be > 0");
+  KV800_REQUIRE(P->e_hs % 8 == 0 && P->e_ts % 8 == 0 && ((uintptr_t)P->epool % 16) == 0,
+                "decode_exact: exact strides must be multiples of 8 elements and the pool 16-byte aligned");
+  const int nsink = P->sk ? NSINK : 0;
+  KV800_REQUIRE(!nsink || (P->sv && P->skoff && P->svoff), "decode_exact: sinks need sv, skoff and svoff");
+  KV800_REQUIRE(B * 4 <= 0x7FFFFFFF, "decode_exact: grid too large");
+  KV800_REQUIRE(!out || ((uintptr_t)out % 4) == 0, "decode: out must be 4-byte aligned");
+  KV800_REQUIRE(epool_elems >= 128, "decode_exact: the exact pool must hold at least one 128-element row");
+  if (out)
+    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3((unsigned)(B * 4)), dim3(64 * XW), 0, (hipStream_t)stream, *P, q,
+                       cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
+  else
+    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3((unsigned)(B * 4)), dim3(64 * XW), 0, (hipStream_t)stream, *P,
+                       q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink,
+                       (uint16_t*)nullptr);
+  return check_launch(out ? "decode_exact_merge" : "decode_exact");
+}
+
 
 }  // namespace
 }  // namespace kv800
@@ -661,19 +789,7 @@ int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_
 int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t,
                                  const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream) {
-  KV800_REQUIRE(P && B >= 0 && ns >= 0, "decode_exact: bad arguments");
-  if (B == 0) return KV800_OK;
-  KV800_REQUIRE(q && cos_t && sin_t && mo && lo && ao && P->epool && P->eoff && P->N && P->NQ,
-                "decode_exact: null pointer");
-  KV800_REQUIRE(P->ebs > 0 && P->win >= 0, "decode_exact: ebs must be > 0");
-  KV800_REQUIRE(P->e_hs % 8 == 0 && P->e_ts % 8 == 0 && ((uintptr_t)P->epool % 16) == 0,
-                "decode_exact: exact strides must be multiples of 8 elements and the pool 16-byte aligned");
-  const int nsink = P->sk ? NSINK : 0;
-  KV800_REQUIRE(!nsink || (P->sv && P->skoff && P->svoff), "decode_exact: sinks need sv, skoff and svoff");
-  KV800_REQUIRE(B * 4 <= 0x7FFFFFFF, "decode_exact: grid too large");
-  hipLaunchKernelGGL(decode_exact_kernel, dim3((unsigned)(B * 4)), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
-                     sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink);
-  return check_launch("decode_exact");
+  return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, nullptr, stream);
 }
 
 int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
@@ -736,10 +852,8 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
                                            ao, B, ns, sp, scale, stream)) != KV800_OK)
       return rc;
   }
-  if ((rc = kv800_hip_decode_exact_sized(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns,
-                                         scale, stream)) != KV800_OK)
-    return rc;
-  return kv800_hip_decode_merge(mo, lo, ao, B, ns, out, stream);
+  // exact tail + sinks, fused with the split merge (one launch writes the bf16 rows)
+  return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, out, stream);
 }
 
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
