@@ -27,6 +27,20 @@ ALG_BYTES = QBYTES + XBYTES                         # the reference's accounting
 HBM_PEAK_GBS = 8000.0
 
 
+def measured_traffic():
+    """HBM bytes per decode_quant launch from the committed rocprofv3 counter summary: FETCH_SIZE + WRITE_SIZE, each
+    scaled by what the counter reads for a plain 1 GiB copy (rocprofv3 cannot run inside this process). None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_quant_c3_pmc.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
@@ -165,16 +179,17 @@ def main():
                                             ctypes.c_void_p(s.cuda_stream))
         assert rc == 0, L.kv800_hip_last_error()
 
+    # one event pair around each launch, so the average is the kernel's own duration (no dispatch gaps)
     with torch.cuda.stream(s):
         for i in range(a.warmup):
             quant(i)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
         for i in range(a.steps):
+            ev[i][0].record(s)
             quant(i)
-        e1.record(s)
-    e1.synchronize()
-    ms_quant = e0.elapsed_time(e1) / a.steps
+            ev[i][1].record(s)
+    ev[-1][1].synchronize()
+    ms_quant = sum(e0.elapsed_time(e1) for e0, e1 in ev) / a.steps
     torch.cuda.synchronize()
 
     out = kh.decode(layers[0], q, cos, sin)
@@ -202,7 +217,7 @@ def main():
                   "hbm_frac": round(layer_gbps / HBM_PEAK_GBS, 4), "decode_tok_s": round(B / (ms_step * 1e-3), 1)},
         "roofline": {"bound": "hbm", "kernel": "decode_quant_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel_ms": round(ms_quant, 5), "bytes_per_launch": QBYTES},
+                     "traffic": measured_traffic(), "kernel_ms": round(ms_quant, 5), "bytes_per_launch": QBYTES},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -88,7 +88,8 @@ int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_
 
 /* Sinks + exact tail. Replaces torch.ops.kv800.xdecode (kv800_sycl.sycl:528-542, Triton _xdec kv800.py:197-228):
  * positions [lo_e, N[b]) with lo_e = NQ[b] * 256 (window layers: max(lo_e, N - win)) and, when P->sk != NULL,
- * sinks at positions < min(4, lo_e, N) -> slot ns of mo / lo / ao. cos_t, sin_t: (>= max(N), 32) bf16. */
+ * sinks at positions < min(4, lo_e, N) -> slot ns of mo / lo / ao. cos_t, sin_t: (>= max(N), 32) bf16.
+ * The exact pool must hold at least one 128-element row (masked lanes read row 0 and discard it). */
 int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
                            float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream);
 
@@ -104,8 +105,9 @@ int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb);
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows);
 
 /* Fused decode of one layer. Replaces kv800.decode's backend body (kv800.py:352-383): plan, [rope table],
- * decode_quant, decode_exact, decode_merge, all on `stream`. cs16 may be NULL (then it is built in the
- * workspace from cos_t / sin_t for the nqmax * 256 rows the quantized kernel reads). spb <= 0: kv800_hip_plan. */
+ * decode_quant, then the exact tail fused with the split merge (one launch), all on `stream`. cs16 may be NULL
+ * (then it is built in the workspace from cos_t / sin_t for the nqmax * 256 rows the quantized kernel reads).
+ * spb <= 0: kv800_hip_plan. */
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
                      const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream);

@@ -8,21 +8,24 @@
 //
 // Kernels
 //   rope_table_kernel   bf16 (cos, sin) tables -> packed fp16 pairs (exact for every table value above 2^-17).
-//   decode_quant_kernel one workgroup (4 waves) per (row b, split s); each wave owns whole 256-token sub-blocks and
-//                       reads them with 16-byte coalesced loads of all 4 heads at once.
-//     QK on MFMA f32_16x16x32_f16: M = 16 tokens, N = the 16 query rows, K = per-token features of head g supplied
-//       by lane group g (block-diagonal weights). With f = 1 + code / 4 (exact in fp16 from the code bits) and
-//       per-channel k = 4 ksc f + (klo - 4 ksc), RoPE is moved onto exact fp16 features:
+//   decode_quant_kernel one workgroup (4 waves) per (row b, split s); each wave owns whole 256-token sub-blocks,
+//                       32 tokens (one chunk) at a time, the next chunk's bytes prefetched into registers.
+//     QK on MFMA f32_16x16x32_f16, N = the 16 query rows. With f = 1 + code / 4 (exact in fp16 from the code bits)
+//       and per-channel k = 4 ksc f + (klo - 4 ksc), RoPE is moved onto exact fp16 features:
 //         rope dims: (cos f0, sin f0, cos f2, sin f2) x weights (q0 S0, q2 S0, q2 S2, -q0 S2), S = 4 ksc scale
 //         nope dims: (f1, f3)                         x weights (q1 S1, q3 S3)
-//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2) (all 16 rows)
-//       and the per-row constant sum(q1 T1 + q3 T3) initialises the accumulator. Weights are rebuilt per sub-block.
+//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2)
+//       and the per-row constant sum(q1 T1 + q3 T3) initialises the accumulator.
+//       Rope / nope MFMAs take M = 16 (token, head) rows -- 4 tokens x the 4 KV heads -- so every weight register is
+//       dense (query row n applies head n / 4's scales) and only the output rows of head n / 4 are kept; the klo part
+//       takes M = 16 tokens (head-independent features, weights from head n / 4). Weights are rebuilt per sub-block.
 //     PV on the same MFMA: M = 16 dims (one bit plane), N = the 16 rows, K = 32 tokens. The bit feature is the
 //       fp16 subnormal bit 2^(i - 24) (one AND per two tokens; MFMA keeps fp16 subnormal inputs exactly), the
-//       weights fp16(p vsc); plane i is scaled back by 2^(24 - i) at the end.
+//       weights fp16(p vsc) masked to the head's rows; plane i is scaled back by 2^(24 - i) at the end.
 //     Softmax with a lazy running max (rescale only when a tile max exceeds it by more than 8 log2 units).
-//   decode_exact_kernel one workgroup per (row b, KV head h): sinks + exact positions, SIMT fp32.
-//   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT.
+//   decode_exact_kernel one workgroup (8 waves, 64 tokens per wave per pass) per (row b, KV head h): sinks + exact
+//                       positions, SIMT fp32; the fused variant also merges the quantized splits of its 4 rows.
+//   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT (staged path).
 #include <math.h>
 
 #include "kv800_common.h"
