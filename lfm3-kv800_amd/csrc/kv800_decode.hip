@@ -10,11 +10,11 @@
 //   rope_table_kernel   bf16 (cos, sin) tables -> packed fp16 pairs (exact for every table value above 2^-17).
 //   decode_quant_kernel one workgroup (4 waves) per (row b, split s); each wave owns whole 256-token sub-blocks,
 //                       32 tokens (one chunk) at a time, the next chunk's bytes prefetched into registers.
-//     QK on MFMA f32_16x16x32_f16, N = the 16 query rows. With f = 1 + code / 4 (exact in fp16 from the code bits)
-//       and per-channel k = 4 ksc f + (klo - 4 ksc), RoPE is moved onto exact fp16 features:
-//         rope dims: (cos f0, sin f0, cos f2, sin f2) x weights (q0 S0, q2 S0, q2 S2, -q0 S2), S = 4 ksc scale
-//         nope dims: (f1, f3)                         x weights (q1 S1, q3 S3)
-//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2)
+//     QK on MFMA f32_16x16x32_f16, N = the 16 query rows. With the 2-bit codes c as exact fp16 features (one
+//       e2m1 -> fp16 conversion per byte) and per-channel k = klo + ksc c, RoPE is moved onto exact fp16 features:
+//         rope dims: (cos c0, sin c0, cos c2, sin c2) x weights (q0 S0, q2 S0, q2 S2, -q0 S2), S = ksc scale
+//         nope dims: (c1, c3)                         x weights (q1 S1, q3 S3)
+//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2), T = klo
 //       and the per-row constant sum(q1 T1 + q3 T3) initialises the accumulator.
 //       Rope / nope MFMAs take M = 16 (token, head) rows -- 4 tokens x the 4 KV heads -- so every weight register is
 //       dense (query row n applies head n / 4's scales) and only the output rows of head n / 4 are kept; the klo part
@@ -54,6 +54,14 @@ __device__ __forceinline__ uint32_t pk2(float a, float b) {   // two floats -> p
   return hbits(v);
 }
 
+// Four fp8 e4m3fn bytes of w -> floats (byte i -> o[i]) with the hardware conversion: gfx950 converts the OCP e4m3
+// format, the same as torch's float8_e4m3fn, exactly; the NaN bytes 0x7F / 0xFF give NaN as torch's .float() does
+// (kv800.py:84-91; the quantizer writes them only for scales beyond +-464).
+__device__ __forceinline__ void f8x4(uint32_t w, float* o) {
+  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  o[0] = a[0]; o[1] = a[1]; o[2] = b[0]; o[3] = b[1];
+}
+
 // ---------------------------------------------------------------- rope table
 __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int64_t n,
                                   uint32_t* __restrict__ cs16) {
@@ -77,7 +85,7 @@ struct QLds {
   float q[16][QROW];
   QWaveLds wv[QWAVES];
 };
-// Per-sub-block scale staging, 4 * scale * ksc and klo - 4 * ksc as [head][channel] floats, lives in the wave's second
+// Per-sub-block scale staging, scale * ksc and klo as [head][channel] floats, lives in the wave's second
 // rope buffer: it is read only while the weights are built, before chunk 1 (the first user of that buffer) is stored,
 // and a wave's LDS instructions execute in order. This keeps a workgroup under 80 KB (two per CU).
 constexpr int SCALE_FLOATS = 8 * HROW;
@@ -94,26 +102,27 @@ __device__ __forceinline__ int vb_at(int t, int k) { return 4 * t + (k ^ ((t >> 
 // (4 tokens x 4 lane groups) cover all 16 bank quads
 __device__ __forceinline__ int cs_at(int r, int p) { return r * CSP + (p ^ ((r >> 2) & 1)); }
 
-// rope + nope features of one kc dword (channels e = 0..3 of the lane's 8, cos / sin in cs4) against weight blocks
-// w0 (channels 0, 1), w1 (channels 2, 3) and wn (nope, channels 0..3). f = 1 + code / 4 is built exactly in fp16 by
-// placing the code under the exponent of 1.0 (0x3C | code in the high byte).
-// km = 0x03030303 and kc = 0x3C3C3C3C arrive in VGPRs so that each (x & km) | kc is a single v_and_or_b32 (a VALU
-// instruction may read only one literal or SGPR).
-__device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn, f4 a, uint32_t km, uint32_t kc) {
-  const uint32_t Q0 = (x & km) | kc;
-  const uint32_t Q2 = ((x >> 4) & km) | kc;
-  const uint32_t Q1 = ((x >> 2) & km) | kc;
-  const uint32_t Q3 = ((x >> 6) & km) | kc;
+// rope + nope features of one kc dword x (channels e = 0..3 of the lane's 8, one byte each holding the codes
+// c0 | c1 << 2 | c2 << 4 | c3 << 6 of dims j, j + 32, j + 64, j + 96; cos / sin of channel e in cs4) against weight
+// blocks w0 (channels 0, 1), w1 (channels 2, 3) and wn (nope, channels 0..3). A byte masked to bits 0-1 | 4-5 is two
+// e2m1 nibbles whose values are c0 / 2 and c2 / 2; v_cvt_scalef32_pk_f16_fp4 with scale 2 turns it into the exact
+// fp16 pair (c0, c2) in one instruction (its scale applies the exponent only), and bits 2-3 | 6-7 shifted down give
+// (c1, c3) the same way.
+template <int E>
+__device__ __forceinline__ h2 codes2(uint32_t m) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 2.0f, E); }
+
+__device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn, f4 a) {
+  const uint32_t m02 = x & 0x33333333u, m13 = (x >> 2) & 0x33333333u;
+  const h2 F[4] = {codes2<0>(m02), codes2<1>(m02), codes2<2>(m02), codes2<3>(m02)};   // (c0, c2) of channel e
+  const uint32_t f13[4] = {hbits(codes2<0>(m13)), hbits(codes2<1>(m13)), hbits(codes2<2>(m13)),
+                           hbits(codes2<3>(m13))};                                  // (c1, c3) of channel e
   const uint32_t csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-  uint32_t ga[4], gb[4], f13[4];
+  uint32_t ga[4], gb[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t sel = 0x0Cu | ((uint32_t)e << 8) | (0x0Cu << 16) | ((uint32_t)(4 + e) << 24);
-    const h2 F = as_h2(__builtin_amdgcn_perm(Q2, Q0, sel));   // (f0, f2) of channel e
     const h2 CS = as_h2(csv[e]);
-    ga[e] = hbits(CS * h2{F.x, F.x});
-    gb[e] = hbits(CS * h2{F.y, F.y});
-    f13[e] = __builtin_amdgcn_perm(Q3, Q1, sel);             // (f1, f3) of channel e
+    ga[e] = hbits(CS * h2{F[e].x, F[e].x});   // (cos c0, sin c0)
+    gb[e] = hbits(CS * h2{F[e].y, F[e].y});   // (cos c2, sin c2)
   }
   a = mfma16(pack8(ga[0], gb[0], ga[1], gb[1]), w0, a);
   a = mfma16(pack8(ga[2], gb[2], ga[3], gb[3]), w1, a);
@@ -136,9 +145,6 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   float* const tpw = s4w + 4 * HROW;
   // kc bytes a lane reads for token group tg of a 16-token tile: token 4 (n / 4) + tg, head n % 4, channels 8 g .. + 7
   const int kofs = (n >> 2) * 512 + (n & 3) * 32 + 8 * g;
-  uint32_t KM, KC;   // code mask and fp16 exponent bytes, opaque VGPR values (see rope_nope)
-  asm volatile("v_mov_b32 %0, 0x03030303" : "=v"(KM));
-  asm volatile("v_mov_b32 %0, 0x3c3c3c3c" : "=v"(KC));
 
   for (int i = tid; i < 16 * 128; i += 256) L.q[i >> 7][i & 127] = bf2f(q[(int64_t)b * 2048 + i]);   // padded rows
   __syncthreads();
@@ -157,37 +163,31 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     const uint8_t* sb = qpool + base;
     const uint32_t* csb = cs16 + (int64_t)jb * BLK * 32;
 
-    // ---- stage per-sub-block scales as floats: S = 4 scale ksc, T = klo - 4 ksc per (head, channel); vlo / vsc
+    // ---- stage per-sub-block scales as floats: S = scale ksc, T = klo per (head, channel); vlo / vsc
     {
       const uint2 lo2 = *reinterpret_cast<const uint2*>(sb + KLO_O + 8 * lane);   // channels 8 lane .. 8 lane + 7
       const uint2 sc2 = *reinterpret_cast<const uint2*>(sb + KSC_O + 8 * lane);
-      float4 sa, sbv, ta, tb;
-      float sv[8], tv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float ksc = f8d(((e < 4 ? sc2.x : sc2.y) >> (8 * (e & 3))) & 0xFFu);
-        const float klo = f8d(((e < 4 ? lo2.x : lo2.y) >> (8 * (e & 3))) & 0xFFu);
-        sv[e] = 4.f * scale * ksc;
-        tv[e] = klo - 4.f * ksc;
-      }
-      sa = make_float4(sv[0], sv[1], sv[2], sv[3]); sbv = make_float4(sv[4], sv[5], sv[6], sv[7]);
-      ta = make_float4(tv[0], tv[1], tv[2], tv[3]); tb = make_float4(tv[4], tv[5], tv[6], tv[7]);
+      float ksc[8], klo[8];
+      f8x4(sc2.x, ksc); f8x4(sc2.y, ksc + 4);
+      f8x4(lo2.x, klo); f8x4(lo2.y, klo + 4);
       const int ho = (lane >> 4) * HROW + 8 * (lane & 15);   // head lane / 16, channels 8 (lane % 16) ..
-      *reinterpret_cast<float4*>(s4w + ho) = sa; *reinterpret_cast<float4*>(s4w + ho + 4) = sbv;
-      *reinterpret_cast<float4*>(tpw + ho) = ta; *reinterpret_cast<float4*>(tpw + ho + 4) = tb;
+      // k = klo + ksc * code: the weights act on the integer code features
+      *reinterpret_cast<float4*>(s4w + ho) = make_float4(scale * ksc[0], scale * ksc[1], scale * ksc[2], scale * ksc[3]);
+      *reinterpret_cast<float4*>(s4w + ho + 4) = make_float4(scale * ksc[4], scale * ksc[5], scale * ksc[6], scale * ksc[7]);
+      *reinterpret_cast<float4*>(tpw + ho) = make_float4(klo[0], klo[1], klo[2], klo[3]);
+      *reinterpret_cast<float4*>(tpw + ho + 4) = make_float4(klo[4], klo[5], klo[6], klo[7]);
     }
     {
       const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
       const uint2 vs2 = *reinterpret_cast<const uint2*>(sb + VSC_O + 8 * lane);
-      // bytes 8 lane + e -> token (8 lane + e) / 2, group (8 lane + e) & 1
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lb = ((e < 4 ? vl2.x : vl2.y) >> (8 * (e & 3))) & 0xFFu;
-        const uint32_t sbt = ((e < 4 ? vs2.x : vs2.y) >> (8 * (e & 3))) & 0xFFu;
-        const int t = 4 * lane + (e >> 1), gg = e & 1;
-        W.vl[gg][t] = f8d(lb);
-        W.vs[gg][t] = f8d(sbt);
-      }
+      // byte 8 lane + e -> token 4 lane + e / 2, head group e & 1
+      float vl[8], vs[8];
+      f8x4(vl2.x, vl); f8x4(vl2.y, vl + 4);
+      f8x4(vs2.x, vs); f8x4(vs2.y, vs + 4);
+      *reinterpret_cast<float4*>(&W.vl[0][4 * lane]) = make_float4(vl[0], vl[2], vl[4], vl[6]);
+      *reinterpret_cast<float4*>(&W.vl[1][4 * lane]) = make_float4(vl[1], vl[3], vl[5], vl[7]);
+      *reinterpret_cast<float4*>(&W.vs[0][4 * lane]) = make_float4(vs[0], vs[2], vs[4], vs[6]);
+      *reinterpret_cast<float4*>(&W.vs[1][4 * lane]) = make_float4(vs[1], vs[3], vs[5], vs[7]);
     }
     // ---- prefetch chunk 0 (vb bytes, rope rows, kc rows of tiles 0 / 1)
     u4v vbn0 = *reinterpret_cast<const u4v*>(sb + VB_O + 32 * lane);
@@ -312,8 +312,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
           const u4v cA = W.cs[cb][cs_at(tok, 2 * g)];
           const u4v cB = W.cs[cb][cs_at(tok, 2 * g + 1)];
           f4 a = {0.f, 0.f, 0.f, 0.f};
-          a = rope_nope(kc[u][tg].x, cA, wr[0], wr[1], wnp[0], a, KM, KC);
-          a = rope_nope(kc[u][tg].y, cB, wr[2], wr[3], wnp[1], a, KM, KC);
+          a = rope_nope(kc[u][tg].x, cA, wr[0], wr[1], wnp[0], a);
+          a = rope_nope(kc[u][tg].y, cB, wr[2], wr[3], wnp[1], a);
           const float lo = (hn & 1) ? a[1] : a[0], hi = (hn & 1) ? a[3] : a[2];
           sacc2[u][tg] = tacc[tg] + ((hn & 2) ? hi : lo);
         }
