@@ -70,6 +70,244 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
   cs16[i] = pk2(bf2f(cos_t[i]), bf2f(sin_t[i]));
 }
 
+// ---------------------------------------------------------------- exact tail + sinks (SIMT)
+constexpr int XW = 8;                  // waves of the standalone exact-tail workgroup (64 tokens per wave per pass)
+template <int NW>
+struct XLdsT {
+  float4 q[128];                       // q rows r = 0..3 of this head at dim d
+  float4 p[NW][64];                    // per wave: softmax weights of rows 0..3 for the chunk's 64 tokens
+  const uint16_t* vrow[NW][64];        // per wave: V row of each token of the chunk (null: masked)
+  float m[NW][4], l[NW][4];            // per wave, per row
+  float acc[NW][4][128];               // per wave, row, dim
+};
+
+// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into split slot ns.
+// MERGE = true : instead merges it with the ns quantized partials of those rows (written before on the same stream)
+//                and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
+// Exact tail of (row b, KV head h) by a workgroup of NW waves (the standalone kernel, or the exact-tail workgroups of
+// the quantized-split grid).
+template <int NW, bool MERGE>
+__device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int h, const kv800_paged_t& P,
+                                           const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
+                                           const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems,
+                                           int64_t sink_elems, float* __restrict__ mo, float* __restrict__ lo_out,
+                                           float* __restrict__ ao, int ns, float scale, int nsink,
+                                           uint16_t* __restrict__ out) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  if (tid < 128) {
+    float4 a;
+    a.x = bf2f(q[((int64_t)b * 16 + h * 4 + 0) * 128 + tid]);
+    a.y = bf2f(q[((int64_t)b * 16 + h * 4 + 1) * 128 + tid]);
+    a.z = bf2f(q[((int64_t)b * 16 + h * 4 + 2) * 128 + tid]);
+    a.w = bf2f(q[((int64_t)b * 16 + h * 4 + 3) * 128 + tid]);
+    X.q[tid] = a;
+  }
+  __syncthreads();
+  const int n = P.N[b];
+  int lo_e = P.NQ[b] * BLK;
+  if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
+  lo_e = max(lo_e, 0);
+  const int cnt = (nsink > 0) ? max(0, min(min(nsink, lo_e), n)) : 0;
+  const int T = cnt + max(0, n - lo_e);
+  const int64_t* et = P.eoff + (int64_t)b * P.eoff_stride;
+
+  // element offset of token i's K row (sink or exact page) and of its V row; -1 if out of range
+  auto rows = [&](int i, int64_t& ko, int64_t& vo, int& pos) {
+    if (i < cnt) {
+      pos = i;
+      ko = P.skoff[b] + ((int64_t)i * 4 + h) * 128;
+      vo = P.svoff[b] + ((int64_t)i * 4 + h) * 128;
+      if (ko < 0 || vo < 0 || ko + 128 > sink_elems || vo + 128 > sink_elems) { ko = vo = -1; }
+    } else {
+      pos = lo_e + (i - cnt);
+      const int64_t pg = pos / P.ebs;
+      if (pg >= P.eoff_stride) { ko = vo = -1; return; }
+      ko = et[pg] + h * P.e_hs + (pos % P.ebs) * P.e_ts;
+      vo = ko + P.e_v;
+      if (ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) { ko = vo = -1; }
+    }
+  };
+
+  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0}, acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  for (int c0 = 64 * w; c0 < T; c0 += 64 * NW) {
+    asm volatile("" ::: "memory");   // keep the q reads below inside the loop (no 512-register hoist)
+    const int i = c0 + lane;
+    int64_t ko = -1, vo = -1;
+    int pos = 0;
+    if (i < T) rows(i, ko, vo, pos);
+    const bool valid = (i < T) && ko >= 0 && pos < rope_rows;
+    const uint16_t* Kb = (i < cnt) ? P.sk : P.epool;
+    // V rows of the chunk's 64 tokens, exchanged through the wave's LDS slots; every lane then requests its two dims of
+    // all 64 rows at once, so these loads overlap the QK work below (masked tokens read row 0 of the exact pool and
+    // are zeroed by vmask)
+    const bool vok = valid && vo >= 0;
+    const uint64_t vmask = __ballot(vok);
+    X.vrow[w][lane] = vok ? ((i < cnt) ? P.sv : P.epool) + vo : P.epool;
+    __builtin_amdgcn_wave_barrier();
+    uint32_t vv[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) vv[j] = *reinterpret_cast<const uint32_t*>(X.vrow[w][j] + 2 * lane);
+    float sc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+      // the token's whole K row and rope row are requested before any of it is used
+      const uint16_t* kr = Kb + ko;
+      u4v kw[16], cw[4], sw[4];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) kw[4 * gq + qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8 * gq);
+        cw[gq] = *reinterpret_cast<const u4v*>(cos_t + (int64_t)pos * 32 + 8 * gq);
+        sw[gq] = *reinterpret_cast<const u4v*>(sin_t + (int64_t)pos * 32 + 8 * gq);
+      }
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const u4v w0 = kw[4 * gq], w1 = kw[4 * gq + 1], w2 = kw[4 * gq + 2], w3 = kw[4 * gq + 3];
+        const u4v c4 = cw[gq], s4 = sw[gq];
+        const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
+        const uint32_t a2[4] = {w2.x, w2.y, w2.z, w2.w}, a3[4] = {w3.x, w3.y, w3.z, w3.w};
+        const uint32_t cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          asm volatile("" ::: "memory");
+          const int j = 8 * gq + e;
+          const uint32_t sh = 16 * (e & 1);
+          const float k0 = bf2f((a0[e >> 1] >> sh) & 0xFFFFu), k1 = bf2f((a1[e >> 1] >> sh) & 0xFFFFu);
+          const float k2 = bf2f((a2[e >> 1] >> sh) & 0xFFFFu), k3 = bf2f((a3[e >> 1] >> sh) & 0xFFFFu);
+          const float cs = bf2f((cc[e >> 1] >> sh) & 0xFFFFu), sn = bf2f((ss[e >> 1] >> sh) & 0xFFFFu);
+          const float kr0 = bfround(__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)));
+          const float kr2 = bfround(__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn)));
+          const float4 qa = X.q[j], qb = X.q[32 + j], qc = X.q[64 + j], qd = X.q[96 + j];
+          sc[0] += qa.x * kr0 + qb.x * k1 + qc.x * kr2 + qd.x * k3;
+          sc[1] += qa.y * kr0 + qb.y * k1 + qc.y * kr2 + qd.y * k3;
+          sc[2] += qa.z * kr0 + qb.z * k1 + qc.z * kr2 + qd.z * k3;
+          sc[3] += qa.w * kr0 + qb.w * k1 + qc.w * kr2 + qd.w * k3;
+        }
+      }
+    }
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = valid ? sc[r] * scale : -INFINITY;
+      float cm = x;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+      const float mn = fmaxf(m[r], cm);
+      const float al = exp2f(m[r] - mn);
+      m[r] = mn;
+      p[r] = valid ? exp2f(x - mn) : 0.f;
+      lsum[r] = lsum[r] * al + p[r];
+      acc[r][0] *= al; acc[r][1] *= al;
+    }
+    // PV: lane owns dims 2 lane, 2 lane + 1; the chunk's weights are read back from LDS as broadcasts
+    X.p[w][lane] = make_float4(p[0], p[1], p[2], p[3]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const float4 pp = X.p[w][j];   // zero for masked tokens and tokens past the chunk
+      const uint32_t vj = ((vmask >> j) & 1) ? vv[j] : 0u;
+      const float v0 = bf2f_lo(vj), v1 = bf2f_hi(vj);
+      acc[0][0] += pp.x * v0; acc[0][1] += pp.x * v1;
+      acc[1][0] += pp.y * v0; acc[1][1] += pp.y * v1;
+      acc[2][0] += pp.z * v0; acc[2][1] += pp.z * v1;
+      acc[3][0] += pp.w * v0; acc[3][1] += pp.w * v1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float l = lsum[r];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) { X.m[w][r] = m[r]; X.l[w][r] = l; }
+    X.acc[w][r][2 * lane] = acc[r][0];
+    X.acc[w][r][2 * lane + 1] = acc[r][1];
+  }
+  __syncthreads();
+  if (tid >= 256) return;
+  // thread -> (row r = tid / 64, dims 2 (tid % 64), +1)
+  const int r = tid >> 6, dd = 2 * (tid & 63);
+  float M = NEG_BIG;
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, X.m[ww][r]);
+  float Ls = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) {
+    const float sc = exp2f(X.m[ww][r] - M);
+    Ls += sc * X.l[ww][r];
+    o0 += sc * X.acc[ww][r][dd];
+    o1 += sc * X.acc[ww][r][dd + 1];
+  }
+  if constexpr (!MERGE) {
+    const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
+    if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
+    ao[row * 128 + dd] = o0;
+    ao[row * 128 + dd + 1] = o1;
+  } else {
+    // wave r = row 4 h + r; lane owns dims dd, dd + 1 (same combination as decode_merge_kernel)
+    const int64_t rq = (int64_t)b * (ns + 1) * 16 + h * 4 + r;   // row of split 0; split s adds 16 s
+    // splits are visited 8 at a time with all of their loads issued together
+    float Mq = M;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mv[k] = (s0 + k < ns) ? mo[rq + 16 * (s0 + k)] : NEG_BIG;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) Mq = fmaxf(Mq, mv[k]);
+    }
+    const float we = exp2f(M - Mq);
+    float L = Ls * we, x0 = 0.f, x1 = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float mv[8], lv[8];
+      float2 av[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const bool in = s0 + k < ns;
+        const int64_t row = rq + 16 * (in ? s0 + k : 0);
+        mv[k] = in ? mo[row] : NEG_BIG;
+        lv[k] = lo_out[row];
+        av[k] = *reinterpret_cast<const float2*>(ao + row * 128 + dd);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float wq = exp2f(mv[k] - Mq);   // 0 for the padding entries
+        L += wq * lv[k];
+        x0 += wq * av[k].x;
+        x1 += wq * av[k].y;
+      }
+    }
+    // y = H x over the 128 dims: bit 0 of the dim in-lane, bits 1..6 across the wave's lanes
+    {
+      const float a = x0, c = x1;
+      x0 = a + c;
+      x1 = a - c;
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int msk = 1 << k;
+      const float p0 = __shfl_xor(x0, msk), p1 = __shfl_xor(x1, msk);
+      x0 = (lane & msk) ? p0 - x0 : x0 + p0;
+      x1 = (lane & msk) ? p1 - x1 : x1 + p1;
+    }
+    const float hn = __uint_as_float(0x3DB504F3u);
+    float y0 = (ns > 0 ? x0 * hn : 0.f) + o0 * we;
+    float y1 = (ns > 0 ? x1 * hn : 0.f) + o1 * we;
+    y0 = L > 0.f ? y0 / L : 0.f;
+    y1 = L > 0.f ? y1 / L : 0.f;
+    *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
+  }
+}
+
+template <bool MERGE>
+__global__ void __launch_bounds__(64 * XW)
+decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
+                    const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
+                    float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
+                    int nsink, uint16_t* __restrict__ out) {
+  __shared__ XLdsT<XW> X;
+  exact_body<XW, MERGE>(X, blockIdx.x >> 2, blockIdx.x & 3, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
+                        lo_out, ao, ns, scale, nsink, out);
+}
+
 // ---------------------------------------------------------------- quantized sub-blocks
 constexpr int QWAVES = 4;
 // LDS row strides are padded (132 floats, 272 floats, 9 x 16 bytes) so that the 16 lanes of a lane group, which read
@@ -130,14 +368,33 @@ __device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn
 }
 static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
 
+// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one
+// (row b, KV head h) (slot ns of the partials, as decode_exact_kernel<false>) before the split workgroups, so their
+// memory latency overlaps the splits' VALU work on the same CUs instead of following it.
+struct ExactArgs {
+  kv800_paged_t P;
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  int64_t rope_rows, epool_elems, sink_elems;
+  int nexact, nsink;
+};
+static_assert(sizeof(XLdsT<QWAVES>) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
+
 __global__ void __launch_bounds__(256, 2)
 decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
                     const int64_t* __restrict__ boff, int64_t bstride, const int32_t* __restrict__ nq,
                     const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
-                    float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale) {
+                    float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale, ExactArgs X) {
   __shared__ __align__(16) char lds_raw[sizeof(QLds)];
+  if ((int)blockIdx.x < X.nexact) {
+    exact_body<QWAVES, false>(*reinterpret_cast<XLdsT<QWAVES>*>(lds_raw), blockIdx.x >> 2, blockIdx.x & 3, X.P, q,
+                              X.cos_t, X.sin_t, X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns, scale,
+                              X.nsink, nullptr);
+    return;
+  }
   QLds& L = *reinterpret_cast<QLds*>(lds_raw);
-  const int b = blockIdx.x / ns, s = blockIdx.x % ns;
+  const int blk = (int)blockIdx.x - X.nexact;
+  const int b = blk / ns, s = blk % ns;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
@@ -402,231 +659,6 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   *reinterpret_cast<float4*>(ao + row * 128 + d0 + 4) = r1;
 }
 
-// ---------------------------------------------------------------- exact tail + sinks (SIMT)
-constexpr int XW = 8;                  // waves per exact-tail workgroup (64 tokens per wave per pass)
-struct XLds {
-  float4 q[128];                       // q rows r = 0..3 of this head at dim d
-  float4 p[XW][64];                    // per wave: softmax weights of rows 0..3 for the chunk's 64 tokens
-  const uint16_t* vrow[XW][64];        // per wave: V row of each token of the chunk (null: masked)
-  float m[XW][4], l[XW][4];            // per wave, per row
-  float acc[XW][4][128];               // per wave, row, dim
-};
-
-// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into split slot ns.
-// MERGE = true : instead merges it with the ns quantized partials of those rows (written before on the same stream)
-//                and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
-template <bool MERGE>
-__global__ void __launch_bounds__(64 * XW)
-decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
-                    const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
-                    float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
-                    int nsink, uint16_t* __restrict__ out) {
-  __shared__ XLds X;
-  const int b = blockIdx.x >> 2, h = blockIdx.x & 3;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  if (tid < 128) {
-    float4 a;
-    a.x = bf2f(q[((int64_t)b * 16 + h * 4 + 0) * 128 + tid]);
-    a.y = bf2f(q[((int64_t)b * 16 + h * 4 + 1) * 128 + tid]);
-    a.z = bf2f(q[((int64_t)b * 16 + h * 4 + 2) * 128 + tid]);
-    a.w = bf2f(q[((int64_t)b * 16 + h * 4 + 3) * 128 + tid]);
-    X.q[tid] = a;
-  }
-  __syncthreads();
-  const int n = P.N[b];
-  int lo_e = P.NQ[b] * BLK;
-  if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
-  lo_e = max(lo_e, 0);
-  const int cnt = (nsink > 0) ? max(0, min(min(nsink, lo_e), n)) : 0;
-  const int T = cnt + max(0, n - lo_e);
-  const int64_t* et = P.eoff + (int64_t)b * P.eoff_stride;
-
-  // element offset of token i's K row (sink or exact page) and of its V row; -1 if out of range
-  auto rows = [&](int i, int64_t& ko, int64_t& vo, int& pos) {
-    if (i < cnt) {
-      pos = i;
-      ko = P.skoff[b] + ((int64_t)i * 4 + h) * 128;
-      vo = P.svoff[b] + ((int64_t)i * 4 + h) * 128;
-      if (ko < 0 || vo < 0 || ko + 128 > sink_elems || vo + 128 > sink_elems) { ko = vo = -1; }
-    } else {
-      pos = lo_e + (i - cnt);
-      const int64_t pg = pos / P.ebs;
-      if (pg >= P.eoff_stride) { ko = vo = -1; return; }
-      ko = et[pg] + h * P.e_hs + (pos % P.ebs) * P.e_ts;
-      vo = ko + P.e_v;
-      if (ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) { ko = vo = -1; }
-    }
-  };
-
-  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0}, acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  for (int c0 = 64 * w; c0 < T; c0 += 64 * XW) {
-    asm volatile("" ::: "memory");   // keep the q reads below inside the loop (no 512-register hoist)
-    const int i = c0 + lane;
-    int64_t ko = -1, vo = -1;
-    int pos = 0;
-    if (i < T) rows(i, ko, vo, pos);
-    const bool valid = (i < T) && ko >= 0 && pos < rope_rows;
-    const uint16_t* Kb = (i < cnt) ? P.sk : P.epool;
-    // V rows of the chunk's 64 tokens, exchanged through the wave's LDS slots; every lane then requests its two dims of
-    // all 64 rows at once, so these loads overlap the QK work below (masked tokens read row 0 of the exact pool and
-    // are zeroed by vmask)
-    const bool vok = valid && vo >= 0;
-    const uint64_t vmask = __ballot(vok);
-    X.vrow[w][lane] = vok ? ((i < cnt) ? P.sv : P.epool) + vo : P.epool;
-    __builtin_amdgcn_wave_barrier();
-    uint32_t vv[64];
-#pragma unroll
-    for (int j = 0; j < 64; ++j) vv[j] = *reinterpret_cast<const uint32_t*>(X.vrow[w][j] + 2 * lane);
-    float sc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
-      // the token's whole K row and rope row are requested before any of it is used
-      const uint16_t* kr = Kb + ko;
-      u4v kw[16], cw[4], sw[4];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) kw[4 * gq + qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8 * gq);
-        cw[gq] = *reinterpret_cast<const u4v*>(cos_t + (int64_t)pos * 32 + 8 * gq);
-        sw[gq] = *reinterpret_cast<const u4v*>(sin_t + (int64_t)pos * 32 + 8 * gq);
-      }
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const u4v w0 = kw[4 * gq], w1 = kw[4 * gq + 1], w2 = kw[4 * gq + 2], w3 = kw[4 * gq + 3];
-        const u4v c4 = cw[gq], s4 = sw[gq];
-        const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
-        const uint32_t a2[4] = {w2.x, w2.y, w2.z, w2.w}, a3[4] = {w3.x, w3.y, w3.z, w3.w};
-        const uint32_t cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          asm volatile("" ::: "memory");
-          const int j = 8 * gq + e;
-          const uint32_t sh = 16 * (e & 1);
-          const float k0 = bf2f((a0[e >> 1] >> sh) & 0xFFFFu), k1 = bf2f((a1[e >> 1] >> sh) & 0xFFFFu);
-          const float k2 = bf2f((a2[e >> 1] >> sh) & 0xFFFFu), k3 = bf2f((a3[e >> 1] >> sh) & 0xFFFFu);
-          const float cs = bf2f((cc[e >> 1] >> sh) & 0xFFFFu), sn = bf2f((ss[e >> 1] >> sh) & 0xFFFFu);
-          const float kr0 = bfround(__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)));
-          const float kr2 = bfround(__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn)));
-          const float4 qa = X.q[j], qb = X.q[32 + j], qc = X.q[64 + j], qd = X.q[96 + j];
-          sc[0] += qa.x * kr0 + qb.x * k1 + qc.x * kr2 + qd.x * k3;
-          sc[1] += qa.y * kr0 + qb.y * k1 + qc.y * kr2 + qd.y * k3;
-          sc[2] += qa.z * kr0 + qb.z * k1 + qc.z * kr2 + qd.z * k3;
-          sc[3] += qa.w * kr0 + qb.w * k1 + qc.w * kr2 + qd.w * k3;
-        }
-      }
-    }
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = valid ? sc[r] * scale : -INFINITY;
-      float cm = x;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
-      const float mn = fmaxf(m[r], cm);
-      const float al = exp2f(m[r] - mn);
-      m[r] = mn;
-      p[r] = valid ? exp2f(x - mn) : 0.f;
-      lsum[r] = lsum[r] * al + p[r];
-      acc[r][0] *= al; acc[r][1] *= al;
-    }
-    // PV: lane owns dims 2 lane, 2 lane + 1; the chunk's weights are read back from LDS as broadcasts
-    X.p[w][lane] = make_float4(p[0], p[1], p[2], p[3]);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      const float4 pp = X.p[w][j];   // zero for masked tokens and tokens past the chunk
-      const uint32_t vj = ((vmask >> j) & 1) ? vv[j] : 0u;
-      const float v0 = bf2f_lo(vj), v1 = bf2f_hi(vj);
-      acc[0][0] += pp.x * v0; acc[0][1] += pp.x * v1;
-      acc[1][0] += pp.y * v0; acc[1][1] += pp.y * v1;
-      acc[2][0] += pp.z * v0; acc[2][1] += pp.z * v1;
-      acc[3][0] += pp.w * v0; acc[3][1] += pp.w * v1;
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float l = lsum[r];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    if (lane == 0) { X.m[w][r] = m[r]; X.l[w][r] = l; }
-    X.acc[w][r][2 * lane] = acc[r][0];
-    X.acc[w][r][2 * lane + 1] = acc[r][1];
-  }
-  __syncthreads();
-  if (tid >= 256) return;
-  // thread -> (row r = tid / 64, dims 2 (tid % 64), +1)
-  const int r = tid >> 6, dd = 2 * (tid & 63);
-  float M = NEG_BIG;
-#pragma unroll
-  for (int ww = 0; ww < XW; ++ww) M = fmaxf(M, X.m[ww][r]);
-  float Ls = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < XW; ++ww) {
-    const float sc = exp2f(X.m[ww][r] - M);
-    Ls += sc * X.l[ww][r];
-    o0 += sc * X.acc[ww][r][dd];
-    o1 += sc * X.acc[ww][r][dd + 1];
-  }
-  if constexpr (!MERGE) {
-    const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
-    if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
-    ao[row * 128 + dd] = o0;
-    ao[row * 128 + dd + 1] = o1;
-  } else {
-    // wave r = row 4 h + r; lane owns dims dd, dd + 1 (same combination as decode_merge_kernel)
-    const int64_t rq = (int64_t)b * (ns + 1) * 16 + h * 4 + r;   // row of split 0; split s adds 16 s
-    // splits are visited 8 at a time with all of their loads issued together
-    float Mq = M;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) mv[k] = (s0 + k < ns) ? mo[rq + 16 * (s0 + k)] : NEG_BIG;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) Mq = fmaxf(Mq, mv[k]);
-    }
-    const float we = exp2f(M - Mq);
-    float L = Ls * we, x0 = 0.f, x1 = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8], lv[8];
-      float2 av[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const bool in = s0 + k < ns;
-        const int64_t row = rq + 16 * (in ? s0 + k : 0);
-        mv[k] = in ? mo[row] : NEG_BIG;
-        lv[k] = lo_out[row];
-        av[k] = *reinterpret_cast<const float2*>(ao + row * 128 + dd);
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float wq = exp2f(mv[k] - Mq);   // 0 for the padding entries
-        L += wq * lv[k];
-        x0 += wq * av[k].x;
-        x1 += wq * av[k].y;
-      }
-    }
-    // y = H x over the 128 dims: bit 0 of the dim in-lane, bits 1..6 across the wave's lanes
-    {
-      const float a = x0, c = x1;
-      x0 = a + c;
-      x1 = a - c;
-    }
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const int msk = 1 << k;
-      const float p0 = __shfl_xor(x0, msk), p1 = __shfl_xor(x1, msk);
-      x0 = (lane & msk) ? p0 - x0 : x0 + p0;
-      x1 = (lane & msk) ? p1 - x1 : x1 + p1;
-    }
-    const float hn = __uint_as_float(0x3DB504F3u);
-    float y0 = (ns > 0 ? x0 * hn : 0.f) + o0 * we;
-    float y1 = (ns > 0 ? x1 * hn : 0.f) + o1 * we;
-    y0 = L > 0.f ? y0 / L : 0.f;
-    y1 = L > 0.f ? y1 / L : 0.f;
-    *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
-  }
-}
-
 // ---------------------------------------------------------------- split merge
 __global__ void __launch_bounds__(256)
 decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
@@ -708,23 +740,33 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Validates the exact-tail arguments and launches decode_exact_kernel; with out != null the fused variant that also
-// merges the quantized splits and writes the bf16 rows.
-int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
-                 int64_t rope_rows, int64_t epool_elems, int64_t sink_elems, float* mo, float* lo, float* ao, int64_t B,
-                 int64_t ns, float scale, uint16_t* out, void* stream) {
+// Validates the exact-tail arguments (for the standalone kernel and for the exact workgroups of the split grid);
+// sets *nsink.
+int check_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                int64_t epool_elems, float* mo, float* lo, float* ao, int64_t B, int64_t ns, uint16_t* out,
+                int* nsink) {
   KV800_REQUIRE(P && B >= 0 && ns >= 0, "decode_exact: bad arguments");
-  if (B == 0) return KV800_OK;
   KV800_REQUIRE(q && cos_t && sin_t && mo && lo && ao && P->epool && P->eoff && P->N && P->NQ,
                 "decode_exact: null pointer");
   KV800_REQUIRE(P->ebs > 0 && P->win >= 0, "decode_exact: ebs must be > 0");
   KV800_REQUIRE(P->e_hs % 8 == 0 && P->e_ts % 8 == 0 && ((uintptr_t)P->epool % 16) == 0,
                 "decode_exact: exact strides must be multiples of 8 elements and the pool 16-byte aligned");
-  const int nsink = P->sk ? NSINK : 0;
-  KV800_REQUIRE(!nsink || (P->sv && P->skoff && P->svoff), "decode_exact: sinks need sv, skoff and svoff");
+  *nsink = P->sk ? NSINK : 0;
+  KV800_REQUIRE(!*nsink || (P->sv && P->skoff && P->svoff), "decode_exact: sinks need sv, skoff and svoff");
   KV800_REQUIRE(B * 4 <= 0x7FFFFFFF, "decode_exact: grid too large");
   KV800_REQUIRE(!out || ((uintptr_t)out % 4) == 0, "decode: out must be 4-byte aligned");
   KV800_REQUIRE(epool_elems >= 128, "decode_exact: the exact pool must hold at least one 128-element row");
+  return KV800_OK;
+}
+
+// Launches decode_exact_kernel; with out != null the fused variant that also merges the quantized splits and writes
+// the bf16 rows.
+int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                 int64_t rope_rows, int64_t epool_elems, int64_t sink_elems, float* mo, float* lo, float* ao, int64_t B,
+                 int64_t ns, float scale, uint16_t* out, void* stream) {
+  if (B == 0) return KV800_OK;
+  int nsink = 0, rc;
+  if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &nsink)) != KV800_OK) return rc;
   if (out)
     hipLaunchKernelGGL(decode_exact_kernel<true>, dim3((unsigned)(B * 4)), dim3(64 * XW), 0, (hipStream_t)stream, *P, q,
                        cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
@@ -735,6 +777,24 @@ int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_
   return check_launch(out ? "decode_exact_merge" : "decode_exact");
 }
 
+// Launches the quantized-split grid; xa != null adds the B * 4 exact-tail workgroups (arguments checked by
+// check_exact).
+int launch_quant(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
+                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows, float* mo, float* lo,
+                 float* ao, int64_t B, int64_t ns, int64_t spb, float scale, const ExactArgs* xa, void* stream) {
+  KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
+  if (B == 0 || ns == 0) return KV800_OK;
+  KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
+  KV800_REQUIRE(B * ns + B * 4 <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
+  KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
+                "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
+  ExactArgs X{};
+  if (xa) X = *xa;
+  else X.nexact = 0;
+  hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(B * ns + X.nexact)), dim3(256), 0, (hipStream_t)stream, q,
+                     qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale, X);
+  return check_launch(xa ? "decode_quant_exact" : "decode_quant");
+}
 
 }  // namespace
 }  // namespace kv800
@@ -771,15 +831,8 @@ int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_
                                  int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
                                  void* stream) {
-  KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
-  if (B == 0 || ns == 0) return KV800_OK;
-  KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
-  KV800_REQUIRE(B * ns <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
-  KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
-                "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(B * ns)), dim3(256), 0, (hipStream_t)stream, q, qpool,
-                     qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale);
-  return check_launch("decode_quant");
+  return launch_quant(q, qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, B, ns, spb, scale,
+                      nullptr, stream);
 }
 
 int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
@@ -851,11 +904,17 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
       if ((rc = kv800_hip_rope_table(cos_t, sin_t, rows, cst, stream)) != KV800_OK) return rc;
       cs16 = cst;
     }
-    if ((rc = kv800_hip_decode_quant_sized(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo,
-                                           ao, B, ns, sp, scale, stream)) != KV800_OK)
+    // quantized splits and the exact tail in one grid, then the split merge
+    ExactArgs X{};
+    X.P = *P; X.cos_t = cos_t; X.sin_t = sin_t; X.rope_rows = rope_rows; X.epool_elems = epool_elems;
+    X.sink_elems = sink_elems; X.nexact = (int)(B * 4);
+    if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;
+    if ((rc = launch_quant(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo, ao, B, ns, sp,
+                           scale, &X, stream)) != KV800_OK)
       return rc;
+    return kv800_hip_decode_merge(mo, lo, ao, B, ns, out, stream);
   }
-  // exact tail + sinks, fused with the split merge (one launch writes the bf16 rows)
+  // no quantized part (window layers): exact tail + sinks fused with the merge (one launch writes the bf16 rows)
   return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, out, stream);
 }
 
