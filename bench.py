@@ -71,6 +71,55 @@ def build_layer(torch, kh, seed, dev):
                     sk=None, sv=None, skoff=None, svoff=None, N=N, NQ=NQt, nqmax=NQ, win=0)
 
 
+C2_B, C2_N, C2_EBS = 64, 2048, 128
+C2_NQ = (C2_N - 128) // 256                         # 7 flushed sub-blocks per sequence (kv800.py:433 flush rule)
+C2_READ = C2_B * C2_NQ * 256 * 4 * 128 * 2 * 2      # bf16 K + V gathered from the exact pages
+C2_WRITE = C2_B * C2_NQ * 51200
+C2_FMA = C2_B * C2_NQ * 256 * 4 * 64 * 192          # fp32 fma of the bit-exact V Hadamard chains (96 per output)
+FMA_PEAK = 256 * 64 * 2.4e9                         # non-packed fp32 fma/s: 256 CUs x 64 lanes x 2.4 GHz
+
+
+def bench_flush_c2(torch, kh, dev, steps, warmup):
+    """BASELINE config 2, the flush kernel alone: 64 sequences x a 2048-token prefill chunk in vLLM-geometry exact
+    pages (128 tokens x 4 heads x [K128 | V128] bf16 per page, shuffled physical pages), K / V ~ N(0,1) with 1 % of
+    the elements x 8, flushed by one launch into shuffled 1280-token quant pages (5 x 51,200 B per 262,144-B page):
+    448 sub-blocks. Per-launch HIP events on the current stream."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    pages = C2_N // C2_EBS
+    npg = C2_B * pages
+    x = torch.randn(npg, 4, C2_EBS, 256, generator=g, device=dev)
+    x[torch.rand(x.shape, generator=g, device=dev) < 0.01] *= 8
+    epool = x.to(torch.bfloat16)
+    del x
+    eoff = (torch.randperm(npg, generator=g, device=dev).view(C2_B, pages) * (4 * C2_EBS * 256)).to(torch.int64)
+    qpp = (C2_NQ * 256 + 1279) // 1280
+    qpool = torch.zeros(C2_B * qpp * 262144, dtype=torch.uint8, device=dev)
+    qbt = torch.randperm(C2_B * qpp, generator=g, device=dev).view(C2_B, qpp).to(torch.int64)
+    nq0 = torch.zeros(C2_B, dtype=torch.int32, device=dev)
+    nq1 = torch.full((C2_B,), C2_NQ, dtype=torch.int32, device=dev)
+
+    def flush():
+        kh.flush(epool, eoff, C2_EBS, C2_EBS * 256, 256, 128, qpool, qbt, 1280, 262144, nq0, nq1, C2_NQ)
+
+    for _ in range(warmup):
+        flush()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record(s)
+        flush()
+        e1.record(s)
+    ev[-1][1].synchronize()
+    ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+    gbps = (C2_READ + C2_WRITE) / (ms * 1e-3) / 1e9
+    return {"workload": "C2: flush of 64 seqs x 2048-token chunk = 448 sub-blocks, vLLM page geometry, shuffled "
+                        "exact and quant page tables, N(0,1) K/V with 1% outliers x8",
+            "ms": round(ms, 5), "bytes": C2_READ + C2_WRITE, "gbps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBS, 4), "bound": "valu",
+            "fma_per_launch": C2_FMA, "fma_frac": round(C2_FMA / (ms * 1e-3) / FMA_PEAK, 4)}
+
+
 def rope_tables(torch, n, dev):
     """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
     inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
@@ -196,6 +245,8 @@ def main():
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
 
+    flush_c2 = bench_flush_c2(torch, kh, dev, max(5, min(a.steps, 20)), 2)
+
     achieved = QBYTES / (ms_quant * 1e-3) / 1e9
     layer_gbps = ALG_BYTES / (ms_step * 1e-3) / 1e9
     cpu = None
@@ -219,6 +270,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(), "kernel_ms": round(ms_quant, 5), "bytes_per_launch": QBYTES},
         "cpu_baseline": cpu,
+        "flush_c2": flush_c2,
     }
     print(json.dumps(res), flush=True)
 

@@ -149,10 +149,10 @@ struct QuantLds {                  // K path: per-wave min / max partials, then 
   float col_lo[512];
   float col_den[512];
 };
-constexpr int LDS_BYTES = (int)sizeof(QuantLds);
 
+// K codes and scales of one sub-block: per (head, channel) min / max over its 256 tokens (8 waves x 32 tokens).
 template <typename Src>
-__device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* lds) {
+__device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   QuantLds& S = *reinterpret_cast<QuantLds*>(lds);
   float* red_min = &S.red_min[0][0];
@@ -160,30 +160,33 @@ __device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* ld
   float* col_lo = S.col_lo;
   float* col_den = S.col_den;
 
-  // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16)
+  // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16). The
+  // rows are read in groups of KG tokens, twice (min / max, then codes; the second pass hits L2), which keeps the
+  // pass within the register budget of the V pass it shares a grid with.
+  constexpr int KG = 8;
   const int h = lane >> 4, c0 = 8 * (lane & 15);
-  uint4 kx[TPW];
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + tt, h) + c0);
   float mn[8], mx[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) { mn[e] = INFINITY; mx[e] = -INFINITY; }
+#pragma unroll 1
+  for (int t0 = 0; t0 < TPW; t0 += KG) {
+    uint4 kx[KG];
 #pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
+    for (int tt = 0; tt < KG; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + t0 + tt, h) + c0);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
-      mn[e] = fminf(mn[e], x);
-      mx[e] = fmaxf(mx[e], x);
+    for (int tt = 0; tt < KG; ++tt) {
+      const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+        mn[e] = fminf(mn[e], x);
+        mx[e] = fmaxf(mx[e], x);
+      }
     }
   }
   const int hc0 = h * 128 + c0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) { red_min[w * 512 + hc0 + e] = mn[e]; red_max[w * 512 + hc0 + e] = mx[e]; }
-  // the code pass re-derives the floats from the packed bf16 registers instead of keeping 128 converted values live
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) asm volatile("" : "+v"(kx[tt].x), "+v"(kx[tt].y), "+v"(kx[tt].z), "+v"(kx[tt].w));
   __syncthreads();
   if (tid < 512) {
     float lo = red_min[tid], hi = red_max[tid];
@@ -202,34 +205,56 @@ __device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* ld
 #pragma unroll
     for (int e = 0; e < 8; ++e) { lof[e] = col_lo[hc0 + e]; den[e] = col_den[hc0 + e]; }
     const int p = (lane & 15) >> 2, q = lane & 3;   // plane of these 8 channels, byte quarter 8q .. 8q + 7
+#pragma unroll 1
+    for (int t0 = 0; t0 < TPW; t0 += KG) {
+      uint4 kx[KG];
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      __builtin_amdgcn_sched_barrier(0);   // one token row at a time: keeps the division temporaries bounded
-      const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
-      uint32_t d0 = 0, d1 = 0;
+      for (int tt = 0; tt < KG; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + t0 + tt, h) + c0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
-        float c = __builtin_rintf(__fdiv_rn(__fsub_rn(x, lof[e]), den[e]));
-        c = fminf(fmaxf(c, 0.f), 3.f);
-        const uint32_t code = (uint32_t)c << (2 * p);
-        if (e < 4) d0 |= code << (8 * e); else d1 |= code << (8 * (e - 4));
-      }
-      d0 |= __shfl_xor(d0, 4); d1 |= __shfl_xor(d1, 4);
-      d0 |= __shfl_xor(d0, 8); d1 |= __shfl_xor(d1, 8);
-      if (p == 0) {
-        const int t = TPW * w + tt;
-        *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + h) * 32 + 8 * q) = make_uint2(d0, d1);
+      for (int tt = 0; tt < KG; ++tt) {
+        __builtin_amdgcn_sched_barrier(0);   // one token row at a time: keeps the division temporaries bounded
+        const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
+        uint32_t d0 = 0, d1 = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+          float c = __builtin_rintf(__fdiv_rn(__fsub_rn(x, lof[e]), den[e]));
+          c = fminf(fmaxf(c, 0.f), 3.f);
+          const uint32_t code = (uint32_t)c << (2 * p);
+          if (e < 4) d0 |= code << (8 * e); else d1 |= code << (8 * (e - 4));
+        }
+        d0 |= __shfl_xor(d0, 4); d1 |= __shfl_xor(d1, 4);
+        d0 |= __shfl_xor(d0, 8); d1 |= __shfl_xor(d1, 8);
+        if (p == 0) {
+          const int t = TPW * w + t0 + tt;
+          *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + h) * 32 + 8 * q) = make_uint2(d0, d1);
+        }
       }
     }
   }
-  __syncthreads();   // the K scratch is reused below
+}
 
-  // ---------------- V: wave w = tokens 32w .. 32w + 31; per token the 4 head rows, lane = dims lane, lane + 64
+// V bits and scales of tokens [t0, t0 + VTOK) of one sub-block: wave w takes VTPW consecutive tokens, per token its
+// 4 head rows with lane = dims lane, lane + 64. The rows reach the Hadamard chains through scalar loads (x is an
+// SGPR operand, no VGPRs hold the rows); every lane touches 16 bytes of the token two ahead with a vector load so
+// that those scalar loads find the rows in L2 instead of waiting on HBM.
+constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
+
+template <typename Src>
+__device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tw = t0 + VTPW * w;                      // this wave's first token
+  const int rh = lane >> 4, rc = 8 * (lane & 15);    // the 16 bytes this lane touches: head rh, dims rc .. rc + 7
+  auto touch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, rh) + rc); };
+  uint4 pf0 = touch(tw), pf1 = touch(tw + 1);
   float hcol[64];
   hadamard_column(hcol, lane);
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int t = TPW * w + tt;
+#pragma unroll 1
+  for (int tt = 0; tt < VTPW; ++tt) {
+    const int t = tw + tt;
+    asm volatile("" :: "v"(pf0.x), "v"(pf0.y), "v"(pf0.z), "v"(pf0.w));   // token t is in L2 by now
+    pf0 = pf1;
+    if (tt + 2 < VTPW) pf1 = touch(t + 2);
     float ya[4], yb[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -263,13 +288,26 @@ __device__ void quantize_sub(const Src& src, uint8_t* __restrict__ out, char* ld
   }
 }
 
+// A quantize grid holds, per sub-block, one K workgroup (all 256 tokens per (head, channel)) followed in the grid by
+// VSPLIT V workgroups (V is independent per token). Both passes fit one register budget, so 4 waves per SIMD run and
+// the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup i < units is the K pass of unit i;
+// i >= units is the V pass of unit (i - units) / VSPLIT, token range (i - units) % VSPLIT.
+constexpr int QLDS_BYTES = (int)sizeof(QuantLds);
+
+template <typename Src>
+__device__ __forceinline__ void quantize_part(const Src& src, uint8_t* __restrict__ out, char* lds, bool kpass, int part) {
+  if (kpass) quantize_k(src, out, lds);
+  else quantize_v(src, out, part * VTOK);
+}
+
 __global__ void __launch_bounds__(QTHREADS) quantize_dense_kernel(const uint16_t* __restrict__ k,
                                                                    const uint16_t* __restrict__ v,
-                                                                   uint8_t* __restrict__ out) {
-  __shared__ __align__(16) char lds[LDS_BYTES];
-  const int64_t m = blockIdx.x;
-  DenseSrc src{k, v, m};
-  quantize_sub(src, out + m * SUB, lds);
+                                                                   uint8_t* __restrict__ out, int64_t M) {
+  __shared__ __align__(16) char lds[QLDS_BYTES];
+  const int64_t i = blockIdx.x;
+  const bool kpass = i < M;
+  const int64_t m = kpass ? i : (i - M) / VSPLIT;
+  quantize_part(DenseSrc{k, v, m}, out + m * SUB, lds, kpass, kpass ? 0 : (int)((i - M) % VSPLIT));
 }
 
 __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restrict__ ep, const int64_t* __restrict__ eoff,
@@ -277,15 +315,18 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
                                                          uint8_t* __restrict__ qpool, const int64_t* __restrict__ qbt,
                                                          int64_t qs, int64_t bsq, int64_t qs0,
                                                          const int32_t* __restrict__ nq_prev,
-                                                         const int32_t* __restrict__ nq_new, int max_new) {
-  __shared__ __align__(16) char lds[LDS_BYTES];
-  const int64_t r = blockIdx.x / max_new;
-  const int j = nq_prev[r] + (int)(blockIdx.x % max_new);
+                                                         const int32_t* __restrict__ nq_new, int64_t R, int max_new) {
+  __shared__ __align__(16) char lds[QLDS_BYTES];
+  const int64_t units = R * max_new, i = blockIdx.x;
+  const bool kpass = i < units;
+  const int64_t unit = kpass ? i : (i - units) / VSPLIT;
+  const int64_t r = unit / max_new;
+  const int j = nq_prev[r] + (int)(unit % max_new);
   if (j >= nq_new[r]) return;   // uniform over the workgroup
   const int64_t tok0 = (int64_t)j * BLK;
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
-  PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
-  quantize_sub(src, dst, lds);
+  quantize_part(PagedSrc{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0}, dst, lds, kpass,
+                kpass ? 0 : (int)((i - units) % VSPLIT));
 }
 
 // ---------------------------------------------------------------- dequantize (kv800.py:79-92)
@@ -358,10 +399,11 @@ int kv800_hip_quantize_blocks(const uint16_t* k, const uint16_t* v, int64_t M, u
   KV800_REQUIRE(M >= 0, "quantize_blocks: M = %lld < 0", (long long)M);
   if (M == 0) return KV800_OK;
   KV800_REQUIRE(k && v && out, "quantize_blocks: null pointer");
-  KV800_REQUIRE(M <= 0x7FFFFFFF, "quantize_blocks: M = %lld too large", (long long)M);
+  KV800_REQUIRE(M * (1 + VSPLIT) <= 0x7FFFFFFF, "quantize_blocks: M = %lld too large", (long long)M);
   KV800_REQUIRE(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && ((uintptr_t)out % 8) == 0,
                 "quantize_blocks: k / v must be 16-byte aligned and out 8-byte aligned");
-  hipLaunchKernelGGL(quantize_dense_kernel, dim3((unsigned)M), dim3(QTHREADS), 0, (hipStream_t)stream, k, v, out);
+  hipLaunchKernelGGL(quantize_dense_kernel, dim3((unsigned)(M * (1 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream, k,
+                     v, out, M);
   return check_launch("quantize_blocks");
 }
 
@@ -376,9 +418,10 @@ int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_str
   KV800_REQUIRE(ebs > 0 && bsq > 0 && bsq % BLK == 0, "flush: ebs must be > 0 and bsq a positive multiple of 256");
   KV800_REQUIRE(e_hs % 8 == 0 && e_ts % 8 == 0 && e_v % 8 == 0 && ((uintptr_t)epool % 16) == 0,
                 "flush: exact-pool strides must be multiples of 8 elements and the pool 16-byte aligned");
-  KV800_REQUIRE(R * max_new <= 0x7FFFFFFF && max_new <= 0x7FFFFFFF, "flush: grid too large");
-  hipLaunchKernelGGL(flush_kernel, dim3((unsigned)(R * max_new)), dim3(QTHREADS), 0, (hipStream_t)stream, epool, eoff,
-                     eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq, qs0, nq_prev, nq_new, (int)max_new);
+  KV800_REQUIRE(R * max_new * (1 + VSPLIT) <= 0x7FFFFFFF, "flush: grid too large");
+  hipLaunchKernelGGL(flush_kernel, dim3((unsigned)(R * max_new * (1 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream,
+                     epool, eoff, eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq, qs0, nq_prev, nq_new, R,
+                     (int)max_new);
   return check_launch("flush");
 }
 
