@@ -155,6 +155,40 @@ def test_flush_two_kv_groups(hip, oracle):
                 assert not q[off:off + 51200].any()
 
 
+def test_flush_c2_full_size(hip, oracle):
+    """BASELINE config 2 at full size: 64 sequences x a 2048-token chunk in vLLM-geometry exact pages (shuffled), K / V
+    ~ N(0,1) with 1 % of the elements x 8, one flush launch into shuffled 1280-token quant pages: all 448 sub-blocks
+    (the flush rule gives 7 per sequence) must equal the oracle quantizer's bytes."""
+    B, n, ebs = 64, 2048, 128
+    nq = (n - 128) // 256
+    pages = n // ebs
+    g = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(B * pages, 4, ebs, 256, generator=g, device=DEV)
+    x[torch.rand(x.shape, generator=g, device=DEV) < 0.01] *= 8
+    epool = x.to(torch.bfloat16)
+    del x
+    perm = torch.randperm(B * pages, generator=g, device=DEV).view(B, pages)
+    eoff = (perm * (4 * ebs * 256)).to(torch.int64)
+    qpp = (nq * 256 + 1279) // 1280
+    qbt = torch.randperm(B * qpp, generator=g, device=DEV).view(B, qpp).to(torch.int64)
+    qpool = torch.zeros(B * qpp * 262144, dtype=torch.uint8, device=DEV)
+    say("flush C2", B, "x", nq, "sub-blocks")
+    hip.flush(epool, eoff, ebs, ebs * 256, 256, 128, qpool, qbt, 1280, 262144,
+              torch.zeros(B, dtype=torch.int32, device=DEV), torch.full((B,), nq, dtype=torch.int32, device=DEV), nq)
+    q = qpool.cpu().numpy()
+    ep = bits_of(epool).reshape(B * pages, 4, ebs, 256)
+    pm, qb = perm.cpu().numpy(), qbt.cpu().numpy()
+    rows = ep[pm].transpose(0, 1, 3, 2, 4).reshape(B, pages * ebs, 4, 256)   # (row, token, head, K | V)
+    want = oracle.quantize_blocks(np.ascontiguousarray(rows[:, :nq * 256, :, :128].reshape(B * nq, 256, 4, 128)),
+                                  np.ascontiguousarray(rows[:, :nq * 256, :, 128:].reshape(B * nq, 256, 4, 128)))
+    bad = 0
+    for r in range(B):
+        for j in range(nq):
+            off = qb[r, (256 * j) // 1280] * 262144 + ((256 * j) % 1280) // 256 * 51200
+            bad += not np.array_equal(q[off:off + 51200], want[r * nq + j])
+    assert bad == 0, f"{bad} of {B * nq} sub-blocks differ"
+
+
 def test_dequantize_vs_oracle(hip, oracle):
     kb, vb = make_golden.case_inputs("outlier")
     sb = oracle.quantize_blocks(kb, vb)
