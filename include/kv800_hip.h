@@ -112,6 +112,23 @@ int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const
                      const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream);
 
+/* Step bookkeeping in vLLM's page geometry (exact page [4 heads, ebs, K128 | V128] bf16 with element strides s0 (page),
+ * s1 (head), s2 (token); quant page = 5 x 51,200-byte sub-blocks per 1280 tokens, qs0 bytes apart). */
+
+/* Write the step's pre-RoPE K and unrotated V rows, k / v (R, 4, 128) bf16, to slot[r] (page slot / ebs, offset
+ * slot % ebs; slot < 0 = padding, skipped). Replaces the index_put of vllm_attn.py:263-272. With sk != NULL (window
+ * layers) rows at pos[r] < 4 are also written to the sink blocks [4 sinks, 4, 128] at sk + skoff[r] / sv + svoff[r]
+ * (the aux area of the host layers' first quant page), replacing vllm_attn.py:276-291. */
+int kv800_hip_write_exact(uint16_t* epool, int64_t s0, int64_t s1, int64_t s2, int64_t e_v, int64_t ebs,
+                          const int64_t* slot, const uint16_t* k, const uint16_t* v, int64_t R, const int64_t* pos,
+                          uint16_t* sk, uint16_t* sv, const int64_t* skoff, const int64_t* svoff, void* stream);
+
+/* Decode tables of a quantized layer, replacing vllm_attn.py:332-340: NQ[r] = max(N[r] - 128, 0) / 256 and, for
+ * j < nqmax, boff[r, j] = qbt[r, 256 j / bsq] * qs0 + (256 j % bsq) / 256 * 51200 (boff row stride nqmax). qbt: the
+ * quant group's (R, qbt_stride) int32 block table. */
+int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
+                            int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream);
+
 /* Bounds-checked forms used by the Python layer. They take the extent of every pool the kernels read, measured from
  * the pointer passed in: qpool_bytes (bytes), epool_elems / sink_elems (bf16 elements), rope_rows (rows of cos_t /
  * sin_t and of cs16). A sub-block, page or row whose offset falls outside its pool is skipped instead of read, so a

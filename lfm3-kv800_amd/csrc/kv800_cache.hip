@@ -1,0 +1,94 @@
+// kv800_cache.hip -- per-step cache bookkeeping of the 800h path in vLLM's page geometry, for gfx950.
+//
+//   write_exact_kernel   the step's K / V rows into the exact pages through the slot mapping (vllm_attn.py:263-272),
+//                        and, for tokens at positions < 4 of a window layer, into the sink aux area of the host
+//                        layers' first quant page (vllm_attn.py:276-291).
+//   decode_tables_kernel per decode row: NQ = max(N - 128, 0) / 256 flushed sub-blocks and the byte offsets of its
+//                        first nqmax sub-blocks in the quant pool, qbt[r, 256 j / bsq] * qs0 + (256 j % bsq) / 256 *
+//                        51200 (vllm_attn.py:332-340).
+// Both are plain data movement: one thread per 16-byte piece or per table entry, coalesced along the row.
+#include "kv800_common.h"
+#include "../../include/kv800_hip.h"
+
+namespace kv800 {
+namespace {
+
+// thread -> (row r, piece): 4 heads x 128 dims = 64 pieces of 8 bf16 per K row and as many per V row
+__global__ void __launch_bounds__(256)
+write_exact_kernel(uint16_t* __restrict__ ep, int64_t s0, int64_t s1, int64_t s2, int64_t e_v, int64_t ebs,
+                   const int64_t* __restrict__ slot, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                   int64_t R, const int64_t* __restrict__ pos, uint16_t* __restrict__ skp, uint16_t* __restrict__ svp,
+                   const int64_t* __restrict__ skoff, const int64_t* __restrict__ svoff, int nsink) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= R * 128) return;
+  const int64_t r = i >> 7;
+  const int piece = (int)(i & 127), isv = piece >> 6, h = (piece >> 4) & 3, d0 = 8 * (piece & 15);
+  const uint4 x = *reinterpret_cast<const uint4*>((isv ? v : k) + (r * 4 + h) * 128 + d0);
+  const int64_t sl = slot[r];
+  if (sl >= 0) {   // slot < 0: padding token, not written (vllm_attn.py:265)
+    const int64_t o = (sl / ebs) * s0 + h * s1 + (sl % ebs) * s2 + (isv ? e_v : 0) + d0;
+    *reinterpret_cast<uint4*>(ep + o) = x;
+  }
+  if (nsink > 0 && pos[r] >= 0 && pos[r] < nsink) {   // sink rows of a window layer
+    uint16_t* dst = isv ? svp : skp;
+    const int64_t base = isv ? svoff[r] : skoff[r];
+    *reinterpret_cast<uint4*>(dst + base + (pos[r] * 4 + h) * 128 + d0) = x;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+decode_tables_kernel(const int32_t* __restrict__ qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0,
+                     const int32_t* __restrict__ N, int64_t R, int64_t nqmax, int64_t* __restrict__ boff,
+                     int32_t* __restrict__ NQ) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t w = nqmax > 0 ? nqmax : 1;
+  if (i >= R * w) return;
+  const int64_t r = i / w, j = i % w;
+  if (j == 0) NQ[r] = max(N[r] - LAG, 0) / BLK;
+  if (nqmax > 0) {
+    const int64_t tok0 = j * BLK;
+    boff[r * nqmax + j] = (int64_t)qbt[r * qbt_stride + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
+  }
+}
+
+}  // namespace
+}  // namespace kv800
+
+using namespace kv800;
+
+extern "C" {
+
+int kv800_hip_write_exact(uint16_t* epool, int64_t s0, int64_t s1, int64_t s2, int64_t e_v, int64_t ebs,
+                          const int64_t* slot, const uint16_t* k, const uint16_t* v, int64_t R, const int64_t* pos,
+                          uint16_t* sk, uint16_t* sv, const int64_t* skoff, const int64_t* svoff, void* stream) {
+  KV800_REQUIRE(R >= 0, "write_exact: R < 0");
+  if (R == 0) return KV800_OK;
+  KV800_REQUIRE(epool && slot && k && v, "write_exact: null pointer");
+  KV800_REQUIRE(ebs > 0 && s0 % 8 == 0 && s1 % 8 == 0 && s2 % 8 == 0 && e_v % 8 == 0,
+                "write_exact: strides must be multiples of 8 elements and ebs > 0");
+  KV800_REQUIRE(((uintptr_t)epool % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0,
+                "write_exact: epool, k and v must be 16-byte aligned");
+  const int nsink = sk ? NSINK : 0;
+  KV800_REQUIRE(!nsink || (sv && pos && skoff && svoff && ((uintptr_t)sk % 16) == 0 && ((uintptr_t)sv % 16) == 0),
+                "write_exact: sinks need sv, pos, skoff, svoff and 16-byte aligned sink buffers");
+  KV800_REQUIRE(R * 128 <= 0x7FFFFFFFLL * 256, "write_exact: R too large");
+  hipLaunchKernelGGL(write_exact_kernel, dim3((unsigned)((R * 128 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     epool, s0, s1, s2, e_v, ebs, slot, k, v, R, pos, sk, sv, skoff, svoff, nsink);
+  return check_launch("write_exact");
+}
+
+int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
+                            int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream) {
+  KV800_REQUIRE(R >= 0 && nqmax >= 0, "decode_tables: R and nqmax must be >= 0");
+  if (R == 0) return KV800_OK;
+  KV800_REQUIRE(N && NQ && (!nqmax || (qbt && boff)), "decode_tables: null pointer");
+  KV800_REQUIRE(bsq > 0 && bsq % BLK == 0, "decode_tables: bsq must be a positive multiple of 256");
+  KV800_REQUIRE(!nqmax || (nqmax - 1) * BLK / bsq < qbt_stride, "decode_tables: nqmax exceeds the quant block table");
+  const int64_t n = R * (nqmax > 0 ? nqmax : 1);
+  KV800_REQUIRE(n <= 0x7FFFFFFFLL * 256, "decode_tables: table too large");
+  hipLaunchKernelGGL(decode_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qbt,
+                     qbt_stride, bsq, qs0, N, R, nqmax, boff, NQ);
+  return check_launch("decode_tables");
+}
+
+}  // extern "C"

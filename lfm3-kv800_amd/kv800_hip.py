@@ -56,6 +56,9 @@ SIGNATURES = {
                                             _I64, _F32, _VP]),
     "kv800_hip_decode_sized": (_I32, [ctypes.POINTER(Paged), _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP, _VP,
                                       _I64, _I64, _VP]),
+    "kv800_hip_write_exact": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP, _VP,
+                                     _VP]),
+    "kv800_hip_decode_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _VP, _VP, _VP]),
 }
 
 
@@ -165,6 +168,44 @@ def flush(epool, eoff, ebs, e_hs, e_ts, e_v, qpool, qbt, bsq, qs0, nq_prev, nq_n
     _check(L.kv800_hip_flush(_ptr(epool), _ptr(eoff), eoff.stride(0), int(ebs), int(e_hs), int(e_ts), int(e_v),
                              _ptr(qpool), _ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(nq_prev), _ptr(nq_new),
                              R, int(max_new), _stream(dev)))
+
+
+def write_exact(ev, slot, k, v, pos=None, sk=None, sv=None, skoff=None, svoff=None):
+    """Write the step's rows k, v (R, 4, 128) bf16 (pre-RoPE K, unrotated V) into the exact cache ev ([pages, 4, ebs,
+    256] bf16 view, K | V) at slot (R,) int64 (< 0: skipped); with sink buffers (window layers) rows at pos < 4 also go
+    to sk + skoff[r] / sv + svoff[r] (bf16 element offsets). One launch (vllm_attn.py:263-291)."""
+    L = ops()
+    dev = ev.device
+    _need(ev, "ev", torch.bfloat16, dev); _need(slot, "slot", torch.int64, dev)
+    k, v = k.contiguous(), v.contiguous()
+    _need(k, "k", torch.bfloat16, dev); _need(v, "v", torch.bfloat16, dev)
+    R = slot.shape[0]
+    if k.shape != (R, 4, 128) or v.shape != (R, 4, 128):
+        raise ValueError(f"k, v must be ({R}, 4, 128), got {tuple(k.shape)}, {tuple(v.shape)}")
+    sinks = sk is not None
+    if sinks:
+        _need(sk, "sk", torch.bfloat16, dev); _need(sv, "sv", torch.bfloat16, dev)
+        _need(pos, "pos", torch.int64, dev); _need(skoff, "skoff", torch.int64, dev); _need(svoff, "svoff", torch.int64, dev)
+    _check(L.kv800_hip_write_exact(_ptr(ev), ev.stride(0), ev.stride(1), ev.stride(2), 128, ev.shape[2], _ptr(slot),
+                                   _ptr(k), _ptr(v), R, _ptr(pos) if sinks else None, _ptr(sk) if sinks else None,
+                                   _ptr(sv) if sinks else None, _ptr(skoff) if sinks else None,
+                                   _ptr(svoff) if sinks else None, _stream(dev)))
+
+
+def decode_tables(qbt, bsq, qs0, N, nqmax):
+    """Quantized layer decode tables (vllm_attn.py:332-340): NQ (R,) int32 and boff (R, max(nqmax, 1)) int64 byte
+    offsets of each row's first nqmax sub-blocks through the (R, blocks) int32 quant block table qbt."""
+    L = ops()
+    dev = N.device
+    _need(qbt, "qbt", torch.int32, dev); _need(N, "N", torch.int32, dev)
+    if qbt.stride(-1) != 1:
+        raise ValueError("qbt rows must be contiguous")
+    R = N.shape[0]
+    boff = torch.empty(R, max(int(nqmax), 1), dtype=torch.int64, device=dev)
+    NQ = torch.empty(R, dtype=torch.int32, device=dev)
+    _check(L.kv800_hip_decode_tables(_ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(N.contiguous()), R, int(nqmax),
+                                     _ptr(boff), _ptr(NQ), _stream(dev)))
+    return boff, NQ
 
 
 def combine(MO, LO, AO, ns):

@@ -1,0 +1,118 @@
+"""Decode step of the 800h attention layers on caches with vLLM's page geometry, without vLLM.
+
+Counterpart of the decode path of the reference's vLLM integration (vllm_attn.py:214-350, KV800Attention.forward for
+decode rows), with the same cache layout so that pages written here are the pages vLLM would hold:
+
+  quantized layers (6, 10, 14, 22): a quant cache of 1280-token pages, 5 x 51,200-byte sub-blocks padded to 262,144 B
+      (vllm_attn.py:36-37, 126-131), block table shared by the four layers (one FullAttention KV group), plus an exact
+      cache of [4 heads, ebs, K128 | V128] bf16 pages (sliding window 640) in the layer's exact KV group;
+  window layers (2, 18): the exact cache only; their 4 sink tokens live in the 6,144-byte aux area at byte 256,000 of
+      the first quant page of the host layers (6, 10) / (14, 22) (vllm_attn.py:3-9, 276-291).
+
+One step of one layer = the step's K / V rows into the exact pages (and sink aux), the flush of the sub-blocks that
+became eligible (n >= 256 j + 384) from this layer's own exact group (the 0.1.1 fix, vllm_attn.py:301), the decode
+tables and the fused decode. Every piece is a launch of libkv800_hip.so on the current stream; the only host values
+are the ones the reference also reads on the host (the rows' sequence lengths, for nqmax and the flush width)."""
+from dataclasses import dataclass, field
+
+import torch
+
+from . import kv800, kv800_hip
+
+QUANT_LAYERS, WINDOW_LAYERS = (6, 10, 14, 22), (2, 18)
+SINK_HOST = {2: (6, 10), 18: (14, 22)}     # window layer -> (layer whose aux holds the sink K, ... the sink V)
+EXACT_WINDOW = 640
+QBLOCK, QPAGE = 1280, 262144
+AUX_BYTES = (QBLOCK // kv800.BLK) * kv800.SUB  # 256,000: start of the aux area in a quant page
+
+
+@dataclass
+class StepMeta:
+    """Per-step metadata of one KV-cache group (the KV800Meta fields the decode path reads, vllm_attn.py:64-75).
+    block_table (R, blocks) int32; slot_mapping (R,) int64 slot of the step's token (-1: none); seq_lens (R,) int32
+    including the step's token; seq_lens_cpu the same on the host; positions (R,) int64. `cache` holds values shared
+    by the layers of the group within the step."""
+    block_table: torch.Tensor
+    slot_mapping: torch.Tensor
+    seq_lens: torch.Tensor
+    seq_lens_cpu: torch.Tensor
+    positions: torch.Tensor
+    cache: dict = field(default_factory=dict)
+
+
+def step_meta(block_table, seq_lens_cpu, ebs, device):
+    """StepMeta of a decode step in which every row appends one token at position seq_len - 1."""
+    sl = seq_lens_cpu.to(torch.int64)
+    pos = (sl - 1).to(device)
+    bt = block_table.to(device=device, dtype=torch.int32)
+    page = bt.gather(1, (pos // ebs)[:, None].long())[:, 0].long()
+    slot = page * ebs + pos % ebs
+    return StepMeta(bt, slot, sl.to(device=device, dtype=torch.int32), sl, pos)
+
+
+class KV800DecodeLayer:
+    """One LFM3 full-attention layer's decode step over its 800h caches. exact: (pages, 4, ebs, 256) bf16 [K | V];
+    quant: (qpages, 262144) uint8 for quantized layers, None for window layers."""
+
+    def __init__(self, layer_idx, exact, quant=None):
+        self.l = layer_idx
+        self.win = layer_idx in WINDOW_LAYERS
+        if self.win == (quant is not None):
+            raise ValueError(f"layer {layer_idx}: window layers take no quant cache, quantized layers need one")
+        if exact.dtype != torch.bfloat16 or exact.dim() != 4 or exact.shape[1] != 4 or exact.shape[3] != 256:
+            raise ValueError("exact cache must be (pages, 4, ebs, 256) bf16")
+        if quant is not None and (quant.dtype != torch.uint8 or quant.dim() != 2 or quant.shape[1] != QPAGE):
+            raise ValueError(f"quant cache must be (pages, {QPAGE}) uint8")
+        self.ev, self.qv = exact, quant
+        self.ebs = exact.shape[2]
+
+    def forward(self, q, k, v, mx: StepMeta, mq: StepMeta = None, hosts=None, cos_t=None, sin_t=None, max_new=1):
+        """q (R, 16, 128) post-RoPE, k (R, 4, 128) pre-RoPE, v (R, 4, 128), all bf16, one decode token per row.
+        mx: this layer's exact-group metadata; mq: the quant group's (quantized layers, and the sink hosts of window
+        layers); hosts: {layer: KV800DecodeLayer} holding the sink hosts' quant caches (window layers); cos_t / sin_t
+        (P, 32) bf16 RoPE tables; max_new: most sub-blocks any row can become eligible for in this step (1 for decode)."""
+        ev, ebs = self.ev, self.ebs
+        s0, s1, s2 = ev.stride(0), ev.stride(1), ev.stride(2)
+        R = q.shape[0]
+        C = mx.cache
+        if self.win:
+            # ---- step rows into the exact window pages, and sink rows into the hosts' aux
+            kh, vh = (hosts[h] for h in SINK_HOST[self.l])
+            skb, svb = kh.qv.view(torch.bfloat16), vh.qv.view(torch.bfloat16)
+            skey = ("sinkoff", self.l)
+            if skey not in mq.cache:
+                page0 = mq.block_table[:, 0].long()
+                mq.cache[skey] = (page0 * skb.stride(0) + AUX_BYTES // 2, page0 * svb.stride(0) + AUX_BYTES // 2)
+            skoff, svoff = mq.cache[skey]
+            kv800_hip.write_exact(ev, mx.slot_mapping, k, v, pos=mx.positions, sk=skb, sv=svb, skoff=skoff, svoff=svoff)
+        else:
+            kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        ekey = ("eoff", s0)
+        if ekey not in C:
+            C[ekey] = (mx.block_table.long() * s0).contiguous()
+        eoff = C[ekey]
+        N = mx.seq_lens
+        if self.win:
+            P = kv800.Paged(qpool=ev, boff=eoff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=skb, sv=svb,
+                            skoff=skoff, svoff=svoff, N=N, NQ=torch.zeros_like(N), nqmax=0, win=kv800.WIN)
+            return kv800_hip.decode(P, q, cos_t, sin_t)
+        # ---- flush the sub-blocks that became eligible this step, from this layer's own exact group
+        qv = self.qv
+        fkey = ("flush", id(mx))
+        if fkey not in mq.cache:
+            prev = mx.seq_lens.to(torch.int64) - 1
+            nq_prev = (torch.clamp(prev - kv800.LAG, min=0) // kv800.BLK).to(torch.int32)
+            nq_new = (torch.clamp(mx.seq_lens.to(torch.int64) - kv800.LAG, min=0) // kv800.BLK).to(torch.int32)
+            mq.cache[fkey] = (nq_prev, nq_new, mq.block_table.long().contiguous())
+        nq_prev, nq_new, qbt64 = mq.cache[fkey]
+        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, qv, qbt64, QBLOCK, QPAGE, nq_prev, nq_new, max_new)
+        # ---- decode tables (shared by the quantized layers of the step) and the fused decode
+        dkey = ("dec",)
+        if dkey not in mq.cache:
+            nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
+            boff, NQ = kv800_hip.decode_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax)
+            mq.cache[dkey] = (boff, NQ, nqmax)
+        boff, NQ, nqmax = mq.cache[dkey]
+        P = kv800.Paged(qpool=qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None, sv=None,
+                        skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
+        return kv800_hip.decode(P, q, cos_t, sin_t)

@@ -1,0 +1,143 @@
+"""One decode step of the vLLM-geometry cache path (lfm3-kv800_amd/vllm_cache.py, the counterpart of
+vllm_attn.py:214-350) on an MI355X, checked against the CPU oracle.
+
+Setup: ragged rows whose step crosses flush boundaries (n = 256 j + 384) on some rows and writes a sink (position < 4)
+on another; exact caches of 128-token pages in two exact KV groups (layers 2, 6 share one block table, layer 10 has
+its own: the 0.1.1 multi-group case), one quant KV group of 1280-token pages for layers 6 and 10, all page tables
+shuffled; window layer 2 keeps its sinks in the aux area of layers 6 (K) and 10 (V). After the step:
+  * the step's K / V rows sit at their slots, and the sink rows in the hosts' aux (bit-exact);
+  * every sub-block that became eligible was flushed from the layer's own exact group, bit-exact with the oracle
+    quantizer, and no other quant sub-block changed;
+  * each layer's decode output is within 2e-2 max-abs / 1e-3 mean-abs of the oracle's torch_decode over a cache built
+    independently from the rows' full K / V history."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+EBS, QBLOCK, QPAGE, AUX = 128, 1280, 262144, 256000
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+
+
+def say(*a):
+    print("[gpu-vllm]", *a, flush=True)
+
+
+def bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bits_of(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_vllm_decode_step(hip, oracle):
+    from lfm3_kv800_amd import vllm_cache as vc
+    rng = np.random.RandomState(77)
+    L0 = np.array([1407, 999, 2, 383, 3000, 1663], np.int64)   # lengths before the step
+    n = L0 + 1
+    R, nmax = len(L0), int(n.max())
+    layers = (2, 6, 10)
+    hist = {l: (oracle.randn_bf16(rng, (R, nmax, 4, 128)), oracle.randn_bf16(rng, (R, nmax, 4, 128))) for l in layers}
+    q = {l: oracle.randn_bf16(rng, (R, 16, 128)) for l in layers}
+    cos, sin = oracle.rope_tables(4096)
+
+    # ---- block tables: exact groups A (layers 2, 6) and B (layer 10), quant group Q (layers 6, 10)
+    epr = nmax // EBS + 1
+    qpr = nmax // QBLOCK + 1
+    bt = {g: rng.permutation(R * epr + 5)[:R * epr].reshape(R, epr).astype(np.int32) for g in "AB"}
+    qbt = rng.permutation(R * qpr + 3)[:R * qpr].reshape(R, qpr).astype(np.int32)
+    group = {2: "A", 6: "A", 10: "B"}
+    nq_prev = np.maximum(L0 - 128, 0) // 256
+    nq_new = np.maximum(n - 128, 0) // 256
+    say("rows", list(n), "flushes", int((nq_new - nq_prev).sum()))
+
+    # ---- caches before the step: history positions [0, L0) in exact pages, sub-blocks j < nq_prev in quant pages
+    exact, quant = {}, {}
+    for l in layers:
+        K, V = hist[l]
+        ep = np.zeros((R * epr + 5, 4, EBS, 256), np.uint16)
+        for r in range(R):
+            for p in range(L0[r]):
+                pg = bt[group[l]][r, p // EBS]
+                ep[pg, :, p % EBS, :128] = K[r, p]
+                ep[pg, :, p % EBS, 128:] = V[r, p]
+        exact[l] = ep
+        if l != 2:
+            qp = np.zeros((R * qpr + 3, QPAGE), np.uint8)
+            for r in range(R):
+                if nq_prev[r]:
+                    sb = oracle.quantize_blocks(K[r, :256 * nq_prev[r]].reshape(-1, 256, 4, 128),
+                                                V[r, :256 * nq_prev[r]].reshape(-1, 256, 4, 128))
+                    for j in range(nq_prev[r]):
+                        off = (256 * j) % QBLOCK // 256 * 51200
+                        qp[qbt[r, 256 * j // QBLOCK], off:off + 51200] = sb[j]
+            quant[l] = qp
+    for r in range(R):                                   # sinks of window layer 2: K in layer 6's aux, V in 10's
+        for p in range(min(4, L0[r])):
+            for host, arr in ((6, hist[2][0]), (10, hist[2][1])):
+                page = quant[host][qbt[r, 0]].view(np.uint16)
+                page[AUX // 2 + p * 512: AUX // 2 + (p + 1) * 512] = arr[r, p].reshape(-1)
+    before = {l: quant[l].copy() for l in quant}
+
+    # ---- the step on the GPU
+    ev = {l: bf16_dev(exact[l]) for l in layers}
+    qv = {l: torch.from_numpy(quant[l]).to(DEV) for l in quant}
+    lay = {l: vc.KV800DecodeLayer(l, ev[l], qv.get(l)) for l in layers}
+    metas = {g: vc.step_meta(torch.from_numpy(bt[g]), torch.from_numpy(n), EBS, DEV) for g in "AB"}
+    mq = vc.step_meta(torch.from_numpy(qbt), torch.from_numpy(n), QBLOCK, DEV)
+    cos_d, sin_d = bf16_dev(cos), bf16_dev(sin)
+    outs = {}
+    for l in layers:
+        K, V = hist[l]
+        kn = bf16_dev(np.stack([K[r, L0[r]] for r in range(R)]))
+        vn = bf16_dev(np.stack([V[r, L0[r]] for r in range(R)]))
+        say("layer", l)
+        outs[l] = bits_of(lay[l].forward(bf16_dev(q[l]), kn, vn, metas[group[l]], mq, hosts=lay, cos_t=cos_d,
+                                         sin_t=sin_d))
+    torch.cuda.synchronize()
+
+    # ---- writes, sinks and flushes
+    for l in layers:
+        K, V = hist[l]
+        ep = bits_of(ev[l]).reshape(exact[l].shape)
+        for r in range(R):
+            p = L0[r]
+            pg = bt[group[l]][r, p // EBS]
+            assert np.array_equal(ep[pg, :, p % EBS, :128], K[r, p]) and np.array_equal(ep[pg, :, p % EBS, 128:], V[r, p])
+    for host, arr in ((6, hist[2][0]), (10, hist[2][1])):
+        qb = qv[host].cpu().numpy()
+        for r in range(R):
+            if L0[r] < 4:
+                page = qb[qbt[r, 0]].view(np.uint16)
+                assert np.array_equal(page[AUX // 2 + L0[r] * 512: AUX // 2 + (L0[r] + 1) * 512], arr[r, L0[r]].reshape(-1))
+    for l in (6, 10):
+        K, V = hist[l]
+        qb = qv[l].cpu().numpy()
+        changed = set()
+        for r in range(R):
+            for j in range(nq_prev[r], nq_new[r]):
+                want = oracle.quantize_blocks(K[r, 256 * j:256 * j + 256][None], V[r, 256 * j:256 * j + 256][None])[0]
+                off = (256 * j) % QBLOCK // 256 * 51200
+                assert np.array_equal(qb[qbt[r, 256 * j // QBLOCK], off:off + 51200], want), (l, r, j)
+                changed.add((int(qbt[r, 256 * j // QBLOCK]), off))
+        qb2 = qb.copy()
+        for pg, off in changed:
+            qb2[pg, off:off + 51200] = before[l][pg, off:off + 51200]
+        qb2[:, AUX:] = before[l][:, AUX:]                  # the aux may hold this step's sinks
+        assert np.array_equal(qb2, before[l]), l
+
+    # ---- decode against the oracle on an independently built cache of the full history
+    for l in layers:
+        K, V = hist[l]
+        case = oracle.build_paged(lambda b, p0, p1: (K[b, p0:p1], V[b, p0:p1]), list(n), win=256 if l == 2 else 0,
+                                  ebs=EBS, shuffle_seed=l)
+        want = oracle.decode(case, q[l], cos, sin)
+        o = torch.from_numpy(outs[l].view(np.int16)).view(torch.bfloat16).float().numpy()
+        w = torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()
+        d = np.abs(o - w)
+        say(f"layer {l}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert np.isfinite(o).all()
+        assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
