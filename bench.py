@@ -5,11 +5,13 @@ tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--calib]
 
-A step = one kv800.decode call (decode_quant + decode_exact + decode_merge kernels) over one layer. Inputs are
-resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one JSON line.
-roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average duration, timed
-with HIP events on its own stream; cpu_baseline: the CPU oracle (a C restatement of torch_decode.py) on a bounded
-sample of the same workload. --calib runs a plain copy of known size instead (for rocprof FETCH/WRITE calibration)."""
+A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
+Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
+JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
+duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
+cpu_baseline: the CPU oracle (a C restatement of torch_decode.py) on a bounded sample of the same workload. Extra
+fields: flush_c2 (the flush kernel alone) and c4 (config 4, one decode step of all 6 attention
+layers over 398 ragged sequences). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
 import argparse
 import json
 import os
@@ -118,6 +120,80 @@ def bench_flush_c2(torch, kh, dev, steps, warmup):
             "ms": round(ms, 5), "bytes": C2_READ + C2_WRITE, "gbps": round(gbps, 1),
             "hbm_frac": round(gbps / HBM_PEAK_GBS, 4), "bound": "valu",
             "fma_per_launch": C2_FMA, "fma_frac": round(C2_FMA / (ms * 1e-3) / FMA_PEAK, 4)}
+
+
+C4_R, C4_MIN, C4_MAX = 398, 1024, 32768
+C4_GROUP = {6: "A", 14: "A", 22: "A", 2: "B", 10: "B", 18: "B"}   # two exact KV groups of three layers
+
+
+def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
+    """the 6 attention layers of an LFM3-1.7B-shaped stack (quantized 6, 10, 14, 22; window + sinks
+    2, 18) over 398 sequences with lengths U[1K, 32K] (seeded), vLLM page geometry (exact: 128-token pages in two exact
+    KV groups; quant: 1280-token pages in one group, sinks in the hosts' aux), one decode step per layer per step:
+    the new token's rows, the flush of the sub-blocks that became eligible, decode tables and decode
+    (lfm3-kv800_amd/vllm_cache.py). Quant pages are filled from a pool of sub-blocks quantized from N(0,1) bf16 K / V;
+    exact pages, sinks and q / k / v are N(0,1)."""
+    import numpy as np
+    from lfm3_kv800_amd import vllm_cache as vc
+    g = torch.Generator(device=dev).manual_seed(41)
+    L0 = np.random.RandomState(41).randint(C4_MIN, C4_MAX + 1, size=C4_R).astype(np.int64)
+    nmax = int(L0.max()) + steps + warmup + 1
+    ebs, qb = 128, vc.QBLOCK
+    epr, qpr = nmax // ebs + 1, nmax // qb + 1
+    gc = torch.Generator().manual_seed(41)
+    bt = {grp: torch.randperm(C4_R * epr, generator=gc).view(C4_R, epr).to(torch.int32) for grp in "AB"}
+    n_ep = C4_R * epr
+    qperm = torch.randperm(C4_R * qpr, generator=gc).view(C4_R, qpr).to(torch.int32)
+    # a pool of real sub-blocks, copied into every quant page slot
+    pool = kh.quantize_blocks(torch.randn(256, 256, 4, 128, generator=g, device=dev).to(torch.bfloat16),
+                              torch.randn(256, 256, 4, 128, generator=g, device=dev).to(torch.bfloat16))
+    layers = {}
+    for l in (2, 6, 10, 14, 18, 22):
+        ev = torch.randn(n_ep, 4, ebs, 256, generator=g, device=dev).to(torch.bfloat16)
+        qv = None
+        if l not in vc.WINDOW_LAYERS:
+            qv = torch.empty(C4_R * qpr, vc.QPAGE, dtype=torch.uint8, device=dev)
+            pick = torch.randint(0, pool.shape[0], (C4_R * qpr * 5,), generator=g, device=dev)
+            qv[:, :vc.AUX_BYTES].view(-1, 5, 51200).copy_(pool[pick].view(-1, 5, 51200))
+            qv[:, vc.AUX_BYTES:].view(torch.bfloat16).copy_(
+                torch.randn(C4_R * qpr, (vc.QPAGE - vc.AUX_BYTES) // 2, generator=g, device=dev))
+        layers[l] = vc.KV800DecodeLayer(l, ev, qv)
+    qkv = {l: (torch.randn(C4_R, 16, 128, generator=g, device=dev).to(torch.bfloat16),
+               torch.randn(C4_R, 4, 128, generator=g, device=dev).to(torch.bfloat16),
+               torch.randn(C4_R, 4, 128, generator=g, device=dev).to(torch.bfloat16)) for l in layers}
+    torch.cuda.synchronize()
+    # per-step metadata (slot mapping, lengths, device block tables) is the scheduler's input; it is built before the
+    # timed steps, as vLLM builds it on the host while the previous step runs on the GPU
+    metas = []
+    for i in range(warmup + steps):
+        lens = torch.from_numpy(L0 + 1 + i)
+        metas.append(({grp: vc.step_meta(bt[grp], lens, ebs, dev) for grp in "AB"}, vc.step_meta(qperm, lens, qb, dev)))
+    torch.cuda.synchronize()
+
+    def step(i):
+        me, mq = metas[i]
+        for l in (2, 6, 10, 14, 18, 22):
+            q, k, v = qkv[l]
+            layers[l].forward(q, k, v, me[C4_GROUP[l]], mq, hosts=layers, cos_t=cos, sin_t=sin)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    # algorithmic bytes of one step (the reference's accounting), at the mean step length
+    nmid = L0 + 1 + warmup + steps // 2
+    nq = np.maximum(nmid - 128, 0) // 256
+    qbytes = int((nq * 51200 + (nmid - 256 * nq) * 2048).sum()) * 4
+    wbytes = int(((np.minimum(4, np.maximum(nmid - 256, 0)) + np.minimum(256, nmid)) * 2048).sum()) * 2
+    gbps = (qbytes + wbytes) / (ms * 1e-3) / 1e9
+    return {"workload": "C4: 6 attention layers (4 quantized + 2 window+sinks), 398 seqs, lengths U[1K, 32K], vLLM "
+                        "page geometry, two exact KV groups, new-token write + flush + decode per layer",
+            "ms_per_step": round(ms, 4), "tok_s": round(C4_R / (ms * 1e-3), 1), "bytes_per_step": qbytes + wbytes,
+            "gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBS, 4)}
 
 
 def rope_tables(torch, n, dev):
@@ -245,8 +321,6 @@ def main():
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
 
-    flush_c2 = bench_flush_c2(torch, kh, dev, max(5, min(a.steps, 20)), 2)
-
     achieved = QBYTES / (ms_quant * 1e-3) / 1e9
     layer_gbps = ALG_BYTES / (ms_step * 1e-3) / 1e9
     cpu = None
@@ -256,6 +330,14 @@ def main():
         cpu = {"value": dt * 1e3 * B / rows, "unit": "ms/layer (64x32K, extrapolated from the sample)", "cores": cores,
                "kind": "port", "sample": f"oracle decode of rows 0..{rows - 1} of the 64 x 32768 layer "
                                          f"({dt:.2f} s), scaled by 64/{rows}"}
+
+    # ---- the other BASELINE configs with a GPU workload: C2 (flush alone) and C4 (6-layer decode step)
+    del layers, structs
+    torch.cuda.empty_cache()
+    extra_steps = max(5, min(a.steps, 20))
+    flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
+    cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
+    c4 = bench_c4(torch, kh, dev, extra_steps, 3, cos4, sin4)
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -271,6 +353,7 @@ def main():
                      "traffic": measured_traffic(), "kernel_ms": round(ms_quant, 5), "bytes_per_launch": QBYTES},
         "cpu_baseline": cpu,
         "flush_c2": flush_c2,
+        "c4": c4,
     }
     print(json.dumps(res), flush=True)
 
