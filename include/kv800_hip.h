@@ -98,16 +98,25 @@ int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint
 int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, int64_t B, int64_t ns, uint16_t* out,
                            void* stream);
 
-/* Split plan used by kv800_hip_decode when spb <= 0 (kv800.py:366-367 plans for the reference kernels). */
+/* Fixed-grid split plan, (ns, spb) with about two workgroups per CU, for the staged entry points above
+ * (kv800.py:366-367 plans for the reference kernels). */
 int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb);
 
-/* Workspace bytes kv800_hip_decode needs for B rows, ns splits and rope rows (0 if cs16 is passed in). */
+/* Workspace bytes kv800_hip_decode needs for B rows, ns splits (spb > 0) and rope rows (0 if cs16 is passed in). */
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows);
 
-/* Fused decode of one layer. Replaces kv800.decode's backend body (kv800.py:352-383): plan, [rope table],
- * decode_quant, then the exact tail fused with the split merge (one launch), all on `stream`. cs16 may be NULL
- * (then it is built in the workspace from cos_t / sin_t for the nqmax * 256 rows the quantized kernel reads).
- * spb <= 0: kv800_hip_plan. */
+/* Balanced schedule of kv800_hip_decode (spb <= 0): the batch's sub-blocks laid end to end and cut into `groups`
+ * equal ranges, one workgroup each, so ragged batches keep every CU busy to the end. No reference counterpart (the
+ * reference splits every row into ns fixed splits). plan_balanced: the group count used for spb == 0;
+ * workspace_balanced: the workspace bytes for `groups` groups. */
+int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups);
+int64_t kv800_hip_decode_workspace_balanced(int64_t B, int64_t groups, int64_t rope_rows);
+
+/* Fused decode of one layer. Replaces kv800.decode's backend body (kv800.py:352-383): [rope table], the quantized
+ * work and the exact tail in one grid, then the merge, all on `stream` (window layers: one launch, the exact tail
+ * fused with the merge). cs16 may be NULL (then it is built in the workspace from cos_t / sin_t for the nqmax * 256
+ * rows the quantized kernel reads). spb > 0: fixed grid of ceil(nqmax / spb) splits per row; spb == 0: balanced
+ * schedule with kv800_hip_plan_balanced's groups; spb < 0: balanced schedule with -spb groups. */
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
                      const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream);

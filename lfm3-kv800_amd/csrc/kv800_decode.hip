@@ -81,7 +81,7 @@ struct XLdsT {
   float acc[NW][4][128];               // per wave, row, dim
 };
 
-// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into split slot ns.
+// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into partial slot xslot.
 // MERGE = true : instead merges it with the ns quantized partials of those rows (written before on the same stream)
 //                and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
 // Exact tail of (row b, KV head h) by a workgroup of NW waves (the standalone kernel, or the exact-tail workgroups of
@@ -91,7 +91,7 @@ __device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int 
                                            const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
                                            const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems,
                                            int64_t sink_elems, float* __restrict__ mo, float* __restrict__ lo_out,
-                                           float* __restrict__ ao, int ns, float scale, int nsink,
+                                           float* __restrict__ ao, int ns, int64_t xslot, float scale, int nsink,
                                            uint16_t* __restrict__ out) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 128) {
@@ -238,7 +238,7 @@ __device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int 
     o1 += sc * X.acc[ww][r][dd + 1];
   }
   if constexpr (!MERGE) {
-    const int64_t row = ((int64_t)b * (ns + 1) + ns) * 16 + h * 4 + r;
+    const int64_t row = xslot * 16 + h * 4 + r;
     if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
     ao[row * 128 + dd] = o0;
     ao[row * 128 + dd + 1] = o1;
@@ -304,12 +304,14 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
                     int nsink, uint16_t* __restrict__ out) {
   __shared__ XLdsT<XW> X;
-  exact_body<XW, MERGE>(X, blockIdx.x >> 2, blockIdx.x & 3, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
-                        lo_out, ao, ns, scale, nsink, out);
+  const int b = blockIdx.x >> 2;
+  exact_body<XW, MERGE>(X, b, blockIdx.x & 3, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo_out, ao, ns,
+                        (int64_t)b * (ns + 1) + ns, scale, nsink, out);
 }
 
 // ---------------------------------------------------------------- quantized sub-blocks
 constexpr int QWAVES = 4;
+constexpr int64_t BAL_CHUNK = 16, BAL_GROUPS = 1536;   // balanced schedule: sub-blocks per workgroup, most workgroups
 // LDS row strides are padded (132 floats, 272 floats, 9 x 16 bytes) so that the 16 lanes of a lane group, which read
 // 16 different rows at the same column, fall into distinct banks; the vb chunk is XOR-swizzled instead (below).
 constexpr int QROW = 132, HROW = 132, VROW = 272, CSP = 9;
@@ -376,25 +378,93 @@ struct ExactArgs {
   const uint16_t* cos_t;
   const uint16_t* sin_t;
   int64_t rope_rows, epool_elems, sink_elems;
+  int64_t xs0, xst;   // exact partial of row b in slot xs0 + b xst
   int nexact, nsink;
 };
+
+// Balanced schedule (groups > 0): the B rows' sub-blocks in quads of 4 (one per wave; a row's last quad may be
+// partial), laid end to end: row b's quads at flat indices [pre[b], pre[b + 1]), T = pre[B] in all. Workgroup g takes
+// flat indices [g C, g C + C) with C = ceil(T / groups), one partial per row it touches, in slot b + g (distinct for
+// every (row, workgroup) pair, since both only grow along the flat order). The exact partial of row b is slot
+// B + groups + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact partial
+// in slot b (ns + 1) + ns (the reference's partial layout).
+struct Sched {
+  int32_t* pre;         // pre[0 .. B]: written by workgroup 0 of the decode grid, read by the merge
+  int groups, B, cap;   // cap: sub-blocks per row are clamped to [0, cap]
+};
+__device__ __forceinline__ int sched_chunk(const Sched& S, int T) { return (T + S.groups - 1) / S.groups; }
+
+// The decode grid's workgroups each scan NQ themselves (thread t owns rows [t k, t k + k), k = ceil(B / 256)) and keep
+// the offsets of RTAB + 1 consecutive rows, from the row holding the flat index they work on, in a small LDS table.
+constexpr int RTAB = 64;
+struct RowTab {
+  int pre[RTAB + 1];   // pre[b0 + i]
+  int b0;
+  int wsum[4];
+};
+__device__ __forceinline__ int row_quads(const int32_t* __restrict__ nq, int r, int cap) {
+  return (min(max(nq[r], 0), cap) + QWAVES - 1) / QWAVES;
+}
+// Returns T; *base = the flat offset of this thread's first row.
+__device__ __forceinline__ int scan_rows(const int32_t* __restrict__ nq, const Sched& S, RowTab& R, int* base) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
+  int sum = 0;
+  for (int r = r0; r < r1; ++r) sum += row_quads(nq, r, S.cap);
+  int v = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  if (lane == 63) R.wsum[w] = v;
+  __syncthreads();
+  int add = 0;
+  for (int ww = 0; ww < w; ++ww) add += R.wsum[ww];
+  *base = add + v - sum;
+  return R.wsum[0] + R.wsum[1] + R.wsum[2] + R.wsum[3];
+}
+// pre[0 .. B] to global memory (workgroup 0; the merge reads it after the grid).
+__device__ __forceinline__ void write_rows(const int32_t* __restrict__ nq, const Sched& S, int base) {
+  const int tid = threadIdx.x, k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
+  int p = base;
+  if (tid == 0) S.pre[0] = 0;
+  for (int r = r0; r < r1; ++r) {
+    p += row_quads(nq, r, S.cap);
+    S.pre[r + 1] = p;
+  }
+}
+// R.b0 = the row holding flat index f (f < T), R.pre[i] = pre[b0 + i] for b0 + i <= B, i <= RTAB.
+__device__ __forceinline__ void fill_rows(const int32_t* __restrict__ nq, const Sched& S, RowTab& R, int base, int f) {
+  const int tid = threadIdx.x, k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
+  __syncthreads();   // earlier readers of R are done
+  int p = base;
+  for (int r = r0; r < r1; ++r) {
+    const int qd = row_quads(nq, r, S.cap);
+    if (p <= f && f < p + qd) R.b0 = r;   // exactly one row
+    p += qd;
+  }
+  __syncthreads();
+  const int b0 = R.b0;
+  p = base;
+  for (int r = r0; r < r1; ++r) {
+    if (r >= b0 && r - b0 <= RTAB) R.pre[r - b0] = p;
+    p += row_quads(nq, r, S.cap);
+  }
+  if (tid == 255 && S.B - b0 <= RTAB) R.pre[S.B - b0] = p;   // thread 255 ends at T = pre[B]
+  __syncthreads();
+}
 static_assert(sizeof(XLdsT<QWAVES>) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
 
-__global__ void __launch_bounds__(256, 2)
-decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
-                    const int64_t* __restrict__ boff, int64_t bstride, const int32_t* __restrict__ nq,
-                    const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
-                    float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale, ExactArgs X) {
-  __shared__ __align__(16) char lds_raw[sizeof(QLds)];
-  if ((int)blockIdx.x < X.nexact) {
-    exact_body<QWAVES, false>(*reinterpret_cast<XLdsT<QWAVES>*>(lds_raw), blockIdx.x >> 2, blockIdx.x & 3, X.P, q,
-                              X.cos_t, X.sin_t, X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns, scale,
-                              X.nsink, nullptr);
-    return;
-  }
+// Attention of row b's 16 query rows over its sub-blocks [j0, j1): wave w takes j0 + w, then every 4th.
+// The workgroup's partial (m, l, acc in the Hadamard domain) goes to partial rows prow .. prow + 15.
+__device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __restrict__ q,
+                                           const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
+                                           const int64_t* __restrict__ boff, int64_t bstride,
+                                           const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
+                                           float* __restrict__ lo_out, float* __restrict__ ao, float scale, const int b,
+                                           const int j0, const int j1, const int64_t prow) {
   QLds& L = *reinterpret_cast<QLds*>(lds_raw);
-  const int blk = (int)blockIdx.x - X.nexact;
-  const int b = blk / ns, s = blk % ns;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
@@ -411,9 +481,6 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  int j1 = min((s + 1) * spb, nq[b]);
-  if (j1 > bstride) j1 = (int)bstride;
-  const int j0 = s * spb;
   for (int jb = j0 + w; jb < j1; jb += QWAVES) {
     const int64_t base = boff[(int64_t)b * bstride + jb];
     if (base < 0 || base + SUB > qpool_bytes || (int64_t)(jb + 1) * BLK > rope_rows) continue;   // guard
@@ -491,9 +558,9 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     // table part (all 16 rows, dense): lane (g, n) channels 16 kk + 4 g .. + 3, features (cos, sin)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const int j0 = 16 * kk + 4 * g;
-      const float4 q0 = *reinterpret_cast<const float4*>(qn + j0), q2 = *reinterpret_cast<const float4*>(qn + 64 + j0);
-      const float4 T0 = *reinterpret_cast<const float4*>(tpn + j0), T2 = *reinterpret_cast<const float4*>(tpn + 64 + j0);
+      const int jc = 16 * kk + 4 * g;
+      const float4 q0 = *reinterpret_cast<const float4*>(qn + jc), q2 = *reinterpret_cast<const float4*>(qn + 64 + jc);
+      const float4 T0 = *reinterpret_cast<const float4*>(tpn + jc), T2 = *reinterpret_cast<const float4*>(tpn + 64 + jc);
       const float a0[4] = {q0.x, q0.y, q0.z, q0.w}, a2[4] = {q2.x, q2.y, q2.z, q2.w};
       const float t0[4] = {T0.x, T0.y, T0.z, T0.w}, t2[4] = {T2.x, T2.y, T2.z, T2.w};
       uint32_t ht[4];
@@ -649,7 +716,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] += sc * F.acc[ww][rr][d0 + e];
   }
-  const int64_t row = ((int64_t)b * (ns + 1) + s) * 16 + rr;
+  const int64_t row = prow + rr;
   if ((tid & 15) == 0) { mo[row] = M; lo_out[row] = Ls; }
   const float pscale = __uint_as_float((uint32_t)(127 + 24 - (d0 >> 4)) << 23);   // 2^(24 - i), plane i = d / 16
   float4 r0, r1;
@@ -659,18 +726,82 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   *reinterpret_cast<float4*>(ao + row * 128 + d0 + 4) = r1;
 }
 
+__global__ void __launch_bounds__(256, 2)
+decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
+                    const int64_t* __restrict__ boff, int64_t bstride, const int32_t* __restrict__ nq,
+                    const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
+                    float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale, ExactArgs X,
+                    Sched S) {
+  __shared__ __align__(16) char lds_raw[sizeof(QLds)];
+  if ((int)blockIdx.x < X.nexact) {
+    const int b = blockIdx.x >> 2;
+    exact_body<QWAVES, false>(*reinterpret_cast<XLdsT<QWAVES>*>(lds_raw), b, blockIdx.x & 3, X.P, q, X.cos_t, X.sin_t,
+                              X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns, X.xs0 + b * X.xst, scale,
+                              X.nsink, nullptr);
+    return;
+  }
+  const int blk = (int)blockIdx.x - X.nexact;
+  if (S.groups == 0) {   // fixed (row, split) grid
+    const int b = blk / ns, s = blk % ns;
+    const int j1 = min(min((s + 1) * spb, nq[b]), (int)min(bstride, (int64_t)INT32_MAX));
+    quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b, s * spb, j1,
+               ((int64_t)b * (ns + 1) + s) * 16);
+    return;
+  }
+  // balanced schedule: flat indices [fw, f1), split at row boundaries
+  __shared__ RowTab R;
+  int base;
+  const int T = scan_rows(nq, S, R, &base);
+  if (blk == 0) write_rows(nq, S, base);
+  if (T <= 0) return;
+  const int C = sched_chunk(S, T);
+  const int fw = (int)min((int64_t)blk * C, (int64_t)T), f1 = min(fw + C, T);
+  if (fw >= f1) return;
+  int f0 = fw;
+  for (bool more = true; more;) {   // rounds of at most RTAB rows
+    fill_rows(nq, S, R, base, f0);
+    const int b0 = R.b0;
+    int b = b0;
+    more = false;
+    for (;;) {
+      const int pb = R.pre[b - b0], e = min(f1, R.pre[b + 1 - b0]);
+      const int nqb = min(max(nq[b], 0), S.cap);
+      quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b,
+                 QWAVES * (f0 - pb), min(QWAVES * (e - pb), nqb), ((int64_t)b + blk) * 16);
+      f0 = e;
+      if (f0 >= f1) break;
+      __syncthreads();   // the next span's q stores reuse the LDS the merge above read
+      do { ++b; } while (b + 1 - b0 <= RTAB && R.pre[b + 1 - b0] <= f0);
+      if (b + 1 - b0 > RTAB) { more = true; break; }
+    }
+  }
+}
+
+
 // ---------------------------------------------------------------- split merge
 __global__ void __launch_bounds__(256)
 decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
-                    uint16_t* __restrict__ out) {
+                    Sched S, uint16_t* __restrict__ out) {
   const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
-  const int S = ns + 1;
-  const int64_t r0 = (int64_t)b * S * 16 + r;   // row of split 0; split s adds 16 s
-  float M = NEG_BIG;
-  for (int s0 = 0; s0 < S; s0 += 4) {   // 4 splits at a time, loads issued together
+  // row b's quantized partials: slots first .. first + ns - 1; its exact partial: slot xs
+  int64_t first = (int64_t)b * (ns + 1), xs = first + ns;
+  if (S.groups > 0) {
+    const int p0 = S.pre[b], p1 = S.pre[b + 1];
+    first = 0;
+    ns = 0;
+    if (p1 > p0) {
+      const int C = sched_chunk(S, S.pre[S.B]);
+      first = (int64_t)b + p0 / C;
+      ns = (p1 - 1) / C - p0 / C + 1;
+    }
+    xs = (int64_t)S.B + S.groups + b;
+  }
+  const int64_t r0 = first * 16 + r;   // row of the first quantized partial; the next adds 16
+  float M = mo[xs * 16 + r];
+  for (int s0 = 0; s0 < ns; s0 += 4) {   // 4 partials at a time, loads issued together
     float mv[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) mv[k] = (s0 + k < S) ? mo[r0 + 16 * (s0 + k)] : NEG_BIG;
+    for (int k = 0; k < 4; ++k) mv[k] = (s0 + k < ns) ? mo[r0 + 16 * (s0 + k)] : NEG_BIG;
 #pragma unroll
     for (int k = 0; k < 4; ++k) M = fmaxf(M, mv[k]);
   }
@@ -696,8 +827,8 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
       for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
     }
   }
-  {   // exact split
-    const int64_t row = r0 + 16 * (int64_t)ns;
+  {   // exact partial
+    const int64_t row = xs * 16 + r;
     const float wgt = exp2f(mo[row] - M);
     Ls += wgt * lo[row];
     const float4 a0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
@@ -781,18 +912,21 @@ int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_
 // check_exact).
 int launch_quant(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
                  int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows, float* mo, float* lo,
-                 float* ao, int64_t B, int64_t ns, int64_t spb, float scale, const ExactArgs* xa, void* stream) {
+                 float* ao, int64_t B, int64_t ns, int64_t spb, float scale, const ExactArgs* xa, Sched S,
+                 void* stream) {
   KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
   if (B == 0 || ns == 0) return KV800_OK;
   KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
-  KV800_REQUIRE(B * ns + B * 4 <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
+  const int64_t nwork = S.groups ? S.groups : B * ns;
+  KV800_REQUIRE(nwork + B * 4 <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
   KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
                 "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
   ExactArgs X{};
   if (xa) X = *xa;
   else X.nexact = 0;
-  hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(B * ns + X.nexact)), dim3(256), 0, (hipStream_t)stream, q,
-                     qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale, X);
+  hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(nwork + X.nexact)), dim3(256), 0, (hipStream_t)stream, q,
+                     qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale, X,
+                     S);
   return check_launch(xa ? "decode_quant_exact" : "decode_quant");
 }
 
@@ -832,7 +966,7 @@ int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
                                  void* stream) {
   return launch_quant(q, qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, B, ns, spb, scale,
-                      nullptr, stream);
+                      nullptr, Sched{nullptr, 0, (int)B, 0}, stream);
 }
 
 int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
@@ -860,13 +994,28 @@ int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, in
   if (B == 0) return KV800_OK;
   KV800_REQUIRE(mo && lo && ao && out, "decode_merge: null pointer");
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, out);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns,
+                     Sched{nullptr, 0, (int)B, 0}, out);
   return check_launch("decode_merge");
 }
 
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows) {
   const int64_t S = ns + 1;
   return align256(B * S * 16 * 4) * 2 + align256(B * S * 16 * 128 * 4) + align256(rope_rows * 32 * 4);
+}
+
+int64_t kv800_hip_decode_workspace_balanced(int64_t B, int64_t groups, int64_t rope_rows) {
+  const int64_t S = 2 * B + groups;
+  return align256(S * 16 * 4) * 2 + align256(S * 16 * 128 * 4) + align256((B + 1) * 4) + align256(rope_rows * 32 * 4);
+}
+
+int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
+  KV800_REQUIRE(B >= 0 && nqmax >= 0 && groups, "plan_balanced: bad arguments");
+  // about BAL_CHUNK sub-blocks per workgroup (at most BAL_GROUPS workgroups) at the batch's largest size B * nqmax;
+  // ragged batches hold fewer sub-blocks, and each workgroup then takes proportionally fewer
+  const int64_t want = (B * ((nqmax + QWAVES - 1) / QWAVES) * QWAVES + BAL_CHUNK - 1) / BAL_CHUNK;
+  *groups = want < 1 ? 1 : want > BAL_GROUPS ? BAL_GROUPS : want;
+  return KV800_OK;
 }
 
 int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
@@ -879,43 +1028,71 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   const int64_t nqmax = P->win ? 0 : P->nqmax;
   KV800_REQUIRE(nqmax >= 0, "decode: nqmax < 0");
   KV800_REQUIRE(!nqmax || (P->qpool && P->boff && nqmax <= P->boff_stride), "decode: nqmax exceeds the boff table");
-  int64_t ns = 0, sp = 1;
-  if (nqmax) {
-    if (spb > 0) { sp = spb; ns = (nqmax + sp - 1) / sp; }
-    else if (kv800_hip_plan(B, nqmax, &ns, &sp) != KV800_OK) return KV800_EINVAL;
-  }
   const int64_t rows = nqmax * BLK;
   KV800_REQUIRE(rows <= rope_rows, "decode: rope tables hold %lld rows, the quantized part needs %lld",
                 (long long)rope_rows, (long long)rows);
-  const int64_t need = kv800_hip_decode_workspace(B, ns, cs16 ? 0 : rows);
+  KV800_REQUIRE(((uintptr_t)workspace % 256) == 0, "decode: workspace must be 256-byte aligned");
+  const float scale = (float)(1.4426950408889634 / sqrt(128.0));
+  char* ws = (char*)workspace;
+  int rc;
+  if (!nqmax) {
+    // no quantized part (window layers): exact tail + sinks fused with the merge (one launch writes the bf16 rows)
+    const int64_t need = kv800_hip_decode_workspace(B, 0, 0);
+    KV800_REQUIRE(workspace_bytes >= need, "decode: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                  (long long)need);
+    float* mo = (float*)ws;
+    float* lo = (float*)(ws + align256(B * 16 * 4));
+    float* ao = (float*)(ws + 2 * align256(B * 16 * 4));
+    return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, 0, scale, out, stream);
+  }
+  // spb > 0: fixed (row, split) grid of spb sub-blocks per split; spb == 0: balanced schedule with the library's group
+  // count; spb < 0: balanced schedule with -spb groups
+  Sched S{nullptr, 0, (int)B, (int)nqmax};
+  int64_t ns, sp, slots;
+  if (spb > 0) {
+    sp = spb;
+    ns = (nqmax + sp - 1) / sp;
+    slots = B * (ns + 1);
+  } else {
+    int64_t G = -spb;
+    if (!G && (rc = kv800_hip_plan_balanced(B, nqmax, &G)) != KV800_OK) return rc;
+    KV800_REQUIRE(B * nqmax < 0x7FFFFFFF - G && B < 0x7FFFFFFF / 2 - G, "decode: batch too large for the balanced schedule");
+    S.groups = (int)G;
+    ns = 1;
+    sp = nqmax;
+    slots = 2 * B + G;
+  }
+  const int64_t need = S.groups ? kv800_hip_decode_workspace_balanced(B, S.groups, cs16 ? 0 : rows)
+                                : kv800_hip_decode_workspace(B, ns, cs16 ? 0 : rows);
   KV800_REQUIRE(workspace_bytes >= need, "decode: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
                 (long long)need);
-  KV800_REQUIRE(((uintptr_t)workspace % 256) == 0, "decode: workspace must be 256-byte aligned");
-  const int64_t S = ns + 1;
-  char* ws = (char*)workspace;
   float* mo = (float*)ws;
-  float* lo = (float*)(ws + align256(B * S * 16 * 4));
-  float* ao = (float*)(ws + 2 * align256(B * S * 16 * 4));
-  uint32_t* cst = (uint32_t*)(ws + 2 * align256(B * S * 16 * 4) + align256(B * S * 16 * 128 * 4));
-  const float scale = (float)(1.4426950408889634 / sqrt(128.0));
-  int rc;
-  if (ns) {
-    if (!cs16) {
-      if ((rc = kv800_hip_rope_table(cos_t, sin_t, rows, cst, stream)) != KV800_OK) return rc;
-      cs16 = cst;
-    }
-    // quantized splits and the exact tail in one grid, then the split merge
-    ExactArgs X{};
-    X.P = *P; X.cos_t = cos_t; X.sin_t = sin_t; X.rope_rows = rope_rows; X.epool_elems = epool_elems;
-    X.sink_elems = sink_elems; X.nexact = (int)(B * 4);
-    if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;
-    if ((rc = launch_quant(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo, ao, B, ns, sp,
-                           scale, &X, stream)) != KV800_OK)
-      return rc;
-    return kv800_hip_decode_merge(mo, lo, ao, B, ns, out, stream);
+  float* lo = (float*)(ws + align256(slots * 16 * 4));
+  float* ao = (float*)(ws + 2 * align256(slots * 16 * 4));
+  char* tail = ws + 2 * align256(slots * 16 * 4) + align256(slots * 16 * 128 * 4);
+  if (S.groups) {
+    S.pre = (int32_t*)tail;
+    tail += align256((B + 1) * 4);
   }
-  // no quantized part (window layers): exact tail + sinks fused with the merge (one launch writes the bf16 rows)
-  return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, out, stream);
+  uint32_t* cst = (uint32_t*)tail;
+  if (!cs16) {
+    if ((rc = kv800_hip_rope_table(cos_t, sin_t, rows, cst, stream)) != KV800_OK) return rc;
+    cs16 = cst;
+  }
+  // quantized work and the exact tail in one grid, then the merge
+  ExactArgs X{};
+  X.P = *P; X.cos_t = cos_t; X.sin_t = sin_t; X.rope_rows = rope_rows; X.epool_elems = epool_elems;
+  X.sink_elems = sink_elems; X.nexact = (int)(B * 4);
+  X.xs0 = S.groups ? B + S.groups : ns;
+  X.xst = S.groups ? 1 : ns + 1;
+  if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;
+  if ((rc = launch_quant(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo, ao, B, ns, sp,
+                         scale, &X, S, stream)) != KV800_OK)
+    return rc;
+  KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, S,
+                     out);
+  return check_launch("decode_merge");
 }
 
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,

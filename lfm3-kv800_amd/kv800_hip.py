@@ -49,6 +49,8 @@ SIGNATURES = {
     "kv800_hip_decode_merge": (_I32, [_VP, _VP, _VP, _I64, _I64, _VP, _VP]),
     "kv800_hip_plan": (_I32, [_I64, _I64, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "kv800_hip_decode_workspace": (_I64, [_I64, _I64, _I64]),
+    "kv800_hip_plan_balanced": (_I32, [_I64, _I64, ctypes.POINTER(_I64)]),
+    "kv800_hip_decode_workspace_balanced": (_I64, [_I64, _I64, _I64]),
     "kv800_hip_decode": (_I32, [ctypes.POINTER(Paged), _VP, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _VP]),
     "kv800_hip_decode_quant_sized": (_I32, [_VP, _VP, _I64, _VP, _I64, _VP, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64,
                                             _F32, _VP]),
@@ -289,8 +291,17 @@ def paged_struct(P, B):
     return s, qbytes, _extent(P.epool), sink_elems
 
 
-def decode(P, q, cos_t, sin_t, spb=None, target=None):
-    """q (B, 16, 128) bf16 post-RoPE -> (B, 16, 128) bf16: the fused HIP decode of one layer (kv800_hip_decode)."""
+def plan_balanced(B, nqmax):
+    """Workgroup count of the balanced schedule (kv800_hip_plan_balanced)."""
+    g = ctypes.c_int64()
+    _check(ops().kv800_hip_plan_balanced(B, nqmax, ctypes.byref(g)))
+    return g.value
+
+
+def decode(P, q, cos_t, sin_t, spb=None, target=None, groups=None):
+    """q (B, 16, 128) bf16 post-RoPE -> (B, 16, 128) bf16: the fused HIP decode of one layer (kv800_hip_decode).
+    spb / target (the reference's split overrides, kv800.py:366-367) select the fixed (row, split) grid; otherwise the
+    balanced schedule runs, with `groups` workgroups (default: the library's plan)."""
     L = ops()
     dev = q.device
     _need(q, "q", torch.bfloat16, dev); _need(cos_t, "cos_t", torch.bfloat16, dev); _need(sin_t, "sin_t", torch.bfloat16, dev)
@@ -304,12 +315,20 @@ def decode(P, q, cos_t, sin_t, spb=None, target=None):
     out = torch.empty(B, 16, 128, dtype=torch.bfloat16, device=dev)
     if B == 0:
         return out
-    ns, sp = plan(B, s.nqmax, spb, target)
-    cs16 = rope_table16(cos_t, sin_t) if ns else None
-    wsb = int(L.kv800_hip_decode_workspace(B, ns, 0))
+    cs16 = rope_table16(cos_t, sin_t) if s.nqmax else None
+    if not s.nqmax:
+        arg, wsb = 0, int(L.kv800_hip_decode_workspace(B, 0, 0))
+    elif spb is None and not target:
+        g = int(groups) if groups else plan_balanced(B, s.nqmax)
+        if g < 1:
+            raise ValueError("groups must be >= 1")
+        arg, wsb = -g, int(L.kv800_hip_decode_workspace_balanced(B, g, 0))
+    else:
+        ns, arg = plan(B, s.nqmax, spb, target)
+        wsb = int(L.kv800_hip_decode_workspace(B, ns, 0))
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     _check(L.kv800_hip_decode_sized(ctypes.byref(s), _ptr(q), B, _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], _ptr(cs16),
-                                    qbytes, eelems, selems, _ptr(out), _ptr(ws), wsb, sp if ns else 0, _stream(dev)))
+                                    qbytes, eelems, selems, _ptr(out), _ptr(ws), wsb, arg, _stream(dev)))
     return out
 
 

@@ -50,17 +50,6 @@ def step_meta(block_table, seq_lens_cpu, ebs, device):
     return StepMeta(bt, slot, sl.to(device=device, dtype=torch.int32), sl, pos)
 
 
-def split_size(total, nqmax, target=512):
-    """Sub-blocks per split for a batch with `total` flushed sub-blocks (longest row nqmax): about `target` workgroups'
-    worth of splits (two per CU), a multiple of the 4 waves of a split workgroup. With ragged rows this keeps the
-    longest workgroup near the average instead of at a share of the longest row; the splits of shorter rows that fall
-    past their last sub-block exit at once."""
-    if nqmax <= 0:
-        return 1
-    spb = max(4, -(-total // target))
-    return min((spb + 3) // 4 * 4, max(4, (nqmax + 3) // 4 * 4))
-
-
 class KV800DecodeLayer:
     """One LFM3 full-attention layer's decode step over its 800h caches. exact: (pages, 4, ebs, 256) bf16 [K | V];
     quant: (qpages, 262144) uint8 for quantized layers, None for window layers."""
@@ -120,11 +109,10 @@ class KV800DecodeLayer:
         # ---- decode tables (shared by the quantized layers of the step) and the fused decode
         dkey = ("dec",)
         if dkey not in mq.cache:
-            nq = torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0) // kv800.BLK
-            nqmax = int(nq.max())
+            nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
             boff, NQ = kv800_hip.decode_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax)
-            mq.cache[dkey] = (boff, NQ, nqmax, split_size(int(nq.sum()), nqmax))
-        boff, NQ, nqmax, spb = mq.cache[dkey]
+            mq.cache[dkey] = (boff, NQ, nqmax)
+        boff, NQ, nqmax = mq.cache[dkey]
         P = kv800.Paged(qpool=qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None, sv=None,
                         skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
-        return kv800_hip.decode(P, q, cos_t, sin_t, spb=spb)
+        return kv800_hip.decode(P, q, cos_t, sin_t)

@@ -265,9 +265,12 @@ def test_decode_shuffled_ragged(hip, oracle, win):
     case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, win=win, ebs=128, shuffle_seed=9)
     say("decode ragged", win, lens)
     P = upload(case)
-    for spb in (None, 1, 3):
-        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=spb)
-        close(bits_of(out), oracle.decode(case, q, cos, sin), f"ragged win={win} spb={spb}")
+    want = oracle.decode(case, q, cos, sin)
+    # fixed grids (spb) and balanced schedules: one workgroup over every row, 5 groups (ranges that start and end
+    # inside rows), and more groups than sub-blocks (most workgroups empty)
+    for spb, groups in ((None, None), (1, None), (3, None), (None, 1), (None, 5), (None, 2000)):
+        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=spb, groups=groups)
+        close(bits_of(out), want, f"ragged win={win} spb={spb} groups={groups}")
 
 
 def test_decode_stages_and_merge(hip, oracle):
