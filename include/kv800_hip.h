@@ -138,6 +138,20 @@ int kv800_hip_write_exact(uint16_t* epool, int64_t s0, int64_t s1, int64_t s2, i
 int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
                             int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream);
 
+/* All per-step tables of the quant KV group in one launch: decode_tables' NQ / boff plus, where non-NULL,
+ * NP[r] = max(N[r] - nnew - 128, 0) / 256 (sub-blocks flushed before the step's nnew tokens: the flush range is
+ * [NP, NQ), vllm_attn.py:297-317), qbt64 = qbt as int64 (R, qbt_stride) for kv800_hip_flush, and
+ * aux[r] = qbt[r, 0] * aux_scale + aux_add (the sink aux area of each row's first quant page, vllm_attn.py:276-291). */
+int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
+                          int64_t R, int64_t nqmax, int64_t nnew, int64_t* boff, int32_t* NQ, int32_t* NP,
+                          int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add, void* stream);
+
+/* off[r, p] = bt[r, p] * scale + add for p < npages (off row stride npages): an exact group's (R, bt_stride) int32
+ * block table as element offsets of its pages, the eoff table the decode and flush read (the reference forms it with
+ * torch ops per step, vllm_attn.py:320-323). */
+int kv800_hip_page_offsets(const int32_t* bt, int64_t bt_stride, int64_t R, int64_t npages, int64_t scale, int64_t add,
+                           int64_t* out, void* stream);
+
 /* Bounds-checked forms used by the Python layer. They take the extent of every pool the kernels read, measured from
  * the pointer passed in: qpool_bytes (bytes), epool_elems / sink_elems (bf16 elements), rope_rows (rows of cos_t /
  * sin_t and of cs16). A sub-block, page or row whose offset falls outside its pool is skipped instead of read, so a

@@ -3,10 +3,14 @@
 //   write_exact_kernel   the step's K / V rows into the exact pages through the slot mapping (vllm_attn.py:263-272),
 //                        and, for tokens at positions < 4 of a window layer, into the sink aux area of the host
 //                        layers' first quant page (vllm_attn.py:276-291).
-//   decode_tables_kernel per decode row: NQ = max(N - 128, 0) / 256 flushed sub-blocks and the byte offsets of its
-//                        first nqmax sub-blocks in the quant pool, qbt[r, 256 j / bsq] * qs0 + (256 j % bsq) / 256 *
-//                        51200 (vllm_attn.py:332-340).
-// Both are plain data movement: one thread per 16-byte piece or per table entry, coalesced along the row.
+//   step_tables_kernel   per row of the quant KV group: NQ = max(N - 128, 0) / 256 flushed sub-blocks and the byte
+//                        offsets of its first nqmax sub-blocks in the quant pool, qbt[r, 256 j / bsq] * qs0 +
+//                        (256 j % bsq) / 256 * 51200 (vllm_attn.py:332-340); optionally the sub-blocks flushed before
+//                        the step's nnew tokens (the flush range's start, vllm_attn.py:297-317), the block table as
+//                        int64 and the offsets of the sink aux areas (vllm_attn.py:276-291).
+//   page_offsets_kernel  off[r, p] = bt[r, p] * scale + add: an exact group's block table as element offsets of its
+//                        pages (the eoff table of the decode and flush kernels).
+// All are plain data movement: one thread per 16-byte piece or per table entry, coalesced along the row.
 #include "kv800_common.h"
 #include "../../include/kv800_hip.h"
 
@@ -37,18 +41,33 @@ write_exact_kernel(uint16_t* __restrict__ ep, int64_t s0, int64_t s1, int64_t s2
 }
 
 __global__ void __launch_bounds__(256)
-decode_tables_kernel(const int32_t* __restrict__ qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0,
-                     const int32_t* __restrict__ N, int64_t R, int64_t nqmax, int64_t* __restrict__ boff,
-                     int32_t* __restrict__ NQ) {
+step_tables_kernel(const int32_t* __restrict__ qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0,
+                   const int32_t* __restrict__ N, int64_t R, int64_t nqmax, int64_t nnew, int64_t* __restrict__ boff,
+                   int32_t* __restrict__ NQ, int32_t* __restrict__ NP, int64_t* __restrict__ qbt64,
+                   int64_t* __restrict__ aux, int64_t aux_scale, int64_t aux_add) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t w = nqmax > 0 ? nqmax : 1;
+  const int64_t w = max(max(nqmax, (int64_t)1), qbt64 ? qbt_stride : (int64_t)1);   // entries per row
   if (i >= R * w) return;
   const int64_t r = i / w, j = i % w;
-  if (j == 0) NQ[r] = max(N[r] - LAG, 0) / BLK;
-  if (nqmax > 0) {
+  if (j == 0) {
+    NQ[r] = max(N[r] - LAG, 0) / BLK;
+    if (NP) NP[r] = max(N[r] - (int)nnew - LAG, 0) / BLK;
+    if (aux) aux[r] = (int64_t)qbt[r * qbt_stride] * aux_scale + aux_add;
+  }
+  if (j < nqmax) {
     const int64_t tok0 = j * BLK;
     boff[r * nqmax + j] = (int64_t)qbt[r * qbt_stride + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
   }
+  if (qbt64 && j < qbt_stride) qbt64[r * qbt_stride + j] = qbt[r * qbt_stride + j];
+}
+
+__global__ void __launch_bounds__(256)
+page_offsets_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int64_t R, int64_t npages, int64_t scale,
+                    int64_t add, int64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= R * npages) return;
+  const int64_t r = i / npages, p = i % npages;
+  out[i] = (int64_t)bt[r * bt_stride + p] * scale + add;
 }
 
 }  // namespace
@@ -77,18 +96,41 @@ int kv800_hip_write_exact(uint16_t* epool, int64_t s0, int64_t s1, int64_t s2, i
   return check_launch("write_exact");
 }
 
+int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
+                          int64_t R, int64_t nqmax, int64_t nnew, int64_t* boff, int32_t* NQ, int32_t* NP,
+                          int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add, void* stream) {
+  KV800_REQUIRE(R >= 0 && nqmax >= 0 && nnew >= 0, "step_tables: R, nqmax and nnew must be >= 0");
+  if (R == 0) return KV800_OK;
+  KV800_REQUIRE(N && NQ && (!nqmax || boff) && ((!nqmax && !qbt64 && !aux) || (qbt && qbt_stride > 0)),
+                "step_tables: null pointer");
+  KV800_REQUIRE(bsq > 0 && bsq % BLK == 0, "step_tables: bsq must be a positive multiple of 256");
+  KV800_REQUIRE(!nqmax || (nqmax - 1) * BLK / bsq < qbt_stride, "step_tables: nqmax exceeds the quant block table");
+  KV800_REQUIRE(nnew <= 0x7FFFFFFF, "step_tables: nnew too large");
+  int64_t w = nqmax > 0 ? nqmax : 1;
+  if (qbt64 && qbt_stride > w) w = qbt_stride;
+  const int64_t n = R * w;
+  KV800_REQUIRE(n <= 0x7FFFFFFFLL * 256, "step_tables: table too large");
+  hipLaunchKernelGGL(step_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qbt,
+                     qbt_stride, bsq, qs0, N, R, nqmax, nnew, boff, NQ, NP, qbt64, aux, aux_scale, aux_add);
+  return check_launch("step_tables");
+}
+
 int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
                             int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream) {
-  KV800_REQUIRE(R >= 0 && nqmax >= 0, "decode_tables: R and nqmax must be >= 0");
-  if (R == 0) return KV800_OK;
-  KV800_REQUIRE(N && NQ && (!nqmax || (qbt && boff)), "decode_tables: null pointer");
-  KV800_REQUIRE(bsq > 0 && bsq % BLK == 0, "decode_tables: bsq must be a positive multiple of 256");
-  KV800_REQUIRE(!nqmax || (nqmax - 1) * BLK / bsq < qbt_stride, "decode_tables: nqmax exceeds the quant block table");
-  const int64_t n = R * (nqmax > 0 ? nqmax : 1);
-  KV800_REQUIRE(n <= 0x7FFFFFFFLL * 256, "decode_tables: table too large");
-  hipLaunchKernelGGL(decode_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qbt,
-                     qbt_stride, bsq, qs0, N, R, nqmax, boff, NQ);
-  return check_launch("decode_tables");
+  return kv800_hip_step_tables(qbt, qbt_stride, bsq, qs0, N, R, nqmax, 0, boff, NQ, nullptr, nullptr, nullptr, 0, 0,
+                               stream);
+}
+
+int kv800_hip_page_offsets(const int32_t* bt, int64_t bt_stride, int64_t R, int64_t npages, int64_t scale, int64_t add,
+                           int64_t* out, void* stream) {
+  KV800_REQUIRE(R >= 0 && npages >= 0 && bt_stride >= npages, "page_offsets: need R, npages >= 0, bt_stride >= npages");
+  if (R == 0 || npages == 0) return KV800_OK;
+  KV800_REQUIRE(bt && out, "page_offsets: null pointer");
+  const int64_t n = R * npages;
+  KV800_REQUIRE(n <= 0x7FFFFFFFLL * 256, "page_offsets: table too large");
+  hipLaunchKernelGGL(page_offsets_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, bt,
+                     bt_stride, R, npages, scale, add, out);
+  return check_launch("page_offsets");
 }
 
 }  // extern "C"

@@ -23,8 +23,10 @@
 //       fp16 subnormal bit 2^(i - 24) (one AND per two tokens; MFMA keeps fp16 subnormal inputs exactly), the
 //       weights fp16(p vsc) masked to the head's rows; plane i is scaled back by 2^(24 - i) at the end.
 //     Softmax with a lazy running max (rescale only when a tile max exceeds it by more than 8 log2 units).
-//   decode_exact_kernel one workgroup (8 waves, 64 tokens per wave per pass) per (row b, KV head h): sinks + exact
-//                       positions, SIMT fp32; the fused variant also merges the quantized splits of its 4 rows.
+//   decode_exact_kernel one workgroup per row b, one wave per KV head (the exact-tail workgroups of the quantized
+//                       grid: one per (row, KV head), its 4 waves taking turns over the chunks): sinks + exact
+//                       positions in 32-token chunks (loads one chunk ahead), QK on v_dot2 bf16 pairs, PV fp32; the
+//                       fused variant also merges the quantized splits of its rows.
 //   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT (staged path).
 #include <math.h>
 
@@ -70,39 +72,57 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
   cs16[i] = pk2(bf2f(cos_t[i]), bf2f(sin_t[i]));
 }
 
-// ---------------------------------------------------------------- exact tail + sinks (SIMT)
-constexpr int XW = 8;                  // waves of the standalone exact-tail workgroup (64 tokens per wave per pass)
-template <int NW>
-struct XLdsT {
-  float4 q[128];                       // q rows r = 0..3 of this head at dim d
-  float4 p[NW][64];                    // per wave: softmax weights of rows 0..3 for the chunk's 64 tokens
-  const uint16_t* vrow[NW][64];        // per wave: V row of each token of the chunk (null: masked)
-  float m[NW][4], l[NW][4];            // per wave, per row
-  float acc[NW][4][128];               // per wave, row, dim
+// ---------------------------------------------------------------- exact tail + sinks
+// A workgroup of 4 waves takes NH KV heads of one row b (query rows 4 h .. 4 h + 3 of head h): NH = 4, one wave per
+// head; NH = 1, the 4 waves take the head's 32-token chunks in turn (wave w: chunks w, w + 4, ...) and merge their
+// states at the end. The tokens are the row's sinks, then its exact positions. QK: two lanes per token (lane l: token
+// l % 32, channels j = 16 (l / 32) + e, e < 16, i.e. dims j, j + 32, j + 64, j + 96); the rotated pair (j, j + 64) is
+// rounded to bf16 by one packed convert and dotted with bf16 q pairs on v_dot2 (exact products, fp32 sums), the
+// unrotated pair (j + 32, j + 96) as stored. PV: lane l = dims 2 l, 2 l + 1, fp32. A wave requests its next chunk's
+// K, V and rope rows before computing the current one, and the row's page-table entries sit in LDS, so no load inside
+// the loop waits on another.
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+constexpr int XCH = 32;                // tokens per chunk
+constexpr int XPG = 64;                // page-table entries of the row kept in LDS (later pages are read from memory)
+struct XWaveLds {
+  float4 p[XCH];                       // softmax weights of the chunk's tokens, rows 0..3
+  const uint16_t* vrow[XCH];           // V row of each token of the chunk (masked tokens: row 0 of the exact pool)
 };
+struct XLds {
+  bf2 q[4][32][2][4];                  // head slot, channel j: (q_r[j], q_r[j + 64]) r = 0..3; (q_r[j + 32], q_r[j + 96])
+  XWaveLds wv[4];
+  int64_t pg[XPG];                     // element offsets of the row's exact pages, from page lo_e / ebs on
+  float fm[4][4], fl[4][4];            // NH = 1: each wave's m and l of rows 0..3
+  float facc[4][4][128];               // NH = 1: each wave's accumulators of rows 0..3
+};
+struct XChunk {                        // one chunk's data in registers
+  u4v k[8];                            // K dims 32 qq + 16 hf .. + 15: k[2 qq], k[2 qq + 1]
+  u4v c[2], s[2];                      // cos / sin of channels 16 hf .. + 15
+  uint32_t v[XCH];                     // dims 2 lane, 2 lane + 1 of the chunk's V rows
+  uint32_t vmask;                      // chunk tokens with a V row
+  bool valid;                          // this lane's token has a K row and a rope row
+};
+__device__ __forceinline__ uint32_t u16of(const u4v& a, const u4v& b, int e) {   // 16-bit element e < 16 of (a, b)
+  const u4v& x = e < 8 ? a : b;
+  const uint32_t w = x[(e & 7) >> 1];
+  return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
 
-// MERGE = false: writes the exact partial (m, l, acc) of rows 4 h .. 4 h + 3 into partial slot xslot.
-// MERGE = true : instead merges it with the ns quantized partials of those rows (written before on the same stream)
-//                and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
-// Exact tail of (row b, KV head h) by a workgroup of NW waves (the standalone kernel, or the exact-tail workgroups of
-// the quantized-split grid).
-template <int NW, bool MERGE>
-__device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int h, const kv800_paged_t& P,
-                                           const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
-                                           const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems,
-                                           int64_t sink_elems, float* __restrict__ mo, float* __restrict__ lo_out,
-                                           float* __restrict__ ao, int ns, int64_t xslot, float scale, int nsink,
-                                           uint16_t* __restrict__ out) {
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  if (tid < 128) {
-    float4 a;
-    a.x = bf2f(q[((int64_t)b * 16 + h * 4 + 0) * 128 + tid]);
-    a.y = bf2f(q[((int64_t)b * 16 + h * 4 + 1) * 128 + tid]);
-    a.z = bf2f(q[((int64_t)b * 16 + h * 4 + 2) * 128 + tid]);
-    a.w = bf2f(q[((int64_t)b * 16 + h * 4 + 3) * 128 + tid]);
-    X.q[tid] = a;
-  }
-  __syncthreads();
+// MERGE = false: writes the exact partial (m, l, acc) of the heads' rows into partial slot xslot.
+// MERGE = true : instead merges it with the ns quantized partials of those rows (slots b (ns + 1) + s, written before
+//                on the same stream) and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
+template <int NH, bool MERGE>
+__device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, const kv800_paged_t& P,
+                                          const uint16_t* __restrict__ q,
+                                          const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t,
+                                          int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
+                                          float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao,
+                                          int ns, int64_t xslot, float scale, int nsink, uint16_t* __restrict__ out) {
+  static_assert(NH == 1 || NH == 4, "a workgroup takes one KV head or all four");
+  constexpr int WPH = 4 / NH;          // waves per head
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hf = lane >> 5;
+  const int hl = w / WPH, ph = w % WPH, h = h0 + hl;   // head slot, chunk phase, KV head
+  XWaveLds& W = X.wv[w];
   const int n = P.N[b];
   int lo_e = P.NQ[b] * BLK;
   if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
@@ -110,101 +130,117 @@ __device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int 
   const int cnt = (nsink > 0) ? max(0, min(min(nsink, lo_e), n)) : 0;
   const int T = cnt + max(0, n - lo_e);
   const int64_t* et = P.eoff + (int64_t)b * P.eoff_stride;
+  const int64_t p0 = lo_e / P.ebs;
+  if (tid < XPG) X.pg[tid] = (p0 + tid < P.eoff_stride) ? et[p0 + tid] : -1;
+  if (tid < 64 * NH) {   // q pairs: thread -> head slot tid / 64, channel (tid % 64) / 2, pair kind tid % 2
+    const int hs = tid >> 6, j = (tid & 63) >> 1, o = 32 * (tid & 1);
+    uint32_t pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint16_t* qr = q + ((int64_t)b * 16 + 4 * (h0 + hs) + r) * 128;
+      pr[r] = (uint32_t)qr[j + o] | ((uint32_t)qr[j + o + 64] << 16);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) X.q[hs][j][tid & 1][r] = __builtin_bit_cast(bf2, pr[r]);
+  }
+  const int64_t sko = cnt ? P.skoff[b] : 0, svo = cnt ? P.svoff[b] : 0;
+  __syncthreads();
 
-  // element offset of token i's K row (sink or exact page) and of its V row; -1 if out of range
+  // element offsets of token i's K and V rows (sink or exact page), its position; -1 if out of range
   auto rows = [&](int i, int64_t& ko, int64_t& vo, int& pos) {
     if (i < cnt) {
       pos = i;
-      ko = P.skoff[b] + ((int64_t)i * 4 + h) * 128;
-      vo = P.svoff[b] + ((int64_t)i * 4 + h) * 128;
-      if (ko < 0 || vo < 0 || ko + 128 > sink_elems || vo + 128 > sink_elems) { ko = vo = -1; }
+      ko = sko + ((int64_t)i * 4 + h) * 128;
+      vo = svo + ((int64_t)i * 4 + h) * 128;
+      if (ko < 0 || vo < 0 || ko + 128 > sink_elems || vo + 128 > sink_elems) ko = vo = -1;
     } else {
       pos = lo_e + (i - cnt);
-      const int64_t pg = pos / P.ebs;
-      if (pg >= P.eoff_stride) { ko = vo = -1; return; }
-      ko = et[pg] + h * P.e_hs + (pos % P.ebs) * P.e_ts;
+      const int64_t pg = pos / P.ebs, pi = pg - p0;
+      int64_t base = -1;
+      if (pi < XPG) base = X.pg[pi];
+      else if (pg < P.eoff_stride) base = et[pg];
+      ko = base + h * P.e_hs + (pos - pg * P.ebs) * P.e_ts;
       vo = ko + P.e_v;
-      if (ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) { ko = vo = -1; }
+      if (base < 0 || ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) ko = vo = -1;
     }
   };
-
-  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0}, acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  for (int c0 = 64 * w; c0 < T; c0 += 64 * NW) {
-    asm volatile("" ::: "memory");   // keep the q reads below inside the loop (no 512-register hoist)
-    const int i = c0 + lane;
+  auto load = [&](int c0, XChunk& C) {
+    const int t = c0 + (lane & 31);
     int64_t ko = -1, vo = -1;
     int pos = 0;
-    if (i < T) rows(i, ko, vo, pos);
-    const bool valid = (i < T) && ko >= 0 && pos < rope_rows;
-    const uint16_t* Kb = (i < cnt) ? P.sk : P.epool;
-    // V rows of the chunk's 64 tokens, exchanged through the wave's LDS slots; every lane then requests its two dims of
-    // all 64 rows at once, so these loads overlap the QK work below (masked tokens read row 0 of the exact pool and
-    // are zeroed by vmask)
-    const bool vok = valid && vo >= 0;
-    const uint64_t vmask = __ballot(vok);
-    X.vrow[w][lane] = vok ? ((i < cnt) ? P.sv : P.epool) + vo : P.epool;
-    __builtin_amdgcn_wave_barrier();
-    uint32_t vv[64];
+    if (t < T) rows(t, ko, vo, pos);
+    C.valid = t < T && ko >= 0 && pos < rope_rows;
+    const bool vok = C.valid && vo >= 0;
+    const uint16_t* Kb = (t < cnt) ? P.sk : P.epool;
+    if (lane < 32) W.vrow[lane] = vok ? ((t < cnt) ? P.sv : P.epool) + vo : P.epool;
+    C.vmask = (uint32_t)__ballot(vok);
+    if (C.valid) {
+      const uint16_t* kr = Kb + ko + 16 * hf;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) vv[j] = *reinterpret_cast<const uint32_t*>(X.vrow[w][j] + 2 * lane);
-    float sc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
-      // the token's whole K row and rope row are requested before any of it is used
-      const uint16_t* kr = Kb + ko;
-      u4v kw[16], cw[4], sw[4];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) kw[4 * gq + qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8 * gq);
-        cw[gq] = *reinterpret_cast<const u4v*>(cos_t + (int64_t)pos * 32 + 8 * gq);
-        sw[gq] = *reinterpret_cast<const u4v*>(sin_t + (int64_t)pos * 32 + 8 * gq);
+      for (int qq = 0; qq < 4; ++qq) {
+        C.k[2 * qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq);
+        C.k[2 * qq + 1] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8);
       }
+      const int64_t ro = (int64_t)pos * 32 + 16 * hf;
+      C.c[0] = *reinterpret_cast<const u4v*>(cos_t + ro); C.c[1] = *reinterpret_cast<const u4v*>(cos_t + ro + 8);
+      C.s[0] = *reinterpret_cast<const u4v*>(sin_t + ro); C.s[1] = *reinterpret_cast<const u4v*>(sin_t + ro + 8);
+    }
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const u4v w0 = kw[4 * gq], w1 = kw[4 * gq + 1], w2 = kw[4 * gq + 2], w3 = kw[4 * gq + 3];
-        const u4v c4 = cw[gq], s4 = sw[gq];
-        const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
-        const uint32_t a2[4] = {w2.x, w2.y, w2.z, w2.w}, a3[4] = {w3.x, w3.y, w3.z, w3.w};
-        const uint32_t cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+    for (int j = 0; j < XCH; ++j) C.v[j] = *reinterpret_cast<const uint32_t*>(W.vrow[j] + 2 * lane);
+  };
+
+  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0};
+  float acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  auto compute = [&](const XChunk& C) {
+    float sc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          asm volatile("" ::: "memory");
-          const int j = 8 * gq + e;
-          const uint32_t sh = 16 * (e & 1);
-          const float k0 = bf2f((a0[e >> 1] >> sh) & 0xFFFFu), k1 = bf2f((a1[e >> 1] >> sh) & 0xFFFFu);
-          const float k2 = bf2f((a2[e >> 1] >> sh) & 0xFFFFu), k3 = bf2f((a3[e >> 1] >> sh) & 0xFFFFu);
-          const float cs = bf2f((cc[e >> 1] >> sh) & 0xFFFFu), sn = bf2f((ss[e >> 1] >> sh) & 0xFFFFu);
-          const float kr0 = bfround(__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)));
-          const float kr2 = bfround(__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn)));
-          const float4 qa = X.q[j], qb = X.q[32 + j], qc = X.q[64 + j], qd = X.q[96 + j];
-          sc[0] += qa.x * kr0 + qb.x * k1 + qc.x * kr2 + qd.x * k3;
-          sc[1] += qa.y * kr0 + qb.y * k1 + qc.y * kr2 + qd.y * k3;
-          sc[2] += qa.z * kr0 + qb.z * k1 + qc.z * kr2 + qd.z * k3;
-          sc[3] += qa.w * kr0 + qb.w * k1 + qc.w * kr2 + qd.w * k3;
-        }
+    for (int e = 0; e < 16; ++e) {
+      // the q reads stay next to their use: without the clobber they are loop-invariant and all 128 get hoisted
+      if ((e & 3) == 0) asm volatile("" ::: "memory");
+      const int j = 16 * hf + e;
+      const float k0 = __uint_as_float(u16of(C.k[0], C.k[1], e) << 16);
+      const float k2 = __uint_as_float(u16of(C.k[4], C.k[5], e) << 16);
+      const float cs = __uint_as_float(u16of(C.c[0], C.c[1], e) << 16);
+      const float sn = __uint_as_float(u16of(C.s[0], C.s[1], e) << 16);
+      const bf2 pr = {(__bf16)__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)),
+                      (__bf16)__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn))};
+      const uint32_t pn32 = u16of(C.k[2], C.k[3], e) | (u16of(C.k[6], C.k[7], e) << 16);
+      const bf2 pn = __builtin_bit_cast(bf2, pn32);
+      // q pairs are read from LDS as bf16-pair values: taking them as components of a 4 x uint32 vector and
+      // bit-casting each to a bf16 pair makes this compiler fold the four rows' dot products into row 0's
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = __builtin_amdgcn_fdot2_f32_bf16(X.q[hl][j][0][r], pr, sc[r], false);
+        sc[r] = __builtin_amdgcn_fdot2_f32_bf16(X.q[hl][j][1][r], pn, sc[r], false);
       }
     }
+    // the two channel halves summed outside any branch (a shuffle cannot sink into one, so neither can the dot
+    // products, whose inputs would otherwise all stay live up to the branch)
+    float tot[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tot[r] = sc[r] + __shfl_xor(sc[r], 32);
     float p[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float x = valid ? sc[r] * scale : -INFINITY;
+      const float x = C.valid ? tot[r] * scale : -INFINITY;
       float cm = x;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+      for (int o = 16; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
       const float mn = fmaxf(m[r], cm);
       const float al = exp2f(m[r] - mn);
       m[r] = mn;
-      p[r] = valid ? exp2f(x - mn) : 0.f;
+      p[r] = C.valid ? exp2f(x - mn) : 0.f;
       lsum[r] = lsum[r] * al + p[r];
       acc[r][0] *= al; acc[r][1] *= al;
     }
-    // PV: lane owns dims 2 lane, 2 lane + 1; the chunk's weights are read back from LDS as broadcasts
-    X.p[w][lane] = make_float4(p[0], p[1], p[2], p[3]);
+    if (lane < 32) W.p[lane] = make_float4(p[0], p[1], p[2], p[3]);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      const float4 pp = X.p[w][j];   // zero for masked tokens and tokens past the chunk
-      const uint32_t vj = ((vmask >> j) & 1) ? vv[j] : 0u;
+    for (int t = 0; t < XCH; ++t) {
+      if ((t & 7) == 0) __builtin_amdgcn_sched_barrier(0);   // bounds the weight reads in flight
+      const float4 pp = W.p[t];   // zero for masked tokens and tokens past the row
+      const uint32_t vj = ((C.vmask >> t) & 1u) ? C.v[t] : 0u;
       const float v0 = bf2f_lo(vj), v1 = bf2f_hi(vj);
       acc[0][0] += pp.x * v0; acc[0][1] += pp.x * v1;
       acc[1][0] += pp.y * v0; acc[1][1] += pp.y * v1;
@@ -212,101 +248,134 @@ __device__ __forceinline__ void exact_body(XLdsT<NW>& X, const int b, const int 
       acc[3][0] += pp.w * v0; acc[3][1] += pp.w * v1;
     }
     __builtin_amdgcn_wave_barrier();
+  };
+  constexpr int STEP = WPH * XCH;     // tokens between this wave's chunks
+  if (ph * XCH < T) {
+    XChunk A, Bc;
+    load(ph * XCH, A);
+    for (int c0 = ph * XCH;;) {   // two chunk buffers, each loaded one chunk ahead of its use
+      if (c0 + STEP < T) load(c0 + STEP, Bc);
+      compute(A);
+      c0 += STEP;
+      if (c0 >= T) break;
+      if (c0 + STEP < T) load(c0 + STEP, A);
+      compute(Bc);
+      c0 += STEP;
+      if (c0 >= T) break;
+    }
   }
+
+  // ---- l over the 32 token lanes (both halves hold the same values); lane owns dims 2 lane, 2 lane + 1
+  const int dd = 2 * lane;
+  float Lr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float l = lsum[r];
+    float L = lsum[r];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    if (lane == 0) { X.m[w][r] = m[r]; X.l[w][r] = l; }
-    X.acc[w][r][2 * lane] = acc[r][0];
-    X.acc[w][r][2 * lane + 1] = acc[r][1];
+    for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o);
+    Lr[r] = L;
   }
-  __syncthreads();
-  if (tid >= 256) return;
-  // thread -> (row r = tid / 64, dims 2 (tid % 64), +1)
-  const int r = tid >> 6, dd = 2 * (tid & 63);
-  float M = NEG_BIG;
+  // (m, l, o0, o1) of query row 4 h + r of this row b -> its partial slot, or merged with the quantized partials
+  auto emit = [&](int r, float M, float L, float o0, float o1) {
+    if constexpr (!MERGE) {
+      const int64_t row = xslot * 16 + h * 4 + r;
+      if (lane == 0) { mo[row] = M; lo_out[row] = L; }
+      *reinterpret_cast<float2*>(ao + row * 128 + dd) = make_float2(o0, o1);
+    } else {
+      const int64_t rq = (int64_t)b * (ns + 1) * 16 + h * 4 + r;   // row of split 0; split s adds 16 s
+      // splits are visited 8 at a time with all of their loads issued together
+      float Mq = M;
+      for (int s0 = 0; s0 < ns; s0 += 8) {
+        float mv[8];
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, X.m[ww][r]);
-  float Ls = 0.f, o0 = 0.f, o1 = 0.f;
+        for (int k = 0; k < 8; ++k) mv[k] = (s0 + k < ns) ? mo[rq + 16 * (s0 + k)] : NEG_BIG;
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww) {
-    const float sc = exp2f(X.m[ww][r] - M);
-    Ls += sc * X.l[ww][r];
-    o0 += sc * X.acc[ww][r][dd];
-    o1 += sc * X.acc[ww][r][dd + 1];
-  }
-  if constexpr (!MERGE) {
-    const int64_t row = xslot * 16 + h * 4 + r;
-    if ((tid & 63) == 0) { mo[row] = M; lo_out[row] = Ls; }
-    ao[row * 128 + dd] = o0;
-    ao[row * 128 + dd + 1] = o1;
-  } else {
-    // wave r = row 4 h + r; lane owns dims dd, dd + 1 (same combination as decode_merge_kernel)
-    const int64_t rq = (int64_t)b * (ns + 1) * 16 + h * 4 + r;   // row of split 0; split s adds 16 s
-    // splits are visited 8 at a time with all of their loads issued together
-    float Mq = M;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8];
+        for (int k = 0; k < 8; ++k) Mq = fmaxf(Mq, mv[k]);
+      }
+      const float we = exp2f(M - Mq);
+      float Lt = L * we, x0 = 0.f, x1 = 0.f;
+      for (int s0 = 0; s0 < ns; s0 += 8) {
+        float mv[8], lv[8];
+        float2 av[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) mv[k] = (s0 + k < ns) ? mo[rq + 16 * (s0 + k)] : NEG_BIG;
+        for (int k = 0; k < 8; ++k) {
+          const bool in = s0 + k < ns;
+          const int64_t row = rq + 16 * (in ? s0 + k : 0);
+          mv[k] = in ? mo[row] : NEG_BIG;
+          lv[k] = lo_out[row];
+          av[k] = *reinterpret_cast<const float2*>(ao + row * 128 + dd);
+        }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) Mq = fmaxf(Mq, mv[k]);
-    }
-    const float we = exp2f(M - Mq);
-    float L = Ls * we, x0 = 0.f, x1 = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float mv[8], lv[8];
-      float2 av[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const bool in = s0 + k < ns;
-        const int64_t row = rq + 16 * (in ? s0 + k : 0);
-        mv[k] = in ? mo[row] : NEG_BIG;
-        lv[k] = lo_out[row];
-        av[k] = *reinterpret_cast<const float2*>(ao + row * 128 + dd);
+        for (int k = 0; k < 8; ++k) {
+          const float wq = exp2f(mv[k] - Mq);   // 0 for the padding entries
+          Lt += wq * lv[k];
+          x0 += wq * av[k].x;
+          x1 += wq * av[k].y;
+        }
+      }
+      // y = H x over the 128 dims: bit 0 of the dim in-lane, bits 1..6 across the wave's lanes
+      {
+        const float a = x0, c = x1;
+        x0 = a + c;
+        x1 = a - c;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float wq = exp2f(mv[k] - Mq);   // 0 for the padding entries
-        L += wq * lv[k];
-        x0 += wq * av[k].x;
-        x1 += wq * av[k].y;
+      for (int k = 0; k < 6; ++k) {
+        const int msk = 1 << k;
+        const float p0 = __shfl_xor(x0, msk), p1 = __shfl_xor(x1, msk);
+        x0 = (lane & msk) ? p0 - x0 : x0 + p0;
+        x1 = (lane & msk) ? p1 - x1 : x1 + p1;
       }
+      const float hn = __uint_as_float(0x3DB504F3u);
+      float y0 = (ns > 0 ? x0 * hn : 0.f) + o0 * we;
+      float y1 = (ns > 0 ? x1 * hn : 0.f) + o1 * we;
+      y0 = Lt > 0.f ? y0 / Lt : 0.f;
+      y1 = Lt > 0.f ? y1 / Lt : 0.f;
+      *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
     }
-    // y = H x over the 128 dims: bit 0 of the dim in-lane, bits 1..6 across the wave's lanes
-    {
-      const float a = x0, c = x1;
-      x0 = a + c;
-      x1 = a - c;
-    }
+  };
+  if constexpr (NH == 4) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const int msk = 1 << k;
-      const float p0 = __shfl_xor(x0, msk), p1 = __shfl_xor(x1, msk);
-      x0 = (lane & msk) ? p0 - x0 : x0 + p0;
-      x1 = (lane & msk) ? p1 - x1 : x1 + p1;
+    for (int r = 0; r < 4; ++r) emit(r, m[r], Lr[r], acc[r][0], acc[r][1]);
+  } else {   // the 4 waves' states of each row, merged by wave r for row r
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (lane == 0) { X.fm[w][r] = m[r]; X.fl[w][r] = Lr[r]; }
+      *reinterpret_cast<float2*>(&X.facc[w][r][dd]) = make_float2(acc[r][0], acc[r][1]);
     }
-    const float hn = __uint_as_float(0x3DB504F3u);
-    float y0 = (ns > 0 ? x0 * hn : 0.f) + o0 * we;
-    float y1 = (ns > 0 ? x1 * hn : 0.f) + o1 * we;
-    y0 = L > 0.f ? y0 / L : 0.f;
-    y1 = L > 0.f ? y1 / L : 0.f;
-    *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
+    __syncthreads();
+    const int r = w;
+    float M = NEG_BIG;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, X.fm[ww][r]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float sc = exp2f(X.fm[ww][r] - M);
+      const float2 a = *reinterpret_cast<const float2*>(&X.facc[ww][r][dd]);
+      L += sc * X.fl[ww][r];
+      o0 += sc * a.x;
+      o1 += sc * a.y;
+    }
+    emit(r, M, L, o0, o1);
   }
 }
 
+// KV heads per workgroup of the standalone exact kernel (window layers) and of the exact-tail workgroups of the
+// quantized grid, which must finish early to free their CUs for the split work
+constexpr int XNH = 4, XNH_TAIL = 1;
+
 template <bool MERGE>
-__global__ void __launch_bounds__(64 * XW)
+__global__ void __launch_bounds__(256)
 decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
                     const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
                     int nsink, uint16_t* __restrict__ out) {
-  __shared__ XLdsT<XW> X;
-  const int b = blockIdx.x >> 2;
-  exact_body<XW, MERGE>(X, b, blockIdx.x & 3, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo_out, ao, ns,
-                        (int64_t)b * (ns + 1) + ns, scale, nsink, out);
+  __shared__ XLds X;
+  constexpr int G = 4 / XNH;   // workgroups per row
+  const int b = blockIdx.x / G;
+  exact_row<XNH, MERGE>(X, b, (blockIdx.x % G) * XNH, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
+                        lo_out, ao, ns, (int64_t)b * (ns + 1) + ns, scale, nsink, out);
 }
 
 // ---------------------------------------------------------------- quantized sub-blocks
@@ -370,9 +439,9 @@ __device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn
 }
 static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
 
-// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one
-// (row b, KV head h) (slot ns of the partials, as decode_exact_kernel<false>) before the split workgroups, so their
-// memory latency overlaps the splits' VALU work on the same CUs instead of following it.
+// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one row's
+// KV head(s) (its exact partial slot, as decode_exact_kernel<false>) before the split workgroups, so their memory
+// latency overlaps the splits' VALU work on the same CUs instead of following it.
 struct ExactArgs {
   kv800_paged_t P;
   const uint16_t* cos_t;
@@ -454,7 +523,7 @@ __device__ __forceinline__ void fill_rows(const int32_t* __restrict__ nq, const 
   if (tid == 255 && S.B - b0 <= RTAB) R.pre[S.B - b0] = p;   // thread 255 ends at T = pre[B]
   __syncthreads();
 }
-static_assert(sizeof(XLdsT<QWAVES>) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
+static_assert(sizeof(XLds) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
 
 // Attention of row b's 16 query rows over its sub-blocks [j0, j1): wave w takes j0 + w, then every 4th.
 // The workgroup's partial (m, l, acc in the Hadamard domain) goes to partial rows prow .. prow + 15.
@@ -734,10 +803,11 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
                     Sched S) {
   __shared__ __align__(16) char lds_raw[sizeof(QLds)];
   if ((int)blockIdx.x < X.nexact) {
-    const int b = blockIdx.x >> 2;
-    exact_body<QWAVES, false>(*reinterpret_cast<XLdsT<QWAVES>*>(lds_raw), b, blockIdx.x & 3, X.P, q, X.cos_t, X.sin_t,
-                              X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns, X.xs0 + b * X.xst, scale,
-                              X.nsink, nullptr);
+    constexpr int G = 4 / XNH_TAIL;   // workgroups per row
+    const int b = (int)blockIdx.x / G;
+    exact_row<XNH_TAIL, false>(*reinterpret_cast<XLds*>(lds_raw), b, ((int)blockIdx.x % G) * XNH_TAIL, X.P, q, X.cos_t,
+                               X.sin_t, X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns,
+                               X.xs0 + b * X.xst, scale, X.nsink, nullptr);
     return;
   }
   const int blk = (int)blockIdx.x - X.nexact;
@@ -899,16 +969,16 @@ int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_
   int nsink = 0, rc;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &nsink)) != KV800_OK) return rc;
   if (out)
-    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3((unsigned)(B * 4)), dim3(64 * XW), 0, (hipStream_t)stream, *P, q,
+    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3((unsigned)(B * (4 / XNH))), dim3(256), 0, (hipStream_t)stream, *P, q,
                        cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
   else
-    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3((unsigned)(B * 4)), dim3(64 * XW), 0, (hipStream_t)stream, *P,
+    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3((unsigned)(B * (4 / XNH))), dim3(256), 0, (hipStream_t)stream, *P,
                        q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink,
                        (uint16_t*)nullptr);
   return check_launch(out ? "decode_exact_merge" : "decode_exact");
 }
 
-// Launches the quantized-split grid; xa != null adds the B * 4 exact-tail workgroups (arguments checked by
+// Launches the quantized-split grid; xa != null adds the exact-tail workgroups (arguments checked by
 // check_exact).
 int launch_quant(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
                  int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows, float* mo, float* lo,
@@ -1082,7 +1152,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   // quantized work and the exact tail in one grid, then the merge
   ExactArgs X{};
   X.P = *P; X.cos_t = cos_t; X.sin_t = sin_t; X.rope_rows = rope_rows; X.epool_elems = epool_elems;
-  X.sink_elems = sink_elems; X.nexact = (int)(B * 4);
+  X.sink_elems = sink_elems; X.nexact = (int)(B * (4 / XNH_TAIL));
   X.xs0 = S.groups ? B + S.groups : ns;
   X.xst = S.groups ? 1 : ns + 1;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;

@@ -61,6 +61,9 @@ SIGNATURES = {
     "kv800_hip_write_exact": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP, _VP,
                                      _VP]),
     "kv800_hip_decode_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _VP, _VP, _VP]),
+    "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
+                                     _VP]),
+    "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
 }
 
 
@@ -208,6 +211,40 @@ def decode_tables(qbt, bsq, qs0, N, nqmax):
     _check(L.kv800_hip_decode_tables(_ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(N.contiguous()), R, int(nqmax),
                                      _ptr(boff), _ptr(NQ), _stream(dev)))
     return boff, NQ
+
+
+def step_tables(qbt, bsq, qs0, N, nqmax, nnew=1, aux_scale=None, aux_add=0):
+    """All per-step tables of the quant KV group in one launch (kv800_hip_step_tables): (boff, NQ, NP, qbt64, aux) with
+    NP = sub-blocks flushed before the step's nnew tokens, qbt64 = qbt as int64 and, if aux_scale is given,
+    aux = qbt[:, 0] * aux_scale + aux_add (else None)."""
+    L = ops()
+    dev = N.device
+    _need(qbt, "qbt", torch.int32, dev); _need(N, "N", torch.int32, dev)
+    if qbt.stride(-1) != 1:
+        raise ValueError("qbt rows must be contiguous")
+    R = N.shape[0]
+    boff = torch.empty(R, max(int(nqmax), 1), dtype=torch.int64, device=dev)
+    NQ = torch.empty(R, dtype=torch.int32, device=dev)
+    NP = torch.empty(R, dtype=torch.int32, device=dev)
+    qbt64 = torch.empty(R, qbt.shape[1], dtype=torch.int64, device=dev)
+    aux = torch.empty(R, dtype=torch.int64, device=dev) if aux_scale is not None else None
+    _check(L.kv800_hip_step_tables(_ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(N.contiguous()), R, int(nqmax),
+                                   int(nnew), _ptr(boff), _ptr(NQ), _ptr(NP), _ptr(qbt64), _ptr(aux),
+                                   int(aux_scale or 0), int(aux_add), _stream(dev)))
+    return boff, NQ, NP, qbt64, aux
+
+
+def page_offsets(bt, scale, add=0):
+    """(R, pages) int64 bt * scale + add of an (R, pages) int32 block table (kv800_hip_page_offsets)."""
+    L = ops()
+    dev = bt.device
+    _need(bt, "bt", torch.int32, dev)
+    if bt.dim() != 2 or bt.stride(-1) != 1:
+        raise ValueError("bt must be (R, pages) with contiguous rows")
+    out = torch.empty(bt.shape[0], bt.shape[1], dtype=torch.int64, device=dev)
+    _check(L.kv800_hip_page_offsets(_ptr(bt), bt.stride(0), bt.shape[0], bt.shape[1], int(scale), int(add), _ptr(out),
+                                    _stream(dev)))
+    return out
 
 
 def combine(MO, LO, AO, ns):

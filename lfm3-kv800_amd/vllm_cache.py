@@ -61,10 +61,12 @@ class KV800DecodeLayer:
             raise ValueError(f"layer {layer_idx}: window layers take no quant cache, quantized layers need one")
         if exact.dtype != torch.bfloat16 or exact.dim() != 4 or exact.shape[1] != 4 or exact.shape[3] != 256:
             raise ValueError("exact cache must be (pages, 4, ebs, 256) bf16")
-        if quant is not None and (quant.dtype != torch.uint8 or quant.dim() != 2 or quant.shape[1] != QPAGE):
-            raise ValueError(f"quant cache must be (pages, {QPAGE}) uint8")
+        if quant is not None and (quant.dtype != torch.uint8 or quant.dim() != 2 or quant.shape[1] != QPAGE
+                                  or quant.stride(0) != QPAGE or quant.stride(1) != 1):
+            raise ValueError(f"quant cache must be a contiguous (pages, {QPAGE}) uint8 tensor")
         self.ev, self.qv = exact, quant
         self.ebs = exact.shape[2]
+        self._zeros = None   # NQ = 0 rows of the window decode
 
     def forward(self, q, k, v, mx: StepMeta, mq: StepMeta = None, hosts=None, cos_t=None, sin_t=None, max_new=1):
         """q (R, 16, 128) post-RoPE, k (R, 4, 128) pre-RoPE, v (R, 4, 128), all bf16, one decode token per row.
@@ -74,45 +76,32 @@ class KV800DecodeLayer:
         ev, ebs = self.ev, self.ebs
         s0, s1, s2 = ev.stride(0), ev.stride(1), ev.stride(2)
         R = q.shape[0]
-        C = mx.cache
-        if self.win:
-            # ---- step rows into the exact window pages, and sink rows into the hosts' aux
-            kh, vh = (hosts[h] for h in SINK_HOST[self.l])
-            skb, svb = kh.qv.view(torch.bfloat16), vh.qv.view(torch.bfloat16)
-            skey = ("sinkoff", self.l)
-            if skey not in mq.cache:
-                page0 = mq.block_table[:, 0].long()
-                mq.cache[skey] = (page0 * skb.stride(0) + AUX_BYTES // 2, page0 * svb.stride(0) + AUX_BYTES // 2)
-            skoff, svoff = mq.cache[skey]
-            kv800_hip.write_exact(ev, mx.slot_mapping, k, v, pos=mx.positions, sk=skb, sv=svb, skoff=skoff, svoff=svoff)
-        else:
-            kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        # ---- per-step tables, built once per KV group and shared by its layers: the exact group's page offsets, and
+        # the quant group's decode / flush / sink tables (one launch each)
         ekey = ("eoff", s0)
-        if ekey not in C:
-            C[ekey] = (mx.block_table.long() * s0).contiguous()
-        eoff = C[ekey]
+        if ekey not in mx.cache:
+            mx.cache[ekey] = kv800_hip.page_offsets(mx.block_table, s0)
+        eoff = mx.cache[ekey]
+        if ("step",) not in mq.cache:
+            nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
+            mq.cache[("step",)] = kv800_hip.step_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax, nnew=1,
+                                                        aux_scale=QPAGE // 2, aux_add=AUX_BYTES // 2) + (nqmax,)
+        boff, NQ, NP, qbt64, aux, nqmax = mq.cache[("step",)]
         N = mx.seq_lens
         if self.win:
+            # ---- step rows into the exact window pages, sink rows into the hosts' aux, then the window decode
+            kh, vh = (hosts[h] for h in SINK_HOST[self.l])
+            skb, svb = kh.qv.view(torch.bfloat16), vh.qv.view(torch.bfloat16)
+            kv800_hip.write_exact(ev, mx.slot_mapping, k, v, pos=mx.positions, sk=skb, sv=svb, skoff=aux, svoff=aux)
+            if self._zeros is None or self._zeros.shape[0] < R:
+                self._zeros = torch.zeros(max(R, 64), dtype=torch.int32, device=ev.device)
             P = kv800.Paged(qpool=ev, boff=eoff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=skb, sv=svb,
-                            skoff=skoff, svoff=svoff, N=N, NQ=torch.zeros_like(N), nqmax=0, win=kv800.WIN)
+                            skoff=aux, svoff=aux, N=N, NQ=self._zeros[:R], nqmax=0, win=kv800.WIN)
             return kv800_hip.decode(P, q, cos_t, sin_t)
-        # ---- flush the sub-blocks that became eligible this step, from this layer's own exact group
-        qv = self.qv
-        fkey = ("flush", id(mx))
-        if fkey not in mq.cache:
-            prev = mx.seq_lens.to(torch.int64) - 1
-            nq_prev = (torch.clamp(prev - kv800.LAG, min=0) // kv800.BLK).to(torch.int32)
-            nq_new = (torch.clamp(mx.seq_lens.to(torch.int64) - kv800.LAG, min=0) // kv800.BLK).to(torch.int32)
-            mq.cache[fkey] = (nq_prev, nq_new, mq.block_table.long().contiguous())
-        nq_prev, nq_new, qbt64 = mq.cache[fkey]
-        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, qv, qbt64, QBLOCK, QPAGE, nq_prev, nq_new, max_new)
-        # ---- decode tables (shared by the quantized layers of the step) and the fused decode
-        dkey = ("dec",)
-        if dkey not in mq.cache:
-            nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
-            boff, NQ = kv800_hip.decode_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax)
-            mq.cache[dkey] = (boff, NQ, nqmax)
-        boff, NQ, nqmax = mq.cache[dkey]
-        P = kv800.Paged(qpool=qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None, sv=None,
-                        skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
+        kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        # ---- flush the sub-blocks that became eligible this step ([NP, NQ) per row), from this layer's own exact group
+        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, self.qv, qbt64, QBLOCK, QPAGE, NP, NQ, max_new)
+        # ---- the fused decode
+        P = kv800.Paged(qpool=self.qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None,
+                        sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
         return kv800_hip.decode(P, q, cos_t, sin_t)

@@ -141,3 +141,23 @@ def test_vllm_decode_step(hip, oracle):
         say(f"layer {l}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
         assert np.isfinite(o).all()
         assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
+
+
+def test_step_tables(hip):
+    """kv800_hip_step_tables / kv800_hip_page_offsets against the torch formulas the reference uses per step
+    (vllm_attn.py:276-291, 297-317, 320-340), including rows with no flushed sub-block and a step of 3 new tokens."""
+    g = torch.Generator().manual_seed(5)
+    R, blocks, bsq, qs0 = 7, 9, 1280, 262144
+    qbt = torch.randperm(R * blocks + 4, generator=g)[:R * blocks].view(R, blocks).to(torch.int32)
+    N = torch.tensor([1, 128, 384, 385, 1663, 5000, 11520], dtype=torch.int32)
+    nqmax = int(((N.long() - 128).clamp(min=0) // 256).max())
+    boff, NQ, NP, qbt64, aux = hip.step_tables(qbt.to(DEV), bsq, qs0, N.to(DEV), nqmax, nnew=3, aux_scale=qs0 // 2,
+                                                aux_add=AUX // 2)
+    assert torch.equal(NQ.cpu(), ((N.long() - 128).clamp(min=0) // 256).to(torch.int32))
+    assert torch.equal(NP.cpu(), ((N.long() - 3 - 128).clamp(min=0) // 256).to(torch.int32))
+    sub = torch.arange(nqmax) * 256
+    assert torch.equal(boff.cpu(), qbt[:, sub // bsq].long() * qs0 + ((sub % bsq) // 256) * 51200)
+    assert torch.equal(qbt64.cpu(), qbt.long())
+    assert torch.equal(aux.cpu(), qbt[:, 0].long() * (qs0 // 2) + AUX // 2)
+    eoff = hip.page_offsets(qbt.to(DEV), 131072, 5)
+    assert torch.equal(eoff.cpu(), qbt.long() * 131072 + 5)
