@@ -3,7 +3,7 @@ over 64 sequences x 32,768 tokens (127 quantized 256-token sub-blocks + 256 exac
 tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape; same bytes and flops per token as
 32 / 8 / 64).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--calib]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--calib]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
@@ -237,6 +237,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
+    ap.add_argument("--c3-only", action="store_true", help="skip the C2 / C4 workloads (counter passes of the C3 kernel)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the 800h path shards by "
@@ -335,9 +336,11 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
-    cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
-    c4 = bench_c4(torch, kh, dev, extra_steps, 3, cos4, sin4)
+    flush_c2 = c4 = None
+    if not a.c3_only:
+        flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
+        cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
+        c4 = bench_c4(torch, kh, dev, extra_steps, 3, cos4, sin4)
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
