@@ -121,6 +121,13 @@ int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const
                      const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream);
 
+/* Training fake quantization, the forward value of train.py's straight-through 800h K / V (train.py:82-100), on the
+ * device: fake_quant_k replaces fake_quant_k (x (G, 256, C) fp32 -> c * sc8 + lo8 per (group, channel), bit-identical
+ * to the quantizer's K path); fake_quant_v replaces fake_quant_v (v (N, 4, 128) fp32 -> the V of a quantize ->
+ * dequantize round trip, Hadamard in the quantizer's / dequantizer's fp32 chain). out may not alias the input. */
+int kv800_hip_fake_quant_k(const float* x, int64_t G, int64_t C, float* out, void* stream);
+int kv800_hip_fake_quant_v(const float* v, int64_t N, float* out, void* stream);
+
 /* Step bookkeeping in vLLM's page geometry (exact page [4 heads, ebs, K128 | V128] bf16 with element strides s0 (page),
  * s1 (head), s2 (token); quant page = 5 x 51,200-byte sub-blocks per 1280 tokens, qs0 bytes apart). */
 

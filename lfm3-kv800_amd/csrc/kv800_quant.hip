@@ -383,6 +383,94 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
   }
 }
 
+
+// ---------------------------------------------------------------- training fake quantization (train.py:82-100)
+// fake_quant_k: x (G, 256, C) fp32 -> c * sc8 + lo8 per (group, channel), the K path of the quantizer on fp32 input
+// (the product and the sum rounded separately, as torch's elementwise ops). One thread per channel, 256 channels per
+// workgroup: the 256 tokens are read twice (min / max, then codes; the second pass hits L2), coalesced along C.
+__global__ void __launch_bounds__(256) fake_quant_k_kernel(const float* __restrict__ x, int64_t C,
+                                                           float* __restrict__ out) {
+  const int64_t g = blockIdx.y, c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  const float* xg = x + g * BLK * C + c;
+  float lo = INFINITY, hi = -INFINITY;
+#pragma unroll 8
+  for (int t = 0; t < BLK; ++t) {
+    const float v = xg[(int64_t)t * C];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+  const float lof = f8d(f8e(lo));
+  const float scf = f8d(f8e(clamp_min_1e8(__fdiv_rn(__fsub_rn(hi, lo), 3.0f))));
+  const float den = clamp_min_1e8(scf);
+  float* og = out + g * BLK * C + c;
+#pragma unroll 8
+  for (int t = 0; t < BLK; ++t) {
+    float code = __builtin_rintf(__fdiv_rn(__fsub_rn(xg[(int64_t)t * C], lof), den));
+    code = fminf(fmaxf(code, 0.f), 3.f);
+    og[(int64_t)t * C] = __fadd_rn(__fmul_rn(code, scf), lof);
+  }
+}
+
+// fake_quant_v: v (N, 4, 128) fp32 -> per token y = v H (the quantizer's sequential fma chain), one bit per dim with
+// fp8 lo / scale per pair of heads, then (bit * sc8 + lo8) H with the dequantizer's chain: the V value of a
+// quantize -> dequantize round trip. One wave per token at a time, the token's rows staged in LDS.
+constexpr int FQV_TPW = 8;   // tokens per wave
+__global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restrict__ v, int64_t N,
+                                                           float* __restrict__ out) {
+  __shared__ __align__(16) float xb[4][4][128];   // per wave: the token's 4 rows (v, then the dequantized y)
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float hcol[64];
+  hadamard_column(hcol, lane);
+  float* X = &xb[w][0][0];
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + w) * FQV_TPW;
+#pragma unroll 1
+  for (int tt = 0; tt < FQV_TPW; ++tt) {
+    const int64_t t = t0 + tt;
+    if (t >= N) break;   // uniform over the wave
+    const float4* src = reinterpret_cast<const float4*>(v + t * 512);
+    const float4 a = src[lane], b = src[64 + lane];
+    reinterpret_cast<float4*>(X)[lane] = a;
+    reinterpret_cast<float4*>(X)[64 + lane] = b;
+    __builtin_amdgcn_wave_barrier();
+    float ya[4], yb[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_barrier(0);   // one chain's row reads in flight at a time
+      hadamard_chain(X + r * 128, hcol, ya[r], yb[r]);
+    }
+    float za[4], zb[4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const float lo = wave_min(fminf(fminf(ya[2 * g], yb[2 * g]), fminf(ya[2 * g + 1], yb[2 * g + 1])));
+      const float hi = wave_max(fmaxf(fmaxf(ya[2 * g], yb[2 * g]), fmaxf(ya[2 * g + 1], yb[2 * g + 1])));
+      const float lof = f8d(f8e(lo)), scf = f8d(f8e(clamp_min_1e8(__fsub_rn(hi, lo))));
+      const float den = clamp_min_1e8(scf);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 2 * g + u;
+        const float ba = fminf(fmaxf(__builtin_rintf(__fdiv_rn(__fsub_rn(ya[r], lof), den)), 0.f), 1.f);
+        const float bb = fminf(fmaxf(__builtin_rintf(__fdiv_rn(__fsub_rn(yb[r], lof), den)), 0.f), 1.f);
+        za[r] = __fadd_rn(__fmul_rn(ba, scf), lof);
+        zb[r] = __fadd_rn(__fmul_rn(bb, scf), lof);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();   // every lane has read the v rows
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { X[r * 128 + lane] = za[r]; X[r * 128 + 64 + lane] = zb[r]; }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float oa, ob;
+      __builtin_amdgcn_sched_barrier(0);
+      hadamard_chain(X + r * 128, hcol, oa, ob);
+      out[t * 512 + r * 128 + lane] = oa;
+      out[t * 512 + r * 128 + 64 + lane] = ob;
+    }
+    __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite X
+  }
+}
+
 }  // namespace
 }  // namespace kv800
 
@@ -434,6 +522,29 @@ int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, f
   KV800_REQUIRE(((uintptr_t)k_out % 16) == 0, "dequantize_blocks: k_out must be 16-byte aligned");
   hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, sb, k_out, v_out);
   return check_launch("dequantize_blocks");
+}
+
+int kv800_hip_fake_quant_k(const float* x, int64_t G, int64_t C, float* out, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(G >= 0 && C >= 0, "fake_quant_k: G and C must be >= 0");
+  if (G == 0 || C == 0) return KV800_OK;
+  KV800_REQUIRE(x && out, "fake_quant_k: null pointer");
+  KV800_REQUIRE(G <= 65535 && (C + 255) / 256 <= 0x7FFFFFFF, "fake_quant_k: at most 65535 groups per call");
+  hipLaunchKernelGGL(fake_quant_k_kernel, dim3((unsigned)((C + 255) / 256), (unsigned)G), dim3(256), 0,
+                     (hipStream_t)stream, x, C, out);
+  return check_launch("fake_quant_k");
+}
+
+int kv800_hip_fake_quant_v(const float* v, int64_t N, float* out, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(N >= 0, "fake_quant_v: N < 0");
+  if (N == 0) return KV800_OK;
+  KV800_REQUIRE(v && out, "fake_quant_v: null pointer");
+  KV800_REQUIRE(((uintptr_t)v % 16) == 0, "fake_quant_v: v must be 16-byte aligned");
+  const int64_t nb = (N + 4 * FQV_TPW - 1) / (4 * FQV_TPW);
+  KV800_REQUIRE(nb <= 0x7FFFFFFF, "fake_quant_v: N too large");
+  hipLaunchKernelGGL(fake_quant_v_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, v, N, out);
+  return check_launch("fake_quant_v");
 }
 
 }  // extern "C"

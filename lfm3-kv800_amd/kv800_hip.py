@@ -64,6 +64,8 @@ SIGNATURES = {
     "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
                                      _VP]),
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
+    "kv800_hip_fake_quant_k": (_I32, [_VP, _I64, _I64, _VP, _VP]),
+    "kv800_hip_fake_quant_v": (_I32, [_VP, _I64, _VP, _VP]),
 }
 
 
@@ -244,6 +246,41 @@ def page_offsets(bt, scale, add=0):
     out = torch.empty(bt.shape[0], bt.shape[1], dtype=torch.int64, device=dev)
     _check(L.kv800_hip_page_offsets(_ptr(bt), bt.stride(0), bt.shape[0], bt.shape[1], int(scale), int(add), _ptr(out),
                                     _stream(dev)))
+    return out
+
+
+def fake_quant_k(x):
+    """x (..., 256, C) float32 on the GPU -> float32 dequantized 800h K per (256-token group, channel)
+    (kv800_hip_fake_quant_k; train.py:82-89)."""
+    L = ops()
+    if x.device.type != "cuda":
+        raise ValueError(f"x must be on a ROCm device, got {x.device}")
+    _need(x, "x", torch.float32, x.device)
+    if x.dim() < 2 or x.shape[-2] != 256:
+        raise ValueError(f"x must be (..., 256, C), got {tuple(x.shape)}")
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    C = x.shape[-1]
+    G = x.numel() // (256 * C) if C else 0
+    for g0 in range(0, G, 65535):                       # grid y holds at most 65535 groups
+        g1 = min(G, g0 + 65535)
+        _check(L.kv800_hip_fake_quant_k(ctypes.c_void_p(x.data_ptr() + g0 * 256 * C * 4), g1 - g0, C,
+                                        ctypes.c_void_p(out.data_ptr() + g0 * 256 * C * 4), _stream(x.device)))
+    return out
+
+
+def fake_quant_v(v):
+    """v (..., 4, 128) float32 on the GPU -> float32: per token the V of a quantize -> dequantize round trip
+    (kv800_hip_fake_quant_v; train.py:92-100)."""
+    L = ops()
+    if v.device.type != "cuda":
+        raise ValueError(f"v must be on a ROCm device, got {v.device}")
+    _need(v, "v", torch.float32, v.device)
+    if v.dim() < 2 or tuple(v.shape[-2:]) != (4, 128):
+        raise ValueError(f"v must be (..., 4, 128), got {tuple(v.shape)}")
+    v = v.contiguous()
+    out = torch.empty_like(v)
+    _check(L.kv800_hip_fake_quant_v(_ptr(v), v.numel() // 512, _ptr(out), _stream(v.device)))
     return out
 
 

@@ -11,11 +11,14 @@
  *   - dequantize_blocks (kv800.py:79-92);
  *   - the pure-torch decode (torch_decode.py:16-80): per row dequantize, RoPE of all keys in fp32 rounded to bf16,
  *     one fp32 softmax (scale 1/sqrt(128)), 4 query rows per KV head, bf16 output;
- *   - the split merge `combine` (kv800.py:231-236).
+ *   - the split merge `combine` (kv800.py:231-236);
+ *   - the training fake quantization fake_quant_k / fake_quant_v (train.py:82-100).
  * Pinning (tests/test_oracle.py): fp8 encode exhaustively against torch; quantize_blocks byte-for-byte against a
  * torch statement of kv800.py:56-76 and against the committed golden fixtures; dequantize as the inverse of the
  * packing; decode against an independent float64 restatement of tests/test_parity.py:45-64 (the reference's own
- * independent check) on its 12 cases.
+ * independent check) on its 12 cases; fake_quant_k against a numpy float32 statement of train.py:82-89 and, on bf16
+ * inputs, against the quantize -> dequantize round trip (tests/test_train_hook.py:92-106); fake_quant_v against the
+ * round trip and against a float64 statement of train.py:92-100 away from rounding ties.
  */
 #include <math.h>
 #include <stdint.h>
@@ -200,6 +203,58 @@ void oracle_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* kout, floa
         }
         had_seq(x, H, vo + (t * 4 + h) * 128);
       }
+  }
+}
+
+/* ---------------------------------------------------------------- training fake quant (train.py:82-100) */
+/* x (G, 256, C) fp32 -> out: per (group, channel) code * sc8 + lo8 with the quantizer's K arithmetic (train.py:82-89:
+ * float32 min / max, lo and (hi - lo) / 3 through fp8, IEEE subtract and divide, half-even round, clamp to [0, 3], then
+ * the product and the sum rounded separately). */
+void oracle_fake_quant_k(const float* x, int64_t G, int64_t C, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < G; ++g)
+    for (int64_t c = 0; c < C; ++c) {
+      const float* xg = x + g * BLK * C + c;
+      float lo = INFINITY, hi = -INFINITY;
+      for (int t = 0; t < BLK; ++t) { const float v = xg[t * C]; lo = v < lo ? v : lo; hi = v > hi ? v : hi; }
+      const float lof = oracle_f8_decode(oracle_f8_encode(lo));
+      const float scf = oracle_f8_decode(oracle_f8_encode(clamp_min_1e8((hi - lo) / 3.0f)));
+      const float den = clamp_min_1e8(scf);
+      for (int t = 0; t < BLK; ++t) {
+        float code = rne((xg[t * C] - lof) / den);
+        code = code < 0.f ? 0.f : (code > 3.f ? 3.f : code);
+        const float prod = code * scf;
+        out[g * BLK * C + t * C + c] = prod + lof;
+      }
+    }
+}
+
+/* v (N, 4, 128) fp32 -> per token the V of a quantize -> dequantize round trip (train.py:92-100): y = v @ H by the
+ * sequential chain, one bit per dim over each pair of heads with fp8 lo and scale = hi - lo, then
+ * (bit * sc8 + lo8) @ H by the same chain. */
+void oracle_fake_quant_v(const float* v, int64_t N, float* out) {
+  float H[128 * 128];
+  oracle_hadamard(H);
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < N; ++t) {
+    float y[512], z[512];
+    for (int h = 0; h < 4; ++h) had_seq(v + t * 512 + h * 128, H, y + h * 128);
+    for (int g = 0; g < 2; ++g) {
+      const float* yg = y + g * 256;
+      float* zg = z + g * 256;
+      float lo = INFINITY, hi = -INFINITY;
+      for (int i = 0; i < 256; ++i) { lo = yg[i] < lo ? yg[i] : lo; hi = yg[i] > hi ? yg[i] : hi; }
+      const float lof = oracle_f8_decode(oracle_f8_encode(lo));
+      const float scf = oracle_f8_decode(oracle_f8_encode(clamp_min_1e8(hi - lo)));
+      const float den = clamp_min_1e8(scf);
+      for (int i = 0; i < 256; ++i) {
+        float b = rne((yg[i] - lof) / den);
+        b = b < 0.f ? 0.f : (b > 1.f ? 1.f : b);
+        const float prod = b * scf;
+        zg[i] = prod + lof;
+      }
+    }
+    for (int h = 0; h < 4; ++h) had_seq(z + h * 128, H, out + t * 512 + h * 128);
   }
 }
 

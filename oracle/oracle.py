@@ -5,8 +5,9 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
 
 Python side of oracle/kv800_oracle.c (ctypes) plus numpy helpers:
   * bf16 <-> float32 bit conversion (round to nearest even, as torch .to(bfloat16));
-  * quantize_blocks / dequantize_blocks / decode / combine: the C restatements of kv800.py:56-92, 231-236 and
-    torch_decode.py:16-80 (see the C file's header for what pins each one);
+  * quantize_blocks / dequantize_blocks / decode / combine / fake_quant_k / fake_quant_v: the C restatements of
+    kv800.py:56-92, 231-236, torch_decode.py:16-80 and train.py:82-100 (see the C file's header for what pins each
+    one);
   * build_paged(): a numpy restatement of the paged store of kv800.py:387-441 (exact pages of `ebs` tokens as
     [4 heads, ebs, K 128 | V 128] bf16, 51,200-byte quantized sub-blocks, sinks [4, 4, 128]) with the reference flush
     rule NQ = (n - 128) // 256 (kv800.py:433) and optionally shuffled physical page tables;
@@ -53,6 +54,8 @@ def lib():
         L.oracle_decode.argtypes = [ctypes.POINTER(Paged), i64, vp, vp, vp, vp]
         L.oracle_decode.restype = ctypes.c_int
         L.oracle_combine.argtypes = [vp, vp, vp, i64, i64, vp]
+        L.oracle_fake_quant_k.argtypes = [vp, i64, i64, vp]
+        L.oracle_fake_quant_v.argtypes = [vp, i64, vp]
         L.oracle_f8_encode_n.argtypes = [vp, i64, vp]
         L.oracle_f8_decode_n.argtypes = [vp, i64, vp]
         L.oracle_hadamard.argtypes = [vp]
@@ -115,6 +118,24 @@ def dequantize_blocks(sb):
     k = np.empty((M, BLK, 4, 128), np.uint16); v = np.empty((M, BLK, 4, 128), np.float32)
     lib().oracle_dequantize_blocks(_p(sb), M, _p(k), _p(v))
     return k, v
+
+
+def fake_quant_k(x):
+    """x (..., 256, C) float32 -> float32 dequantized 800h K per (group, channel) (train.py:82-89)."""
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.ndim >= 2 and x.shape[-2] == BLK, x.shape
+    out = np.empty_like(x)
+    lib().oracle_fake_quant_k(_p(x), x.size // (BLK * x.shape[-1]), x.shape[-1], _p(out))
+    return out
+
+
+def fake_quant_v(v):
+    """v (..., 4, 128) float32 -> float32: the V of a quantize -> dequantize round trip per token (train.py:92-100)."""
+    v = np.ascontiguousarray(v, np.float32)
+    assert v.shape[-2:] == (4, 128), v.shape
+    out = np.empty_like(v)
+    lib().oracle_fake_quant_v(_p(v), v.size // 512, _p(out))
+    return out
 
 
 def combine(MO, LO, AO, ns):

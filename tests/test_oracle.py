@@ -176,3 +176,77 @@ def test_oracle_combine():
     ref = (w[:, :ns, :, None] * AO[:, :ns]).sum(1) @ H + w[:, ns, :, None] * AO[:, ns]
     ref = ref / L[..., None]
     assert np.abs(out - ref).max() <= np.abs(ref).max() * 2 ** -7
+
+
+# ---------------------------------------------------------------- training fake quant (train.py:82-100)
+def _fq_k_numpy(oracle, x):
+    """train.py:82-89 restated with numpy float32 ops (independent of the C oracle)."""
+    x = np.asarray(x, np.float32)
+    lo = x.min(axis=-2, keepdims=True); hi = x.max(axis=-2, keepdims=True)
+    lo8 = oracle.f8_decode(oracle.f8_encode(lo))
+    sc8 = oracle.f8_decode(oracle.f8_encode(np.maximum((hi - lo) / np.float32(3), np.float32(1e-8))))
+    c = np.clip(np.rint((x - lo8) / np.maximum(sc8, np.float32(1e-8))), 0, 3).astype(np.float32)
+    return (c * sc8 + lo8).astype(np.float32)
+
+
+def _train_inputs(oracle, seed):
+    """tests/test_train_hook.py:93-96 shapes: K with per-channel scale and offset, V x 2 (bf16 bits)."""
+    rng = np.random.RandomState(seed)
+    k = rng.standard_normal((3, 256, 4, 128)) * rng.rand(1, 1, 4, 128) * 4 + 0.3
+    v = rng.standard_normal((3, 256, 4, 128)) * 2
+    return oracle.f32_to_bf16(k.astype(np.float32)), oracle.f32_to_bf16(v.astype(np.float32))
+
+
+def test_fake_quant_k_numpy_statement(oracle):
+    """C oracle vs the numpy statement on float32 inputs that are not bf16 values, with constant and outlier channels."""
+    rng = np.random.RandomState(3)
+    x = (rng.standard_normal((2, 256, 300)) * rng.rand(1, 1, 300) * 5).astype(np.float32)
+    x[0, :, 7] = 1.25                                 # constant channel: scale clamps to 1e-8
+    x[1, ::17, 11] *= 40                              # outliers
+    assert np.array_equal(oracle.fake_quant_k(x), _fq_k_numpy(oracle, x))
+
+
+def test_fake_quant_k_equals_round_trip(oracle):
+    """tests/test_train_hook.py:97-99 analogue: fake_quant_k on bf16 keys, cast to bf16, equals the K of
+    dequantize(quantize(k, v)) bit for bit."""
+    kb, vb = _train_inputs(oracle, 0)
+    kr, _ = oracle.dequantize_blocks(oracle.quantize_blocks(kb, vb))
+    kq = oracle.fake_quant_k(oracle.bf16_to_f32(kb).reshape(3, 256, 512)).reshape(3, 256, 4, 128)
+    assert np.array_equal(oracle.f32_to_bf16(kq), kr)
+    # a planted mistake (scale (hi - lo) / 4) must not pass
+    x = oracle.bf16_to_f32(kb).reshape(3, 256, 512)
+    lo = x.min(1, keepdims=True); hi = x.max(1, keepdims=True)
+    sc8 = oracle.f8_decode(oracle.f8_encode(np.maximum((hi - lo) / np.float32(4), np.float32(1e-8))))
+    lo8 = oracle.f8_decode(oracle.f8_encode(lo))
+    bad = (np.clip(np.rint((x - lo8) / sc8), 0, 3) * sc8 + lo8).astype(np.float32).reshape(3, 256, 4, 128)
+    assert not np.array_equal(oracle.f32_to_bf16(bad), kr)
+
+
+def test_fake_quant_v_equals_round_trip(oracle):
+    """tests/test_train_hook.py:100-101 analogue: fake_quant_v equals the V of dequantize(quantize(k, v)) (same fp32
+    chains, so bit for bit here; the reference's bar is atol 1e-5)."""
+    kb, vb = _train_inputs(oracle, 1)
+    _, vr = oracle.dequantize_blocks(oracle.quantize_blocks(kb, vb))
+    vq = oracle.fake_quant_v(oracle.bf16_to_f32(vb))
+    assert np.array_equal(vq, vr)
+
+
+def test_fake_quant_v_float64(oracle):
+    """Against a float64 statement of train.py:92-100: tokens whose bits agree match within the fp32 rounding of the
+    two 128-term chains (1e-5 relative to the token's largest output); a token whose bits differ (an error of about
+    sc8 / sqrt(128), far above that) must hold a rounding tie (|(y - lo8) / sc8 - 1/2| tiny in float64)."""
+    rng = np.random.RandomState(2)
+    v = (rng.standard_normal((512, 4, 128)) * 2).astype(np.float32)
+    got = oracle.fake_quant_v(v).astype(np.float64)
+    H = oracle.hadamard().astype(np.float64)
+    y = (v.astype(np.float64) @ H).reshape(512, 2, 256)
+    lo = y.min(-1, keepdims=True); hi = y.max(-1, keepdims=True)
+    lo8 = oracle.f8_decode(oracle.f8_encode(lo.astype(np.float32))).astype(np.float64)
+    sc8 = oracle.f8_decode(oracle.f8_encode(np.maximum(hi - lo, 1e-8).astype(np.float32))).astype(np.float64)
+    r = (y - lo8) / np.maximum(sc8, 1e-8)
+    want = (np.clip(np.round(r), 0, 1) * sc8 + lo8).reshape(512, 4, 128) @ H
+    diff = np.abs(got - want).max(axis=(1, 2))
+    bad = np.nonzero(diff > 1e-5 * (1 + np.abs(want).max(axis=(1, 2))))[0]
+    for t in bad:
+        assert np.abs(np.abs(r[t] - np.floor(r[t])) - 0.5).min() < 1e-5, t
+    assert len(bad) <= 2
