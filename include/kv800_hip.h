@@ -128,6 +128,16 @@ int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const
 int kv800_hip_fake_quant_k(const float* x, int64_t G, int64_t C, float* out, void* stream);
 int kv800_hip_fake_quant_v(const float* v, int64_t N, float* out, void* stream);
 
+/* Prefill over compressed history (vllm_attn.py:351-380): row r's positions [0, P->N[r]) written as contiguous bf16
+ * K and V at rows out_off[r] + p of k_out / v_out ((S, 4, 128) each). Positions below 256 * P->NQ[r] are dequantized
+ * from their sub-block (dequantize_blocks, kv800.py:79-92; V cast to bf16), the others read from the exact pages.
+ * With cos_t / sin_t ((rope_rows, 32) bf16) the keys are rotated as the reference's _rope (vllm_attn.py:160-163) does
+ * over its 128-wide tables; NULL leaves them unrotated (sliding layers). P's sink and window fields are ignored.
+ * max_n >= every P->N[r]; rows, sub-blocks or positions outside their pools / tables are written as zeros. */
+int kv800_hip_history(const kv800_paged_t* P, int64_t R, int64_t max_n, const uint16_t* cos_t, const uint16_t* sin_t,
+                      int64_t rope_rows, int64_t qpool_bytes, int64_t epool_elems, const int64_t* out_off,
+                      uint16_t* k_out, uint16_t* v_out, void* stream);
+
 /* Step bookkeeping in vLLM's page geometry (exact page [4 heads, ebs, K128 | V128] bf16 with element strides s0 (page),
  * s1 (head), s2 (token); quant page = 5 x 51,200-byte sub-blocks per 1280 tokens, qs0 bytes apart). */
 

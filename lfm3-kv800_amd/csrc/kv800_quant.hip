@@ -471,6 +471,149 @@ __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restri
   }
 }
 
+
+// ---------------------------------------------------------------- prefill history (vllm_attn.py:160-163, 351-380)
+// Row r's positions [0, N[r]) as contiguous bf16 K (rotated when cos_t != null) and V at output rows out_off[r] + p:
+// positions below 256 NQ[r] come from sub-block p / 256 (K = bf16(code ksc + klo), V = (bit vsc + vlo) H by the
+// dequantizer's fp32 chain, then bf16: dequantize_blocks, kv800.py:79-92), the others from the exact pages. RoPE is the
+// reference's fp32 kf c + rotate_half(kf) s over the 128-wide tables (cos32 | 1 | cos32 | 1), (sin32 | 0 | sin32 | 0),
+// each product and the sum rounded once, then bf16. Unreadable rows (offsets outside their pool, positions past the
+// rope table) are written as zeros. One workgroup per (256-position tile, row).
+__device__ __forceinline__ void rope8(float (&a)[8], float (&b)[8], const uint16_t* cs, const uint16_t* sn, bool rope) {
+  // a = dims d0 .. d0 + 7, b = dims d0 + 64 .. d0 + 71; rope: d0 < 32 (cs / sn the tables' entries d0 ..), else the
+  // unrotated dims, for which the table holds cos 1, sin 0
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = rope ? bf2f(cs[e]) : 1.0f, s = rope ? bf2f(sn[e]) : 0.0f;
+    const float x = a[e], y = b[e];
+    a[e] = __fadd_rn(__fmul_rn(x, c), __fmul_rn(-y, s));
+    b[e] = __fadd_rn(__fmul_rn(y, c), __fmul_rn(x, s));
+  }
+}
+__device__ __forceinline__ uint4 pack_bf16x8(const float (&x)[8]) {
+  return make_uint4(f2bf(x[0]) | (f2bf(x[1]) << 16), f2bf(x[2]) | (f2bf(x[3]) << 16), f2bf(x[4]) | (f2bf(x[5]) << 16),
+                    f2bf(x[6]) | (f2bf(x[7]) << 16));
+}
+
+__global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uint16_t* __restrict__ cos_t,
+                                                      const uint16_t* __restrict__ sin_t, int64_t rope_rows,
+                                                      int64_t qpool_bytes, int64_t epool_elems,
+                                                      const int64_t* __restrict__ out_off, uint16_t* __restrict__ kout,
+                                                      uint16_t* __restrict__ vout) {
+  __shared__ __align__(16) float xbuf[4][512];   // per wave: one token's 4 dequantized V rows
+  __shared__ float klo_s[512], ksc_s[512];
+  const int r = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int n = P.N[r], p0 = blockIdx.x * BLK;
+  if (p0 >= n) return;   // uniform over the workgroup
+  const int cnt = min(BLK, n - p0);
+  const int64_t ob = out_off[r] + p0;
+  const bool rot = cos_t != nullptr;
+  const int nq = min((int64_t)max(P.NQ[r], 0), P.boff_stride);
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+  if ((int)blockIdx.x < nq) {
+    const int64_t base = P.boff[(int64_t)r * P.boff_stride + blockIdx.x];
+    const bool ok = base >= 0 && base + SUB <= qpool_bytes;   // uniform
+    const uint8_t* s = P.qpool + (ok ? base : 0);
+    if (ok)
+      for (int i = tid; i < 512; i += 256) { klo_s[i] = f8d(s[KLO_O + i]); ksc_s[i] = f8d(s[KSC_O + i]); }
+    __syncthreads();
+    // K: unit u = (token t, head h, d0 = 8 (u % 8)): dims d0 .. d0 + 7 and d0 + 64 .. d0 + 71
+    for (int u = tid; u < cnt * 32; u += 256) {
+      const int t = u >> 5, h = (u >> 3) & 3, d0 = 8 * (u & 7);
+      uint16_t* ko = kout + (ob + t) * 512 + h * 128 + d0;
+      const int pos = p0 + t;
+      if (!ok || (rot && pos >= rope_rows)) {
+        *reinterpret_cast<uint4*>(ko) = zero4;
+        *reinterpret_cast<uint4*>(ko + 64) = zero4;
+        continue;
+      }
+      const uint2 by = *reinterpret_cast<const uint2*>(s + KC_O + (t * 4 + h) * 32 + (d0 & 31));
+      const uint32_t bw[2] = {by.x, by.y};
+      const int sa = 2 * (d0 >> 5), sb = sa + 4;   // code fields of dims d0 + e and d0 + 64 + e
+      float a[8], b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t byte = (bw[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+        const int ia = h * 128 + d0 + e, ib = ia + 64;
+        a[e] = bf2f(f2bf(__fadd_rn(__fmul_rn((float)((byte >> sa) & 3u), ksc_s[ia]), klo_s[ia])));
+        b[e] = bf2f(f2bf(__fadd_rn(__fmul_rn((float)((byte >> sb) & 3u), ksc_s[ib]), klo_s[ib])));
+      }
+      if (rot) rope8(a, b, cos_t + (int64_t)pos * 32 + d0, sin_t + (int64_t)pos * 32 + d0, d0 < 32);
+      *reinterpret_cast<uint4*>(ko) = pack_bf16x8(a);
+      *reinterpret_cast<uint4*>(ko + 64) = pack_bf16x8(b);
+    }
+    // V: wave w takes tokens w, w + 4, ...; lane (head lane / 16, dims 8 (lane % 16) ..) builds bit vsc + vlo, then the
+    // four Hadamard chains (lane = dims lane, lane + 64)
+    float hcol[64];
+    hadamard_column(hcol, lane);
+    float* xb = xbuf[w];
+    const int rr = lane >> 4, e0 = 8 * (lane & 15);
+    for (int t = w; t < cnt; t += 4) {
+      uint16_t* vo = vout + (ob + t) * 512;
+      if (!ok) {
+        for (int i = lane; i < 512; i += 64) vo[i] = 0;
+        continue;
+      }
+      {
+        const float vsc = f8d(s[VSC_O + t * 2 + (rr >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (rr >> 1)]);
+        const uint8_t* vb = s + VB_O + (t * 4 + rr) * 16;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = e0 + e;
+          const float bit = (float)((vb[d & 15] >> (d >> 4)) & 1u);
+          xb[rr * 128 + d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float ya, yb;
+        __builtin_amdgcn_sched_barrier(0);
+        hadamard_chain(xb + h * 128, hcol, ya, yb);
+        vo[h * 128 + lane] = (uint16_t)f2bf(ya);
+        vo[h * 128 + 64 + lane] = (uint16_t)f2bf(yb);
+      }
+      __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite xb
+    }
+    return;
+  }
+  // exact positions: unit u = (token t, head h, d0), K rotated, V copied
+  const int64_t* et = P.eoff + (int64_t)r * P.eoff_stride;
+  for (int u = tid; u < cnt * 32; u += 256) {
+    const int t = u >> 5, h = (u >> 3) & 3, d0 = 8 * (u & 7);
+    const int pos = p0 + t;
+    uint16_t* ko = kout + (ob + t) * 512 + h * 128 + d0;
+    uint16_t* vo = vout + (ob + t) * 512 + h * 128 + d0;
+    const int64_t pg = pos / P.ebs;
+    const int64_t eb = pg < P.eoff_stride ? et[pg] : -1;
+    const int64_t kr = eb + h * P.e_hs + (pos - pg * P.ebs) * P.e_ts, vr = kr + P.e_v;
+    if (eb < 0 || kr < 0 || vr < 0 || kr + 128 > epool_elems || vr + 128 > epool_elems || (rot && pos >= rope_rows)) {
+      *reinterpret_cast<uint4*>(ko) = zero4; *reinterpret_cast<uint4*>(ko + 64) = zero4;
+      *reinterpret_cast<uint4*>(vo) = zero4; *reinterpret_cast<uint4*>(vo + 64) = zero4;
+      continue;
+    }
+    const uint4 k0 = *reinterpret_cast<const uint4*>(P.epool + kr + d0);
+    const uint4 k1 = *reinterpret_cast<const uint4*>(P.epool + kr + d0 + 64);
+    *reinterpret_cast<uint4*>(vo) = *reinterpret_cast<const uint4*>(P.epool + vr + d0);
+    *reinterpret_cast<uint4*>(vo + 64) = *reinterpret_cast<const uint4*>(P.epool + vr + d0 + 64);
+    if (!rot) {
+      *reinterpret_cast<uint4*>(ko) = k0;
+      *reinterpret_cast<uint4*>(ko + 64) = k1;
+      continue;
+    }
+    const uint32_t wa[4] = {k0.x, k0.y, k0.z, k0.w}, wb[4] = {k1.x, k1.y, k1.z, k1.w};
+    float a[8], b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = (e & 1) ? bf2f_hi(wa[e >> 1]) : bf2f_lo(wa[e >> 1]);
+      b[e] = (e & 1) ? bf2f_hi(wb[e >> 1]) : bf2f_lo(wb[e >> 1]);
+    }
+    rope8(a, b, cos_t + (int64_t)pos * 32 + d0, sin_t + (int64_t)pos * 32 + d0, d0 < 32);
+    *reinterpret_cast<uint4*>(ko) = pack_bf16x8(a);
+    *reinterpret_cast<uint4*>(ko + 64) = pack_bf16x8(b);
+  }
+}
+
 }  // namespace
 }  // namespace kv800
 
@@ -545,6 +688,26 @@ int kv800_hip_fake_quant_v(const float* v, int64_t N, float* out, void* stream) 
   KV800_REQUIRE(nb <= 0x7FFFFFFF, "fake_quant_v: N too large");
   hipLaunchKernelGGL(fake_quant_v_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, v, N, out);
   return check_launch("fake_quant_v");
+}
+
+int kv800_hip_history(const kv800_paged_t* P, int64_t R, int64_t max_n, const uint16_t* cos_t, const uint16_t* sin_t,
+                       int64_t rope_rows, int64_t qpool_bytes, int64_t epool_elems, const int64_t* out_off,
+                       uint16_t* k_out, uint16_t* v_out, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(P && R >= 0 && max_n >= 0, "history: bad arguments");
+  if (R == 0 || max_n == 0) return KV800_OK;
+  KV800_REQUIRE(P->N && P->NQ && P->epool && P->eoff && out_off && k_out && v_out, "history: null pointer");
+  KV800_REQUIRE(!cos_t == !sin_t, "history: cos_t and sin_t go together");
+  KV800_REQUIRE(P->ebs > 0 && P->e_hs % 8 == 0 && P->e_ts % 8 == 0 && P->e_v % 8 == 0 && ((uintptr_t)P->epool % 16) == 0,
+                "history: exact strides must be multiples of 8 elements and the pool 16-byte aligned");
+  KV800_REQUIRE(P->boff_stride == 0 || (P->qpool && P->boff), "history: quantized rows need qpool and boff");
+  KV800_REQUIRE(((uintptr_t)k_out % 16) == 0 && ((uintptr_t)v_out % 16) == 0, "history: outputs must be 16-byte aligned");
+  KV800_REQUIRE(R <= 65535, "history: at most 65535 rows per call");
+  const int64_t tiles = (max_n + BLK - 1) / BLK;
+  KV800_REQUIRE(tiles <= 0x7FFFFFFF, "history: max_n too large");
+  hipLaunchKernelGGL(history_kernel, dim3((unsigned)tiles, (unsigned)R), dim3(256), 0, (hipStream_t)stream, *P, cos_t,
+                     sin_t, rope_rows, qpool_bytes, epool_elems, out_off, k_out, v_out);
+  return check_launch("history");
 }
 
 }  // extern "C"

@@ -64,6 +64,7 @@ SIGNATURES = {
     "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
                                      _VP]),
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
+    "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_fake_quant_k": (_I32, [_VP, _I64, _I64, _VP, _VP]),
     "kv800_hip_fake_quant_v": (_I32, [_VP, _I64, _VP, _VP]),
 }
@@ -247,6 +248,54 @@ def page_offsets(bt, scale, add=0):
     _check(L.kv800_hip_page_offsets(_ptr(bt), bt.stride(0), bt.shape[0], bt.shape[1], int(scale), int(add), _ptr(out),
                                     _stream(dev)))
     return out
+
+
+def history(P, lens, cos_t=None, sin_t=None):
+    """Prefill over compressed history (kv800_hip_history, vllm_attn.py:351-380): rows b < len(lens) of the paged cache
+    P, positions [0, lens[b]), as contiguous bf16 K (rotated with the (P, 32) cos_t / sin_t tables, or unrotated when
+    they are None) and V, (sum(lens), 4, 128) each, row b's positions starting at offs[b]. Positions below
+    256 * P.NQ[b] are dequantized from their sub-blocks, the others read from the exact pages. Returns (K, V, offs)."""
+    L = ops()
+    dev = P.epool.device
+    lens = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
+    R = len(lens)
+    if any(x < 0 for x in lens):
+        raise ValueError("lens must be >= 0")
+    S = sum(lens)
+    K = torch.empty(S, 4, 128, dtype=torch.bfloat16, device=dev)
+    V = torch.empty_like(K)
+    offs = [0] * R
+    for b in range(1, R):
+        offs[b] = offs[b - 1] + lens[b - 1]
+    if R == 0 or S == 0:
+        return K, V, offs
+    rot = cos_t is not None
+    if rot:
+        _need(cos_t, "cos_t", torch.bfloat16, dev); _need(sin_t, "sin_t", torch.bfloat16, dev)
+        if cos_t.shape != sin_t.shape or cos_t.dim() != 2 or cos_t.shape[1] != 32:
+            raise ValueError("cos_t / sin_t must be (P, 32)")
+        cos_t, sin_t = cos_t.contiguous(), sin_t.contiguous()
+    _need(P.epool, "epool", torch.bfloat16, dev); _need(P.eoff, "eoff", torch.int64, dev)
+    _need(P.NQ, "NQ", torch.int32, dev)
+    if P.eoff.stride(-1) != 1 or P.eoff.shape[0] < R or P.NQ.shape[0] < R:
+        raise ValueError("eoff / NQ must cover the rows with contiguous eoff rows")
+    s = Paged()
+    s.epool, s.eoff, s.eoff_stride = P.epool.data_ptr(), P.eoff.data_ptr(), P.eoff.stride(0)
+    s.ebs, s.e_hs, s.e_ts, s.e_v = int(P.ebs), int(P.e_hs), int(P.e_ts), int(P.e_v)
+    N = torch.tensor(lens, dtype=torch.int32, device=dev)   # the output extents, from the host lengths
+    s.N, s.NQ = N.data_ptr(), P.NQ.data_ptr()
+    qbytes = 0
+    if P.qpool is not None and P.boff is not None and P.boff.numel():
+        _need(P.qpool, "qpool", torch.uint8, dev); _need(P.boff, "boff", torch.int64, dev)
+        if P.boff.stride(-1) != 1 or P.boff.shape[0] < R:
+            raise ValueError("boff must cover the rows with contiguous rows")
+        s.qpool, s.boff, s.boff_stride = P.qpool.data_ptr(), P.boff.data_ptr(), P.boff.stride(0)
+        qbytes = _extent(P.qpool)
+    offt = torch.tensor(offs, dtype=torch.int64, device=dev)
+    _check(L.kv800_hip_history(ctypes.byref(s), R, max(lens), _ptr(cos_t) if rot else None,
+                               _ptr(sin_t) if rot else None, cos_t.shape[0] if rot else 0, qbytes, _extent(P.epool),
+                               _ptr(offt), _ptr(K), _ptr(V), _stream(dev)))
+    return K, V, offs
 
 
 def fake_quant_k(x):

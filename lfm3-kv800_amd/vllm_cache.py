@@ -105,3 +105,54 @@ class KV800DecodeLayer:
         P = kv800.Paged(qpool=self.qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None,
                         sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
         return kv800_hip.decode(P, q, cos_t, sin_t)
+
+
+# ---------------------------------------------------------------- prefill / extend rows over compressed history
+def rope_keys(k, pos, cos_t, sin_t):
+    """vllm_attn.py:160-163: keys k (S, 4, 128) bf16 at positions pos (S,) rotated with the 128-wide tables
+    (cos32 | 1 | cos32 | 1), (sin32 | 0 | sin32 | 0) built from the (P, 32) bf16 tables; fp32, then bf16."""
+    c32, s32 = cos_t[pos].float(), sin_t[pos].float()
+    c = torch.cat((c32, torch.ones_like(c32), c32, torch.ones_like(c32)), 1)[:, None]
+    s = torch.cat((s32, torch.zeros_like(s32), s32, torch.zeros_like(s32)), 1)[:, None]
+    kf = k.float()
+    return (kf * c + torch.cat((-kf[..., 64:], kf[..., :64]), -1) * s).to(torch.bfloat16)
+
+
+def prefill_attention(q, K, V, kp, n0, n):
+    """Causal attention of the queries at positions n0 .. n-1 over keys at positions kp (vllm_attn.py:168-184, the
+    quantized layers' mask): q (n - n0, 16, 128), K / V (S, 4, 128) bf16 -> (n - n0, 16, 128) fp32. fp32 products on
+    contiguous operands, 512 queries at a time."""
+    Kf = K.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()           # (16, S, 128)
+    KT = Kf.transpose(1, 2).contiguous()                                          # (16, 128, S)
+    Vf = V.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()
+    qi = q.float().transpose(0, 1).contiguous()                                   # (16, Tq, 128)
+    qp = torch.arange(n0, n, device=q.device)
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    for a in range(0, n - n0, 512):
+        m = kp[None] <= qp[a:a + 512, None]
+        sc = torch.matmul(qi[:, a:a + 512].contiguous(), KT) * (128 ** -0.5)
+        w = sc.masked_fill(~m[None], float("-inf")).softmax(-1)
+        out[a:a + 512] = torch.matmul(w, Vf).transpose(0, 1)
+    return out
+
+
+def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
+    """Prefill / extend rows of a quantized layer (vllm_attn.py:351-402 for quant layers): row i has queries
+    q[qsl[i]:qsl[i+1]] (post-RoPE) at positions prev[i] .. prev[i] + (qsl[i+1] - qsl[i]) - 1, new pre-RoPE keys and
+    values k / v at the same rows, and a history of prev[i] positions in the cache P (its first (prev - 128) // 256
+    sub-blocks flushed, P.NQ, the rest in the exact pages). The history comes out of one kv800_hip_history launch
+    (dequantized, rotated, bf16); the new keys are rotated as the reference does; then causal attention per row.
+    qsl / prev are host sequences. Returns (T, 16, 128) bf16."""
+    R = len(prev)
+    Kh, Vh, offs = kv800_hip.history(P, [int(x) for x in prev], cos_t, sin_t)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    for i in range(R):
+        s, e, n0 = int(qsl[i]), int(qsl[i + 1]), int(prev[i])
+        n = n0 + (e - s)
+        pos = torch.arange(n0, n, device=q.device)
+        Kn = rope_keys(k[s:e], pos, cos_t, sin_t)
+        Kb = torch.cat((Kh[offs[i]:offs[i] + n0], Kn))
+        Vb = torch.cat((Vh[offs[i]:offs[i] + n0], v[s:e].to(torch.bfloat16)))
+        kp = torch.arange(n, device=q.device)
+        out[s:e] = prefill_attention(q[s:e], Kb, Vb, kp, n0, n).to(torch.bfloat16)
+    return out

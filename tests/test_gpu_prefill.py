@@ -1,0 +1,115 @@
+"""Prefill over compressed history on an MI355X: kv800_hip_history (the dequantize -> bf16 producer of
+vllm_attn.py:351-380) bit-exact against the oracle, and the quantized-layer prefill rows (vllm_cache.prefill_quant_rows)
+against a float64 restatement."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+
+
+def say(*a):
+    print("[gpu-prefill]", *a, flush=True)
+
+
+def to_dev_bf16(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bits_of(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def upload(case):
+    import lfm3_kv800_amd.kv800 as kv
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return kv.Paged(qpool=T(case.qpool), boff=T(case.boff), epool=to_dev_bf16(case.epool), eoff=T(case.eoff),
+                    ebs=case.ebs, e_hs=case.e_hs, e_ts=case.e_ts, e_v=case.e_v, sk=None, sv=None, skoff=None,
+                    svoff=None, N=T(case.N), NQ=T(case.NQ), nqmax=case.nqmax, win=0)
+
+
+def rope_np(oracle, kbits, pos, cos, sin):
+    """vllm_attn.py:160-163 in numpy float32 (each product and the sum rounded once), then bf16 bits."""
+    k = oracle.bf16_to_f32(kbits)
+    c32, s32 = oracle.bf16_to_f32(cos[pos]), oracle.bf16_to_f32(sin[pos])
+    one, zero = np.ones_like(c32), np.zeros_like(s32)
+    c = np.concatenate([c32, one, c32, one], 1)[:, None, :]
+    s = np.concatenate([s32, zero, s32, zero], 1)[:, None, :]
+    rot = np.concatenate([-k[..., 64:], k[..., :64]], -1)
+    return oracle.f32_to_bf16((k * c + rot * s).astype(np.float32))
+
+
+def history_np(oracle, K, V, n):
+    """Positions [0, n) of one row as the reference assembles them: dequantized sub-blocks (K bf16, V fp32 -> bf16),
+    then the exact rows; returns unrotated K bits and V bits."""
+    nq = oracle.nq_of(n)
+    kb, vb = K[:n].copy(), V[:n].copy()
+    if nq:
+        kq, vq = oracle.dequantize_blocks(oracle.quantize_blocks(K[:256 * nq].reshape(nq, 256, 4, 128),
+                                                                 V[:256 * nq].reshape(nq, 256, 4, 128)))
+        kb[:256 * nq] = kq.reshape(-1, 4, 128)
+        vb[:256 * nq] = oracle.f32_to_bf16(vq.reshape(-1, 4, 128))
+    return kb, vb
+
+
+def test_history_bitexact(hip, oracle):
+    rng = np.random.RandomState(5)
+    lens = [50, 384, 640, 1000, 2311]
+    K = [oracle.randn_bf16(rng, (n, 4, 128), offset=rng.standard_normal((1, 4, 128))) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    cos, sin = oracle.rope_tables(2400)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, ebs=64, shuffle_seed=3)
+    P = upload(case)
+    say("history", lens)
+    Kh, Vh, offs = hip.history(P, lens, to_dev_bf16(cos), to_dev_bf16(sin))
+    Ku, Vu, _ = hip.history(P, lens)                          # unrotated (sliding layers)
+    kh, vh, ku, vu = bits_of(Kh), bits_of(Vh), bits_of(Ku), bits_of(Vu)
+    for b, n in enumerate(lens):
+        kb, vb = history_np(oracle, K[b], V[b], n)
+        sl = slice(offs[b], offs[b] + n)
+        assert np.array_equal(vh[sl], vb), b
+        assert np.array_equal(vu[sl], vb), b
+        assert np.array_equal(ku[sl], kb), b
+        assert np.array_equal(kh[sl], rope_np(oracle, kb, np.arange(n), cos, sin)), b
+
+
+def test_prefill_quant_rows(hip, oracle):
+    """Extend rows of a quantized layer: queries at positions n0 .. n-1 over the compressed history + new rows, against
+    a float64 attention over the reference's assembled keys / values."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    rng = np.random.RandomState(8)
+    prev = [700, 383, 1500]
+    new = [37, 5, 64]
+    lens = [p + t for p, t in zip(prev, new)]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    cos, sin = oracle.rope_tables(1700)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), prev, ebs=64, shuffle_seed=4)
+    P = upload(case)
+    q = oracle.randn_bf16(rng, (sum(new), 16, 128))
+    qsl = np.concatenate([[0], np.cumsum(new)])
+    kn = np.concatenate([K[b][prev[b]:] for b in range(3)])
+    vn = np.concatenate([V[b][prev[b]:] for b in range(3)])
+    say("prefill rows", prev, new)
+    out = vc.prefill_quant_rows(P, to_dev_bf16(q), to_dev_bf16(kn), to_dev_bf16(vn), qsl, prev, to_dev_bf16(cos),
+                                to_dev_bf16(sin))
+    o = torch.from_numpy(bits_of(out).view(np.int16)).view(torch.bfloat16).float().numpy()
+    for b in range(3):
+        n0, n = prev[b], lens[b]
+        kb, vb = history_np(oracle, K[b], V[b], n0)
+        kb = np.concatenate([kb, K[b][n0:n]]); vb = np.concatenate([vb, V[b][n0:n]])
+        Kr = oracle.bf16_to_f32(rope_np(oracle, kb, np.arange(n), cos, sin)).astype(np.float64)
+        Vf = oracle.bf16_to_f32(vb).astype(np.float64)
+        qf = oracle.bf16_to_f32(q[qsl[b]:qsl[b + 1]]).astype(np.float64)
+        Kr, Vf = np.repeat(Kr, 4, axis=1), np.repeat(Vf, 4, axis=1)                   # (n, 16, 128)
+        sc = np.einsum("thd,shd->hts", qf, Kr) * 128 ** -0.5
+        qp = np.arange(n0, n)
+        sc = np.where(np.arange(n)[None, None, :] <= qp[None, :, None], sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
+        want = np.einsum("hts,shd->thd", w, Vf)
+        d = np.abs(o[qsl[b]:qsl[b + 1]] - want)
+        say(f"row {b}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (b, d.max(), d.mean())
