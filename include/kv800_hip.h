@@ -69,6 +69,14 @@ int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_str
                     int64_t qs0, const int32_t* nq_prev, const int32_t* nq_new, int64_t R, int64_t max_new,
                     void* stream);
 
+/* kv800_hip_flush with the same arguments and bytes, organised for the latency of a flush of few sub-blocks (a decode
+ * step flushes at most one per row, usually one or two per layer): one token per V wave, each K row read once. Use
+ * kv800_hip_flush when many sub-blocks are flushed at once (prefill chunks). */
+int kv800_hip_flush_latency(const uint16_t* epool, const int64_t* eoff, int64_t eoff_stride, int64_t ebs, int64_t e_hs,
+                            int64_t e_ts, int64_t e_v, uint8_t* qpool, const int64_t* qbt, int64_t qbt_stride,
+                            int64_t bsq, int64_t qs0, const int32_t* nq_prev, const int32_t* nq_new, int64_t R,
+                            int64_t max_new, void* stream);
+
 /* Dequantize M sub-blocks. Replaces kv800.dequantize_blocks (kv800.py:79-92).
  * k_out: (M, 256, 4, 128) bf16 = bf16(code * ksc + klo); v_out: (M, 256, 4, 128) f32 = (bit * vsc + vlo) @ H. */
 int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, float* v_out, void* stream);

@@ -76,7 +76,7 @@ __device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)
   float a = 0.f;
 #pragma unroll
   for (int k = 0; k < 64; k += 4) {
-    if ((k & 15) == 0) __builtin_amdgcn_sched_barrier(0);   // bound the LDS loads in flight
+    __builtin_amdgcn_sched_barrier(0);   // one float4 of the row in flight: the chain is serial anyway
     const float4 v4 = *reinterpret_cast<const float4*>(x + k);
     a = __builtin_fmaf(v4.x, hc[k], a);
     a = __builtin_fmaf(v4.y, hc[k + 1], a);
@@ -86,7 +86,7 @@ __device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)
   float b = a;
 #pragma unroll
   for (int k = 64; k < 128; k += 4) {
-    if ((k & 15) == 0) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
     const float4 v4 = *reinterpret_cast<const float4*>(x + k);
     a = __builtin_fmaf(v4.x, hc[k - 64], a);     b = __builtin_fmaf(v4.x, -hc[k - 64], b);
     a = __builtin_fmaf(v4.y, hc[k - 63], a);     b = __builtin_fmaf(v4.y, -hc[k - 63], b);
@@ -151,7 +151,7 @@ struct QuantLds {                  // K path: per-wave min / max partials, then 
 };
 
 // K codes and scales of one sub-block: per (head, channel) min / max over its 256 tokens (8 waves x 32 tokens).
-template <typename Src>
+template <typename Src, int KG = 8>
 __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   QuantLds& S = *reinterpret_cast<QuantLds*>(lds);
@@ -163,7 +163,6 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
   // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16). The
   // rows are read in groups of KG tokens, twice (min / max, then codes; the second pass hits L2), which keeps the
   // pass within the register budget of the V pass it shares a grid with.
-  constexpr int KG = 8;
   const int h = lane >> 4, c0 = 8 * (lane & 15);
   float mn[8], mx[8];
 #pragma unroll
@@ -240,21 +239,21 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
 // that those scalar loads find the rows in L2 instead of waiting on HBM.
 constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
 
-template <typename Src>
+template <int VT, typename Src>
 __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int tw = t0 + VTPW * w;                      // this wave's first token
+  const int tw = t0 + VT * w;                        // this wave's first token; VT tokens per wave
   const int rh = lane >> 4, rc = 8 * (lane & 15);    // the 16 bytes this lane touches: head rh, dims rc .. rc + 7
   auto touch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, rh) + rc); };
-  uint4 pf0 = touch(tw), pf1 = touch(tw + 1);
+  uint4 pf0 = touch(tw), pf1 = VT > 1 ? touch(tw + 1) : pf0;
   float hcol[64];
   hadamard_column(hcol, lane);
 #pragma unroll 1
-  for (int tt = 0; tt < VTPW; ++tt) {
+  for (int tt = 0; tt < VT; ++tt) {
     const int t = tw + tt;
     asm volatile("" :: "v"(pf0.x), "v"(pf0.y), "v"(pf0.z), "v"(pf0.w));   // token t is in L2 by now
     pf0 = pf1;
-    if (tt + 2 < VTPW) pf1 = touch(t + 2);
+    if (tt + 2 < VT) pf1 = touch(t + 2);
     float ya[4], yb[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -297,7 +296,7 @@ constexpr int QLDS_BYTES = (int)sizeof(QuantLds);
 template <typename Src>
 __device__ __forceinline__ void quantize_part(const Src& src, uint8_t* __restrict__ out, char* lds, bool kpass, int part) {
   if (kpass) quantize_k(src, out, lds);
-  else quantize_v(src, out, part * VTOK);
+  else quantize_v<VTPW>(src, out, part * VTOK);
 }
 
 __global__ void __launch_bounds__(QTHREADS) quantize_dense_kernel(const uint16_t* __restrict__ k,
@@ -327,6 +326,33 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
   quantize_part(PagedSrc{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0}, dst, lds, kpass,
                 kpass ? 0 : (int)((i - units) % VSPLIT));
+}
+
+// ---------------------------------------------------------------- latency-oriented flush (decode steps)
+// A decode step flushes one or two sub-blocks per layer, so the flush costs one sub-block's latency, not throughput.
+// Same code as the throughput flush, with finer work: one token per V wave (32 V workgroups per sub-block instead of 4
+// of 64 tokens) and the K rows read 16 at a time (4 dependent round trips instead of 8).
+constexpr int LSPLIT = BLK / QW;   // V workgroups per sub-block in the latency flush: one token per wave
+
+__global__ void __launch_bounds__(QTHREADS) flush_lat_kernel(const uint16_t* __restrict__ ep,
+                                                             const int64_t* __restrict__ eoff, int64_t es, int64_t ebs,
+                                                             int64_t e_hs, int64_t e_ts, int64_t e_v,
+                                                             uint8_t* __restrict__ qpool, const int64_t* __restrict__ qbt,
+                                                             int64_t qs, int64_t bsq, int64_t qs0,
+                                                             const int32_t* __restrict__ nq_prev,
+                                                             const int32_t* __restrict__ nq_new, int64_t R, int max_new) {
+  __shared__ __align__(16) char lds[QLDS_BYTES];
+  const int64_t units = R * max_new, i = blockIdx.x;
+  const bool kpass = i < units;
+  const int64_t unit = kpass ? i : (i - units) / LSPLIT;
+  const int64_t r = unit / max_new;
+  const int j = nq_prev[r] + (int)(unit % max_new);
+  if (j >= nq_new[r]) return;   // uniform over the workgroup
+  const int64_t tok0 = (int64_t)j * BLK;
+  uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
+  const PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
+  if (kpass) quantize_k<PagedSrc, 16>(src, dst, lds);
+  else quantize_v<1>(src, dst, (int)((i - units) % LSPLIT) * QW);
 }
 
 // ---------------------------------------------------------------- dequantize (kv800.py:79-92)
@@ -654,6 +680,24 @@ int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_str
                      epool, eoff, eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq, qs0, nq_prev, nq_new, R,
                      (int)max_new);
   return check_launch("flush");
+}
+
+int kv800_hip_flush_latency(const uint16_t* epool, const int64_t* eoff, int64_t eoff_stride, int64_t ebs, int64_t e_hs,
+                            int64_t e_ts, int64_t e_v, uint8_t* qpool, const int64_t* qbt, int64_t qbt_stride,
+                            int64_t bsq, int64_t qs0, const int32_t* nq_prev, const int32_t* nq_new, int64_t R,
+                            int64_t max_new, void* stream) {
+  g_err[0] = 0;
+  KV800_REQUIRE(R >= 0 && max_new >= 0, "flush_latency: R and max_new must be >= 0");
+  if (R == 0 || max_new == 0) return KV800_OK;
+  KV800_REQUIRE(epool && eoff && qpool && qbt && nq_prev && nq_new, "flush_latency: null pointer");
+  KV800_REQUIRE(ebs > 0 && bsq > 0 && bsq % BLK == 0, "flush_latency: ebs must be > 0 and bsq a positive multiple of 256");
+  KV800_REQUIRE(e_hs % 8 == 0 && e_ts % 8 == 0 && e_v % 8 == 0 && ((uintptr_t)epool % 16) == 0,
+                "flush_latency: exact-pool strides must be multiples of 8 elements and the pool 16-byte aligned");
+  KV800_REQUIRE(R * max_new * (1 + LSPLIT) <= 0x7FFFFFFF, "flush_latency: grid too large");
+  hipLaunchKernelGGL(flush_lat_kernel, dim3((unsigned)(R * max_new * (1 + LSPLIT))), dim3(QTHREADS), 0,
+                     (hipStream_t)stream, epool, eoff, eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq,
+                     qs0, nq_prev, nq_new, R, (int)max_new);
+  return check_launch("flush_latency");
 }
 
 int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, float* v_out, void* stream) {

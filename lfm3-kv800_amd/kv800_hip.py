@@ -66,6 +66,8 @@ SIGNATURES = {
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
     "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_fake_quant_k": (_I32, [_VP, _I64, _I64, _VP, _VP]),
+    "kv800_hip_flush_latency": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP,
+                                       _I64, _I64, _VP]),
     "kv800_hip_fake_quant_v": (_I32, [_VP, _I64, _VP, _VP]),
 }
 
@@ -160,10 +162,11 @@ def dequantize_blocks(sb):
     return k, v
 
 
-def flush(epool, eoff, ebs, e_hs, e_ts, e_v, qpool, qbt, bsq, qs0, nq_prev, nq_new, max_new):
+def flush(epool, eoff, ebs, e_hs, e_ts, e_v, qpool, qbt, bsq, qs0, nq_prev, nq_new, max_new, latency=False):
     """Quantize sub-blocks j in [nq_prev[r], nq_new[r]) of every row r from the exact pages into the quant pool
     (one launch; see kv800_hip_flush). epool bf16 (any shape, element offsets), eoff (R, pages) int64 element
-    offsets, qpool uint8 (byte offsets), qbt (R, >= 1) int64 quant block table, nq_prev / nq_new (R,) int32."""
+    offsets, qpool uint8 (byte offsets), qbt (R, >= 1) int64 quant block table, nq_prev / nq_new (R,) int32.
+    latency=True: kv800_hip_flush_latency (same bytes; for steps that flush few sub-blocks, e.g. decode)."""
     L = ops()
     dev = epool.device
     _need(epool, "epool", torch.bfloat16, dev); _need(qpool, "qpool", torch.uint8, dev)
@@ -173,9 +176,9 @@ def flush(epool, eoff, ebs, e_hs, e_ts, e_v, qpool, qbt, bsq, qs0, nq_prev, nq_n
         raise ValueError("eoff and qbt rows must be contiguous")
     R = nq_prev.shape[0]
     nq_prev, nq_new = nq_prev.contiguous(), nq_new.contiguous()
-    _check(L.kv800_hip_flush(_ptr(epool), _ptr(eoff), eoff.stride(0), int(ebs), int(e_hs), int(e_ts), int(e_v),
-                             _ptr(qpool), _ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(nq_prev), _ptr(nq_new),
-                             R, int(max_new), _stream(dev)))
+    fn = L.kv800_hip_flush_latency if latency else L.kv800_hip_flush
+    _check(fn(_ptr(epool), _ptr(eoff), eoff.stride(0), int(ebs), int(e_hs), int(e_ts), int(e_v), _ptr(qpool), _ptr(qbt),
+              qbt.stride(0), int(bsq), int(qs0), _ptr(nq_prev), _ptr(nq_new), R, int(max_new), _stream(dev)))
 
 
 def write_exact(ev, slot, k, v, pos=None, sk=None, sv=None, skoff=None, svoff=None):

@@ -100,7 +100,7 @@ class KV800DecodeLayer:
             return kv800_hip.decode(P, q, cos_t, sin_t)
         kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
         # ---- flush the sub-blocks that became eligible this step ([NP, NQ) per row), from this layer's own exact group
-        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, self.qv, qbt64, QBLOCK, QPAGE, NP, NQ, max_new)
+        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, self.qv, qbt64, QBLOCK, QPAGE, NP, NQ, max_new, latency=True)
         # ---- the fused decode
         P = kv800.Paged(qpool=self.qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None,
                         sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)

@@ -103,10 +103,12 @@ def test_quantize_random_vs_oracle(hip, oracle, dist):
     assert np.array_equal(got, want), f"{int((got != want).sum())} bytes differ"
 
 
-def test_flush_two_kv_groups(hip, oracle):
+@pytest.mark.parametrize("latency", [False, True])
+def test_flush_two_kv_groups(hip, oracle, latency):
     """vLLM geometry: two exact KV groups (different shuffled block tables, ebs 128, [pages, 4, 128, 256] bf16) and one
     quant layer per group with 1280-token quant pages of 262,144 bytes. Each layer must gather from its own group's
-    pages (the 0.1.1 fix, vllm_attn.py:301); reading the other group's table must give different bytes."""
+    pages (the 0.1.1 fix, vllm_attn.py:301); reading the other group's table must give different bytes. Both flush
+    kernels: the throughput one and the latency one of decode steps."""
     rng = np.random.RandomState(5)
     R, n_tok, ebs = 6, 2048 + 384, 128
     pages_per_row = (n_tok + ebs - 1) // ebs
@@ -134,9 +136,10 @@ def test_flush_two_kv_groups(hip, oracle):
         epool = to_dev_bf16(pools[gidx])
         eoff = torch.from_numpy(tables[gidx] * elems).to(DEV)
         qpool = torch.zeros(qpages * 262144, dtype=torch.uint8, device=DEV)
-        say("flush group", gidx)
+        say("flush group", gidx, "latency" if latency else "throughput")
         hip.flush(epool, eoff, ebs, ebs * 256, 256, 128, qpool, torch.from_numpy(qperm).to(DEV), 1280, 262144,
-                  torch.from_numpy(nq_prev).to(DEV), torch.from_numpy(nq_new).to(DEV), int((nq_new - nq_prev).max()))
+                  torch.from_numpy(nq_prev).to(DEV), torch.from_numpy(nq_new).to(DEV), int((nq_new - nq_prev).max()),
+                  latency=latency)
         outs.append(qpool.cpu().numpy())
     for gidx in range(2):
         q = outs[gidx]
