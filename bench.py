@@ -172,6 +172,8 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
 
     def step(i):
         me, mq = metas[i]
+        # the step's flushes start at once on a side stream, under the decode of the layers before them
+        vc.launch_flushes(list(layers.values()), {l: me[C4_GROUP[l]] for l in layers}, mq)
         for l in (2, 6, 10, 14, 18, 22):
             q, k, v = qkv[l]
             layers[l].forward(q, k, v, me[C4_GROUP[l]], mq, hosts=layers, cos_t=cos, sin_t=sin)

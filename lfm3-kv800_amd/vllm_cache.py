@@ -78,15 +78,8 @@ class KV800DecodeLayer:
         R = q.shape[0]
         # ---- per-step tables, built once per KV group and shared by its layers: the exact group's page offsets, and
         # the quant group's decode / flush / sink tables (one launch each)
-        ekey = ("eoff", s0)
-        if ekey not in mx.cache:
-            mx.cache[ekey] = kv800_hip.page_offsets(mx.block_table, s0)
-        eoff = mx.cache[ekey]
-        if ("step",) not in mq.cache:
-            nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
-            mq.cache[("step",)] = kv800_hip.step_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax, nnew=1,
-                                                        aux_scale=QPAGE // 2, aux_add=AUX_BYTES // 2) + (nqmax,)
-        boff, NQ, NP, qbt64, aux, nqmax = mq.cache[("step",)]
+        eoff = self._eoff(mx)
+        boff, NQ, NP, qbt64, aux, nqmax = _step_tables(mq)
         N = mx.seq_lens
         if self.win:
             # ---- step rows into the exact window pages, sink rows into the hosts' aux, then the window decode
@@ -99,12 +92,76 @@ class KV800DecodeLayer:
                             skoff=aux, svoff=aux, N=N, NQ=self._zeros[:R], nqmax=0, win=kv800.WIN)
             return kv800_hip.decode(P, q, cos_t, sin_t)
         kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
-        # ---- flush the sub-blocks that became eligible this step ([NP, NQ) per row), from this layer's own exact group
-        kv800_hip.flush(ev, eoff, ebs, s1, s2, 128, self.qv, qbt64, QBLOCK, QPAGE, NP, NQ, max_new, latency=True)
+        # ---- flush the sub-blocks that became eligible this step ([NP, NQ) per row), from this layer's own exact group;
+        # if launch_flushes ran it ahead on the side stream, wait for it instead
+        done = mq.cache.get(("flushed", self.l))
+        if done is not None:
+            torch.cuda.current_stream(ev.device).wait_event(done)
+        else:
+            self._flush(mx, mq, max_new)
         # ---- the fused decode
         P = kv800.Paged(qpool=self.qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None,
                         sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
         return kv800_hip.decode(P, q, cos_t, sin_t)
+
+    def _eoff(self, mx):
+        """The exact group's page offsets for this cache's page stride (one launch per group and step)."""
+        key = ("eoff", self.ev.stride(0))
+        if key not in mx.cache:
+            mx.cache[key] = kv800_hip.page_offsets(mx.block_table, self.ev.stride(0))
+        return mx.cache[key]
+
+    def _flush(self, mx, mq, max_new=1):
+        """This step's flush of a quantized layer on the current stream: rows r quantize sub-blocks [NP[r], NQ[r])
+        of this layer's own exact group into its quant pages."""
+        ev = self.ev
+        _, NQ, NP, qbt64, _, _ = _step_tables(mq)
+        kv800_hip.flush(ev, self._eoff(mx), self.ebs, ev.stride(1), ev.stride(2), 128, self.qv, qbt64, QBLOCK, QPAGE, NP,
+                        NQ, max_new, latency=True)
+
+
+def _step_tables(mq):
+    """(boff, NQ, NP, qbt64, aux, nqmax) of the quant group for this step, built once (kv800_hip_step_tables)."""
+    if ("step",) not in mq.cache:
+        nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
+        mq.cache[("step",)] = kv800_hip.step_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax, nnew=1,
+                                                    aux_scale=QPAGE // 2, aux_add=AUX_BYTES // 2) + (nqmax,)
+    return mq.cache[("step",)]
+
+
+_SIDE = {}
+
+
+def launch_flushes(layers, metas, mq, max_new=1):
+    """Start this step's flushes of the quantized layers at once, on a side stream (default priority), so that they
+    run under the decode of the layers before them; each layer's forward then only waits for its own flush. A step's
+    flush reads tokens written in earlier steps only (sub-block j flushes at n >= 256 j + 384, so it ends 128 tokens
+    before the step's token), and the side stream first waits for everything queued so far on the current stream.
+    layers: the KV800DecodeLayer objects of the step; metas: {layer index: its exact group's StepMeta}; mq: the quant
+    group's StepMeta. Call once per step, before the step's first attention layer."""
+    quant = [l for l in layers if not l.win]
+    if not quant:
+        return
+    dev = quant[0].ev.device
+    main = torch.cuda.current_stream(dev)
+    tabs = _step_tables(mq)                        # tables built on the current stream, before the fork
+    eoffs = {l.l: l._eoff(metas[l.l]) for l in quant}
+    side = _SIDE.get(dev)
+    if side is None:
+        side = _SIDE[dev] = torch.cuda.Stream(device=dev)
+    fork = torch.cuda.Event()
+    fork.record(main)
+    side.wait_event(fork)
+    with torch.cuda.stream(side):
+        for t in tabs[:5]:
+            if t is not None:
+                t.record_stream(side)
+        for l in quant:
+            eoffs[l.l].record_stream(side)
+            l._flush(metas[l.l], mq, max_new)
+            done = torch.cuda.Event()
+            done.record(side)
+            mq.cache[("flushed", l.l)] = done
 
 
 # ---------------------------------------------------------------- prefill / extend rows over compressed history

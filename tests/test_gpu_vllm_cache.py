@@ -33,7 +33,8 @@ def bits_of(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def test_vllm_decode_step(hip, oracle):
+@pytest.mark.parametrize("early_flush", [False, True])
+def test_vllm_decode_step(hip, oracle, early_flush):
     from lfm3_kv800_amd import vllm_cache as vc
     rng = np.random.RandomState(77)
     L0 = np.array([1407, 999, 2, 383, 3000, 1663], np.int64)   # lengths before the step
@@ -89,6 +90,9 @@ def test_vllm_decode_step(hip, oracle):
     metas = {g: vc.step_meta(torch.from_numpy(bt[g]), torch.from_numpy(n), EBS, DEV) for g in "AB"}
     mq = vc.step_meta(torch.from_numpy(qbt), torch.from_numpy(n), QBLOCK, DEV)
     cos_d, sin_d = bf16_dev(cos), bf16_dev(sin)
+    if early_flush:                                      # all quant layers' flushes ahead, on the side stream
+        say("launch_flushes")
+        vc.launch_flushes(list(lay.values()), {l: metas[group[l]] for l in layers}, mq)
     outs = {}
     for l in layers:
         K, V = hist[l]
