@@ -56,6 +56,28 @@ __device__ __forceinline__ uint32_t pk2(float a, float b) {   // two floats -> p
   return hbits(v);
 }
 
+// Values of the lanes 16 (32) apart without an LDS round trip: v_permlane16_swap (v_permlane32_swap) on two copies of
+// x leaves the even 16-lane row (lower half) in .x and the odd row (upper half) in .y, in both lanes of each pair, so
+// combining .x and .y gives the pair the same result. All 64 lanes must be active.
+__device__ __forceinline__ float2 rows16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 halves32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum4rows(float x) {   // sum over lanes l, l ^ 16, l ^ 32, l ^ 48
+  float2 p = rows16(x);
+  p = halves32(p.x + p.y);
+  return p.x + p.y;
+}
+__device__ __forceinline__ float max4rows(float x) {
+  float2 p = rows16(x);
+  p = halves32(fmaxf(p.x, p.y));
+  return fmaxf(p.x, p.y);
+}
+
 // Four fp8 e4m3fn bytes of w -> floats (byte i -> o[i]) with the hardware conversion: gfx950 converts the OCP e4m3
 // format, the same as torch's float8_e4m3fn, exactly; the NaN bytes 0x7F / 0xFF give NaN as torch's .float() does
 // (kv800.py:84-91; the quantizer writes them only for scales beyond +-464).
@@ -648,9 +670,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
             q1b.w * t1b.w + q3a.x * t3a.x + q3a.y * t3a.y + q3a.z * t3a.z + q3a.w * t3a.w + q3b.x * t3b.x +
             q3b.y * t3b.y + q3b.z * t3b.z + q3b.w * t3b.w;
     }
-    c13 += __shfl_xor(c13, 16);
-    c13 += __shfl_xor(c13, 32);
-    c13 *= scale;
+    c13 = sum4rows(c13) * scale;
     asm volatile("" ::: "memory");   // the scale staging reads above stay before the chunk stores below
 
     // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
@@ -714,8 +734,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
       float tmax = fmaxf(fmaxf(fmaxf(sacc2[0][0], sacc2[0][1]), fmaxf(sacc2[0][2], sacc2[0][3])),
                          fmaxf(fmaxf(sacc2[1][0], sacc2[1][1]), fmaxf(sacc2[1][2], sacc2[1][3])));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      tmax = max4rows(tmax);
       if (__any(tmax > m + LAZY)) {
         const float mn = fmaxf(m, tmax);
         const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
@@ -762,8 +781,8 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   }
 
   // ---- combine the 4 waves of the split
-  lsum += __shfl_xor(lsum, 16); lsum += __shfl_xor(lsum, 32);
-  lvs += __shfl_xor(lvs, 16);   lvs += __shfl_xor(lvs, 32);
+  lsum = sum4rows(lsum);
+  lvs = sum4rows(lvs);
   __syncthreads();
   QFinLds& F = *reinterpret_cast<QFinLds*>(lds_raw);
   if (g == 0) { F.m[w][n] = m; F.l[w][n] = lsum; F.lv[w][n] = lvs; }
