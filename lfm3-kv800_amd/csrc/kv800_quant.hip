@@ -77,6 +77,7 @@ __device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)
 #pragma unroll
   for (int k = 0; k < 64; k += 4) {
     __builtin_amdgcn_sched_barrier(0);   // one float4 of the row in flight: the chain is serial anyway
+    asm volatile("" ::: "memory");     // and no later read is moved up to here
     const float4 v4 = *reinterpret_cast<const float4*>(x + k);
     a = __builtin_fmaf(v4.x, hc[k], a);
     a = __builtin_fmaf(v4.y, hc[k + 1], a);
@@ -87,40 +88,12 @@ __device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)
 #pragma unroll
   for (int k = 64; k < 128; k += 4) {
     __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
     const float4 v4 = *reinterpret_cast<const float4*>(x + k);
     a = __builtin_fmaf(v4.x, hc[k - 64], a);     b = __builtin_fmaf(v4.x, -hc[k - 64], b);
     a = __builtin_fmaf(v4.y, hc[k - 63], a);     b = __builtin_fmaf(v4.y, -hc[k - 63], b);
     a = __builtin_fmaf(v4.z, hc[k - 62], a);     b = __builtin_fmaf(v4.z, -hc[k - 62], b);
     a = __builtin_fmaf(v4.w, hc[k - 61], a);     b = __builtin_fmaf(v4.w, -hc[k - 61], b);
-  }
-  ya = a;
-  yb = b;
-}
-
-typedef const __attribute__((address_space(4))) uint32_t* cu32p;   // read-only scalar-cache view
-
-// Same chain with x = a bf16 row in global memory at a wave-uniform address: the row is read with scalar loads
-// and converted on the scalar unit, so the x operand of every fma is an SGPR and no VGPRs hold the row.
-__device__ __forceinline__ void hadamard_chain_row(const uint16_t* row, const float (&hc)[64], float& ya, float& yb) {
-  const uint64_t ad = (uint64_t)(uintptr_t)row;
-  const uint32_t lo32 = __builtin_amdgcn_readfirstlane((uint32_t)ad), hi32 = __builtin_amdgcn_readfirstlane((uint32_t)(ad >> 32));
-  const cu32p r = (cu32p)(uintptr_t)(((uint64_t)hi32 << 32) | lo32);
-  float a = 0.f;
-#pragma unroll
-  for (int k = 0; k < 64; k += 2) {
-    if ((k & 31) == 0) __builtin_amdgcn_sched_barrier(0);   // at most a quarter row in SGPRs
-    const uint32_t wd = r[k >> 1];
-    a = __builtin_fmaf(__uint_as_float(wd << 16), hc[k], a);
-    a = __builtin_fmaf(__uint_as_float(wd & 0xFFFF0000u), hc[k + 1], a);
-  }
-  float b = a;
-#pragma unroll
-  for (int k = 64; k < 128; k += 2) {
-    if ((k & 31) == 0) __builtin_amdgcn_sched_barrier(0);
-    const uint32_t wd = r[k >> 1];
-    const float x0 = __uint_as_float(wd << 16), x1 = __uint_as_float(wd & 0xFFFF0000u);
-    a = __builtin_fmaf(x0, hc[k - 64], a);     b = __builtin_fmaf(x0, -hc[k - 64], b);
-    a = __builtin_fmaf(x1, hc[k - 63], a);     b = __builtin_fmaf(x1, -hc[k - 63], b);
   }
   ya = a;
   yb = b;
@@ -234,31 +207,39 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
 }
 
 // V bits and scales of tokens [t0, t0 + VTOK) of one sub-block: wave w takes VTPW consecutive tokens, per token its
-// 4 head rows with lane = dims lane, lane + 64. The rows reach the Hadamard chains through scalar loads (x is an
-// SGPR operand, no VGPRs hold the rows); every lane touches 16 bytes of the token two ahead with a vector load so
-// that those scalar loads find the rows in L2 instead of waiting on HBM.
+// 4 head rows with lane = dims lane, lane + 64. Each lane loads 16 bytes of a token's rows (head rh, dims rc .. +7),
+// two tokens ahead; the wave writes them as floats into its own 2 KB of LDS, and the 4 rows' Hadamard chains run
+// interleaved from there (hadamard_chain_rows4).
 constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
+constexpr int VLDS_BYTES = QW * 4 * 128 * 4;   // per wave: the current token's 4 rows as floats
 
 template <int VT, typename Src>
-__device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0) {
+__device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int tw = t0 + VT * w;                        // this wave's first token; VT tokens per wave
-  const int rh = lane >> 4, rc = 8 * (lane & 15);    // the 16 bytes this lane touches: head rh, dims rc .. rc + 7
-  auto touch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, rh) + rc); };
-  uint4 pf0 = touch(tw), pf1 = VT > 1 ? touch(tw + 1) : pf0;
+  const int rh = lane >> 4, rc = 8 * (lane & 15);    // the 16 bytes this lane loads: head rh, dims rc .. rc + 7
+  float (*xs)[128] = reinterpret_cast<float (*)[128]>(lds) + 4 * w;
+  auto fetch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, rh) + rc); };
+  uint4 pf0 = fetch(tw), pf1 = VT > 1 ? fetch(tw + 1) : pf0;
   float hcol[64];
   hadamard_column(hcol, lane);
 #pragma unroll 1
   for (int tt = 0; tt < VT; ++tt) {
     const int t = tw + tt;
-    asm volatile("" :: "v"(pf0.x), "v"(pf0.y), "v"(pf0.z), "v"(pf0.w));   // token t is in L2 by now
+    // token t's rows -> xs (a wave's LDS instructions execute in order: these stores follow the previous token's
+    // reads and precede this token's)
+    *reinterpret_cast<float4*>(xs[rh] + rc) = make_float4(bf2f_lo(pf0.x), bf2f_hi(pf0.x), bf2f_lo(pf0.y), bf2f_hi(pf0.y));
+    *reinterpret_cast<float4*>(xs[rh] + rc + 4) = make_float4(bf2f_lo(pf0.z), bf2f_hi(pf0.z), bf2f_lo(pf0.w), bf2f_hi(pf0.w));
     pf0 = pf1;
-    if (tt + 2 < VT) pf1 = touch(t + 2);
+    if (tt + 2 < VT) pf1 = fetch(t + 2);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float ya[4], yb[4];
-#pragma unroll
+#pragma unroll 1
     for (int r = 0; r < 4; ++r) {
-      __builtin_amdgcn_sched_barrier(0);
-      hadamard_chain_row(src.vrow(t, r), hcol, ya[r], yb[r]);
+      float a1, b1;
+      hadamard_chain(xs[r], hcol, a1, b1);
+      ya[r] = a1; yb[r] = b1;
     }
     uint64_t ma[4], mb[4];
 #pragma unroll
@@ -291,12 +272,12 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0) {
 // VSPLIT V workgroups (V is independent per token). Both passes fit one register budget, so 4 waves per SIMD run and
 // the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup i < units is the K pass of unit i;
 // i >= units is the V pass of unit (i - units) / VSPLIT, token range (i - units) % VSPLIT.
-constexpr int QLDS_BYTES = (int)sizeof(QuantLds);
+constexpr int QLDS_BYTES = (int)sizeof(QuantLds) > VLDS_BYTES ? (int)sizeof(QuantLds) : VLDS_BYTES;
 
 template <typename Src>
 __device__ __forceinline__ void quantize_part(const Src& src, uint8_t* __restrict__ out, char* lds, bool kpass, int part) {
   if (kpass) quantize_k(src, out, lds);
-  else quantize_v<VTPW>(src, out, part * VTOK);
+  else quantize_v<VTPW>(src, out, part * VTOK, lds);
 }
 
 __global__ void __launch_bounds__(QTHREADS) quantize_dense_kernel(const uint16_t* __restrict__ k,
@@ -352,7 +333,7 @@ __global__ void __launch_bounds__(QTHREADS) flush_lat_kernel(const uint16_t* __r
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
   const PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
   if (kpass) quantize_k<PagedSrc, 16>(src, dst, lds);
-  else quantize_v<1>(src, dst, (int)((i - units) % LSPLIT) * QW);
+  else quantize_v<1>(src, dst, (int)((i - units) % LSPLIT) * QW, lds);
 }
 
 // ---------------------------------------------------------------- dequantize (kv800.py:79-92)
