@@ -99,6 +99,37 @@ __device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)
   yb = b;
 }
 
+// The chains of two rows x0, x1 interleaved (each in hadamard_chain's order): two float4 reads in flight, and each
+// row's dependent fmas alternate with the other's.
+__device__ __forceinline__ void hadamard_chain2(const float* x0, const float* x1, const float (&hc)[64], float (&ya)[2],
+                                                float (&yb)[2]) {
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 64; k += 4) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    const float4 u = *reinterpret_cast<const float4*>(x0 + k), v = *reinterpret_cast<const float4*>(x1 + k);
+    a0 = __builtin_fmaf(u.x, hc[k], a0);     a1 = __builtin_fmaf(v.x, hc[k], a1);
+    a0 = __builtin_fmaf(u.y, hc[k + 1], a0); a1 = __builtin_fmaf(v.y, hc[k + 1], a1);
+    a0 = __builtin_fmaf(u.z, hc[k + 2], a0); a1 = __builtin_fmaf(v.z, hc[k + 2], a1);
+    a0 = __builtin_fmaf(u.w, hc[k + 3], a0); a1 = __builtin_fmaf(v.w, hc[k + 3], a1);
+  }
+  float b0 = a0, b1 = a1;
+#pragma unroll
+  for (int k = 64; k < 128; k += 4) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    const float4 u = *reinterpret_cast<const float4*>(x0 + k), v = *reinterpret_cast<const float4*>(x1 + k);
+    const float h0 = hc[k - 64], h1 = hc[k - 63], h2 = hc[k - 62], h3 = hc[k - 61];
+    a0 = __builtin_fmaf(u.x, h0, a0); b0 = __builtin_fmaf(u.x, -h0, b0); a1 = __builtin_fmaf(v.x, h0, a1); b1 = __builtin_fmaf(v.x, -h0, b1);
+    a0 = __builtin_fmaf(u.y, h1, a0); b0 = __builtin_fmaf(u.y, -h1, b0); a1 = __builtin_fmaf(v.y, h1, a1); b1 = __builtin_fmaf(v.y, -h1, b1);
+    a0 = __builtin_fmaf(u.z, h2, a0); b0 = __builtin_fmaf(u.z, -h2, b0); a1 = __builtin_fmaf(v.z, h2, a1); b1 = __builtin_fmaf(v.z, -h2, b1);
+    a0 = __builtin_fmaf(u.w, h3, a0); b0 = __builtin_fmaf(u.w, -h3, b0); a1 = __builtin_fmaf(v.w, h3, a1); b1 = __builtin_fmaf(v.w, -h3, b1);
+  }
+  ya[0] = a0; ya[1] = a1;
+  yb[0] = b0; yb[1] = b1;
+}
+
 __device__ __forceinline__ float wave_min(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
@@ -208,8 +239,8 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
 
 // V bits and scales of tokens [t0, t0 + VTOK) of one sub-block: wave w takes VTPW consecutive tokens, per token its
 // 4 head rows with lane = dims lane, lane + 64. Each lane loads 16 bytes of a token's rows (head rh, dims rc .. +7),
-// two tokens ahead; the wave writes them as floats into its own 2 KB of LDS, and the 4 rows' Hadamard chains run
-// interleaved from there (hadamard_chain_rows4).
+// two tokens ahead; the wave writes them as floats into its own 2 KB of LDS, and the rows' Hadamard chains run from
+// there two at a time (hadamard_chain2).
 constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
 constexpr int VLDS_BYTES = QW * 4 * 128 * 4;   // per wave: the current token's 4 rows as floats
 
@@ -236,10 +267,11 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float ya[4], yb[4];
 #pragma unroll 1
-    for (int r = 0; r < 4; ++r) {
-      float a1, b1;
-      hadamard_chain(xs[r], hcol, a1, b1);
-      ya[r] = a1; yb[r] = b1;
+    for (int r = 0; r < 4; r += 2) {   // a runtime loop: two rows' reads at a time keep the registers bounded
+      float a2[2], b2[2];
+      hadamard_chain2(xs[r], xs[r + 1], hcol, a2, b2);
+      ya[r] = a2[0]; ya[r + 1] = a2[1];
+      yb[r] = b2[0]; yb[r + 1] = b2[1];
     }
     uint64_t ma[4], mb[4];
 #pragma unroll
