@@ -276,6 +276,25 @@ def test_decode_shuffled_ragged(hip, oracle, win):
         close(bits_of(out), want, f"ragged win={win} spb={spb} groups={groups}")
 
 
+def test_decode_many_rows_few_groups(hip, oracle):
+    """Balanced schedule with workgroups spanning more rows than their 64-row offset table holds (the table is refilled
+    in rounds), rows without quantized sub-blocks between them, and row ranges that start and end inside rows."""
+    rng = np.random.RandomState(57)
+    lens = [int(x) for x in rng.randint(1, 1400, size=150)]
+    lens[10:20] = [1, 2, 127, 128, 129, 383, 384, 385, 639, 640]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (len(lens), 16, 128))
+    cos, sin = oracle.rope_tables(1500)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, ebs=128, shuffle_seed=57)
+    say("decode many rows", len(lens), "sub-blocks", int(case.NQ.sum()))
+    P = upload(case)
+    want = oracle.decode(case, q, cos, sin)
+    for groups in (1, 2, 7, None):
+        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), groups=groups)
+        close(bits_of(out), want, f"150 rows groups={groups}")
+
+
 def test_decode_stages_and_merge(hip, oracle):
     rng = np.random.RandomState(31)
     lens = [900, 3000, 1500]
