@@ -473,10 +473,12 @@ __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restri
     reinterpret_cast<float4*>(X)[64 + lane] = b;
     __builtin_amdgcn_wave_barrier();
     float ya[4], yb[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      __builtin_amdgcn_sched_barrier(0);   // one chain's row reads in flight at a time
-      hadamard_chain(X + r * 128, hcol, ya[r], yb[r]);
+#pragma unroll 1
+    for (int r = 0; r < 4; r += 2) {   // a runtime loop: two rows' reads at a time keep the registers bounded
+      float a2[2], b2[2];
+      hadamard_chain2(X + r * 128, X + (r + 1) * 128, hcol, a2, b2);
+      ya[r] = a2[0]; ya[r + 1] = a2[1];
+      yb[r] = b2[0]; yb[r + 1] = b2[1];
     }
     float za[4], zb[4];
 #pragma unroll
@@ -498,13 +500,14 @@ __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restri
 #pragma unroll
     for (int r = 0; r < 4; ++r) { X[r * 128 + lane] = za[r]; X[r * 128 + 64 + lane] = zb[r]; }
     __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float oa, ob;
-      __builtin_amdgcn_sched_barrier(0);
-      hadamard_chain(X + r * 128, hcol, oa, ob);
-      out[t * 512 + r * 128 + lane] = oa;
-      out[t * 512 + r * 128 + 64 + lane] = ob;
+#pragma unroll 1
+    for (int r = 0; r < 4; r += 2) {
+      float oa[2], ob[2];
+      hadamard_chain2(X + r * 128, X + (r + 1) * 128, hcol, oa, ob);
+      out[t * 512 + r * 128 + lane] = oa[0];
+      out[t * 512 + r * 128 + 64 + lane] = ob[0];
+      out[t * 512 + (r + 1) * 128 + lane] = oa[1];
+      out[t * 512 + (r + 1) * 128 + 64 + lane] = ob[1];
     }
     __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite X
   }
