@@ -97,38 +97,50 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
 // ---------------------------------------------------------------- exact tail + sinks
 // A workgroup of 4 waves takes NH KV heads of one row b (query rows 4 h .. 4 h + 3 of head h): NH = 4, one wave per
 // head; NH = 1, the 4 waves take the head's 32-token chunks in turn (wave w: chunks w, w + 4, ...) and merge their
-// states at the end. The tokens are the row's sinks, then its exact positions. QK: two lanes per token (lane l: token
-// l % 32, channels j = 16 (l / 32) + e, e < 16, i.e. dims j, j + 32, j + 64, j + 96); the rotated pair (j, j + 64) is
-// rounded to bf16 by one packed convert and dotted with bf16 q pairs on v_dot2 (exact products, fp32 sums), the
-// unrotated pair (j + 32, j + 96) as stored. PV: lane l = dims 2 l, 2 l + 1, fp32. A wave requests its next chunk's
-// K, V and rope rows before computing the current one, and the row's page-table entries sit in LDS, so no load inside
-// the loop waits on another.
+// states at the end. The tokens are the row's sinks, then its exact positions. Both products run on MFMA
+// f32_16x16x32_bf16 with a 32-token chunk as two 16-token tiles u; lane (g, n) = (lane / 16, lane % 16):
+// - QK: A = the tile's K rows (row n = token 16 u + n; k-step s = dims 32 s + 8 g .. + 7), B = q (column n < 8 =
+//   query row n % 4, zero above). The RoPE pairs (j, j + 64), j < 32, are rotated in fp32 and rounded to bf16 by one
+//   packed convert (RNE, as kv800.py:182-183); the NoPE dims go in as stored. Score register i of tile u in lane
+//   (g, n) is token 16 u + 4 g + i, column n.
+// - softmax: fp32, log2 units, with a lazy running max (rescale only when a chunk max exceeds it by more than LAZY).
+// - PV: A = V^T (row = dim; K = the 8 tokens 4 g .. 4 g + 3, 16 + 4 g .. + 3 whose scores the lane holds), read by
+//   ds_read_b64_tr_b16 from the wave's LDS copy of the chunk's V rows; B = the weights in bf16, hi = bf16(p) in
+//   columns 0..3 and lo = bf16(p - hi) in the duplicate columns 4..7, so hi + lo carries p to ~16 bits.
+// A wave requests its next chunk's K, V and rope rows before computing the current one; the row's page-table entries
+// sit in LDS, so no load inside the loop waits on another.
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
 constexpr int XCH = 32;                // tokens per chunk
 constexpr int XPG = 64;                // page-table entries of the row kept in LDS (later pages are read from memory)
-struct XWaveLds {
-  float4 p[XCH];                       // softmax weights of the chunk's tokens, rows 0..3
-  const uint16_t* vrow[XCH];           // V row of each token of the chunk (masked tokens: row 0 of the exact pool)
-};
+constexpr int XVROW = 144;             // bf16 per staged V row: 128 + 16 padding spreads a tile's rows over the banks
+constexpr int XTROW = 132;             // floats per row of the end-of-row column dump
 struct XLds {
-  bf2 q[4][32][2][4];                  // head slot, channel j: (q_r[j], q_r[j + 64]) r = 0..3; (q_r[j + 32], q_r[j + 96])
-  XWaveLds wv[4];
   int64_t pg[XPG];                     // element offsets of the row's exact pages, from page lo_e / ebs on
+  uint16_t v[4][XCH][XVROW];           // each wave's copy of its chunk's V rows; at the end its columns and (m, l)
+  u4v qb[4][4][64];                    // each wave's QK B operand: k-step s of lane l in qb[w][s][l]
   float fm[4][4], fl[4][4];            // NH = 1: each wave's m and l of rows 0..3
   float facc[4][4][128];               // NH = 1: each wave's accumulators of rows 0..3
 };
-struct XChunk {                        // one chunk's data in registers
-  u4v k[8];                            // K dims 32 qq + 16 hf .. + 15: k[2 qq], k[2 qq + 1]
-  u4v c[2], s[2];                      // cos / sin of channels 16 hf .. + 15
-  uint32_t v[XCH];                     // dims 2 lane, 2 lane + 1 of the chunk's V rows
-  uint32_t vmask;                      // chunk tokens with a V row
-  bool valid;                          // this lane's token has a K row and a rope row
+static_assert(sizeof(float) * (8 * XTROW + 8) <= sizeof(uint16_t) * XCH * XVROW, "column dump must fit the V copy");
+struct XChunk {                        // one chunk's data in registers; lane (g, r): token 16 u + r of tile u
+  u4v k[2][4];                         // K dims 32 s + 8 g .. + 7
+  u4v v[2][4];                         // V dims 32 s + 8 g .. + 7
+  u4v c[2], s[2];                      // cos / sin of channels 8 g .. + 7 at the token's position
+  uint32_t ok;                         // chunk tokens with K, V and rope rows (bit t = chunk token t)
 };
-__device__ __forceinline__ uint32_t u16of(const u4v& a, const u4v& b, int e) {   // 16-bit element e < 16 of (a, b)
-  const u4v& x = e < 8 ? a : b;
-  const uint32_t w = x[(e & 7) >> 1];
-  return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+__device__ __forceinline__ float bf_elem(const u4v& x, int e) {   // bf16 element e < 8 of x as a float
+  const uint32_t w = x[e >> 1];
+  return __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
 }
+__device__ __forceinline__ uint32_t bfpk(float a, float b) {   // two floats -> packed bf16 (round to nearest even)
+  const bf2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ b8 as_b8(const u4v& x) { return __builtin_bit_cast(b8, x); }
+__device__ __forceinline__ f4 mfma_bf(b8 a, b8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 
 // MERGE = false: writes the exact partial (m, l, acc) of the heads' rows into partial slot xslot.
 // MERGE = true : instead merges it with the ns quantized partials of those rows (slots b (ns + 1) + s, written before
@@ -142,9 +154,8 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
                                           int ns, int64_t xslot, float scale, int nsink, uint16_t* __restrict__ out) {
   static_assert(NH == 1 || NH == 4, "a workgroup takes one KV head or all four");
   constexpr int WPH = 4 / NH;          // waves per head
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hf = lane >> 5;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int hl = w / WPH, ph = w % WPH, h = h0 + hl;   // head slot, chunk phase, KV head
-  XWaveLds& W = X.wv[w];
   const int n = P.N[b];
   int lo_e = P.NQ[b] * BLK;
   if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
@@ -154,16 +165,13 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
   const int64_t* et = P.eoff + (int64_t)b * P.eoff_stride;
   const int64_t p0 = lo_e / P.ebs;
   if (tid < XPG) X.pg[tid] = (p0 + tid < P.eoff_stride) ? et[p0 + tid] : -1;
-  if (tid < 64 * NH) {   // q pairs: thread -> head slot tid / 64, channel (tid % 64) / 2, pair kind tid % 2
-    const int hs = tid >> 6, j = (tid & 63) >> 1, o = 32 * (tid & 1);
-    uint32_t pr[4];
+  // q as the QK B operand: column r16 < 8 holds query row 4 h + r16 % 4, dims 32 s + 8 g .. + 7 in k-step s (kept in
+  // LDS and read per chunk: 16 registers fewer across the loop)
+  {
+    const uint16_t* qr = q + ((int64_t)b * 16 + 4 * h + (r16 & 3)) * 128 + 8 * g;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint16_t* qr = q + ((int64_t)b * 16 + 4 * (h0 + hs) + r) * 128;
-      pr[r] = (uint32_t)qr[j + o] | ((uint32_t)qr[j + o + 64] << 16);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) X.q[hs][j][tid & 1][r] = __builtin_bit_cast(bf2, pr[r]);
+    for (int s = 0; s < 4; ++s)
+      X.qb[w][s][lane] = (r16 < 8) ? *reinterpret_cast<const u4v*>(qr + 32 * s) : u4v{0u, 0u, 0u, 0u};
   }
   const int64_t sko = cnt ? P.skoff[b] : 0, svo = cnt ? P.svoff[b] : 0;
   __syncthreads();
@@ -186,116 +194,164 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
       if (base < 0 || ko < 0 || ko + 128 > epool_elems || vo + 128 > epool_elems) ko = vo = -1;
     }
   };
+  // lanes without a token read the row's first query row instead (finite data: its scores are masked and its
+  // weights are zero, so nothing of it reaches the output), which keeps every load unconditional
+  const uint16_t* qf = q + (int64_t)b * 16 * 128 + 8 * g;
   auto load = [&](int c0, XChunk& C) {
-    const int t = c0 + (lane & 31);
-    int64_t ko = -1, vo = -1;
-    int pos = 0;
-    if (t < T) rows(t, ko, vo, pos);
-    C.valid = t < T && ko >= 0 && pos < rope_rows;
-    const bool vok = C.valid && vo >= 0;
-    const uint16_t* Kb = (t < cnt) ? P.sk : P.epool;
-    if (lane < 32) W.vrow[lane] = vok ? ((t < cnt) ? P.sv : P.epool) + vo : P.epool;
-    C.vmask = (uint32_t)__ballot(vok);
-    if (C.valid) {
-      const uint16_t* kr = Kb + ko + 16 * hf;
+    uint32_t okm = 0;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        C.k[2 * qq] = *reinterpret_cast<const u4v*>(kr + 32 * qq);
-        C.k[2 * qq + 1] = *reinterpret_cast<const u4v*>(kr + 32 * qq + 8);
+    for (int u = 0; u < 2; ++u) {
+      const int t = c0 + 16 * u + r16;
+      int64_t ko = -1, vo = -1;
+      int pos = 0;
+      if (t < T) rows(t, ko, vo, pos);
+      const bool ok = t < T && ko >= 0 && pos < rope_rows;   // rows() sets ko and vo out of range together
+      const uint16_t *kr = qf, *vr = qf, *cr = qf, *sr = qf;
+      if (ok) {
+        kr = ((t < cnt) ? P.sk : P.epool) + ko + 8 * g;
+        vr = ((t < cnt) ? P.sv : P.epool) + vo + 8 * g;
+        cr = cos_t + (int64_t)pos * 32 + 8 * g;
+        sr = sin_t + (int64_t)pos * 32 + 8 * g;
       }
-      const int64_t ro = (int64_t)pos * 32 + 16 * hf;
-      C.c[0] = *reinterpret_cast<const u4v*>(cos_t + ro); C.c[1] = *reinterpret_cast<const u4v*>(cos_t + ro + 8);
-      C.s[0] = *reinterpret_cast<const u4v*>(sin_t + ro); C.s[1] = *reinterpret_cast<const u4v*>(sin_t + ro + 8);
-    }
-    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int j = 0; j < XCH; ++j) C.v[j] = *reinterpret_cast<const uint32_t*>(W.vrow[j] + 2 * lane);
+      for (int s = 0; s < 4; ++s) C.k[u][s] = *reinterpret_cast<const u4v*>(kr + 32 * s);
+      C.c[u] = *reinterpret_cast<const u4v*>(cr);
+      C.s[u] = *reinterpret_cast<const u4v*>(sr);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) C.v[u][s] = *reinterpret_cast<const u4v*>(vr + 32 * s);
+      okm |= ((uint32_t)__ballot(ok) & 0xFFFFu) << (16 * u);
+    }
+    C.ok = okm;
   };
 
-  float m[4] = {NEG_BIG, NEG_BIG, NEG_BIG, NEG_BIG}, lsum[4] = {0, 0, 0, 0};
-  float acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  auto compute = [&](const XChunk& C) {
-    float sc[4] = {0.f, 0.f, 0.f, 0.f};
+  uint16_t (*Vs)[XVROW] = X.v[w];
+  float m = NEG_BIG, lsum = 0.f;      // column r16's running max; this lane's share of its weight sum
+  f4 acc[8];                          // dims 16 j + 4 g + i of column r16
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      // the q reads stay next to their use: without the clobber they are loop-invariant and all 128 get hoisted
-      if ((e & 3) == 0) asm volatile("" ::: "memory");
-      const int j = 16 * hf + e;
-      const float k0 = __uint_as_float(u16of(C.k[0], C.k[1], e) << 16);
-      const float k2 = __uint_as_float(u16of(C.k[4], C.k[5], e) << 16);
-      const float cs = __uint_as_float(u16of(C.c[0], C.c[1], e) << 16);
-      const float sn = __uint_as_float(u16of(C.s[0], C.s[1], e) << 16);
-      const bf2 pr = {(__bf16)__fsub_rn(__fmul_rn(k0, cs), __fmul_rn(k2, sn)),
-                      (__bf16)__fadd_rn(__fmul_rn(k2, cs), __fmul_rn(k0, sn))};
-      const uint32_t pn32 = u16of(C.k[2], C.k[3], e) | (u16of(C.k[6], C.k[7], e) << 16);
-      const bf2 pn = __builtin_bit_cast(bf2, pn32);
-      // q pairs are read from LDS as bf16-pair values: taking them as components of a 4 x uint32 vector and
-      // bit-casting each to a bf16 pair makes this compiler fold the four rows' dot products into row 0's
+  for (int j = 0; j < 8; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+  // the chunk's V rows into the wave's LDS rows (row = chunk token; the previous chunk's reads are issued before)
+  auto stage = [&](const XChunk& C) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sc[r] = __builtin_amdgcn_fdot2_f32_bf16(X.q[hl][j][0][r], pr, sc[r], false);
-        sc[r] = __builtin_amdgcn_fdot2_f32_bf16(X.q[hl][j][1][r], pn, sc[r], false);
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) *reinterpret_cast<u4v*>(&Vs[16 * u + r16][32 * s + 8 * g]) = C.v[u][s];
+  };
+  auto qk = [&](const XChunk& C, f4 (&sc)[2]) {
+    asm volatile("" ::: "memory");   // keeps the q reads in the loop
+    u4v qb[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qb[s] = X.qb[w][s][lane];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u4v a0, a2;   // rotated dims 8 g .. + 7 and 64 + 8 g .. + 7, bf16
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float r0[2], r2[2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+#pragma clang fp contract(off)   // products rounded before the sum, as torch_decode.py:22-23 evaluates them
+          const float k0 = bf_elem(C.k[u][0], e + d), k2 = bf_elem(C.k[u][2], e + d);
+          const float cs = bf_elem(C.c[u], e + d), sn = bf_elem(C.s[u], e + d);
+          r0[d] = k0 * cs - k2 * sn;
+          r2[d] = k2 * cs + k0 * sn;
+        }
+        a0[e >> 1] = bfpk(r0[0], r0[1]);
+        a2[e >> 1] = bfpk(r2[0], r2[1]);
+        __builtin_amdgcn_sched_barrier(0);   // one channel pair's temporaries at a time
       }
+      f4 x = {0.f, 0.f, 0.f, 0.f};
+      x = mfma_bf(as_b8(a0), as_b8(qb[0]), x);
+      x = mfma_bf(as_b8(C.k[u][1]), as_b8(qb[1]), x);
+      x = mfma_bf(as_b8(a2), as_b8(qb[2]), x);
+      x = mfma_bf(as_b8(C.k[u][3]), as_b8(qb[3]), x);
+      sc[u] = x;
     }
-    // the two channel halves summed outside any branch (a shuffle cannot sink into one, so neither can the dot
-    // products, whose inputs would otherwise all stay live up to the branch)
-    float tot[4];
+  };
+  auto pv = [&](const XChunk& C, const f4 (&sc)[2]) {
+    const uint32_t tb = C.ok >> (4 * g);   // bit 16 u + i: token 16 u + 4 g + i
+    float xs[2][4], cm = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) tot[r] = sc[r] + __shfl_xor(sc[r], 32);
-    float p[4];
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = C.valid ? tot[r] * scale : -INFINITY;
-      float cm = x;
+      for (int i = 0; i < 4; ++i) {
+        xs[u][i] = ((tb >> (16 * u + i)) & 1u) ? sc[u][i] * scale : -INFINITY;
+        cm = fmaxf(cm, xs[u][i]);
+      }
+    cm = max4rows(cm);
+    if (__ballot(cm > m + LAZY)) {
+      const float mn = fmaxf(m, cm), al = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      lsum *= al;
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
-      const float mn = fmaxf(m[r], cm);
-      const float al = exp2f(m[r] - mn);
-      m[r] = mn;
-      p[r] = C.valid ? exp2f(x - mn) : 0.f;
-      lsum[r] = lsum[r] * al + p[r];
-      acc[r][0] *= al; acc[r][1] *= al;
+      for (int j = 0; j < 8; ++j) acc[j] *= al;
     }
-    if (lane < 32) W.p[lane] = make_float4(p[0], p[1], p[2], p[3]);
-    __builtin_amdgcn_wave_barrier();
+    u4v bp;   // weights of the lane's 8 tokens in K order, column r16: hi (r16 < 4), lo (4 <= r16 < 8), 0 above
 #pragma unroll
-    for (int t = 0; t < XCH; ++t) {
-      if ((t & 7) == 0) __builtin_amdgcn_sched_barrier(0);   // bounds the weight reads in flight
-      const float4 pp = W.p[t];   // zero for masked tokens and tokens past the row
-      const uint32_t vj = ((C.vmask >> t) & 1u) ? C.v[t] : 0u;
-      const float v0 = bf2f_lo(vj), v1 = bf2f_hi(vj);
-      acc[0][0] += pp.x * v0; acc[0][1] += pp.x * v1;
-      acc[1][0] += pp.y * v0; acc[1][1] += pp.y * v1;
-      acc[2][0] += pp.z * v0; acc[2][1] += pp.z * v1;
-      acc[3][0] += pp.w * v0; acc[3][1] += pp.w * v1;
+    for (int k = 0; k < 4; ++k) {
+      const int u = k >> 1, i = 2 * (k & 1);
+      const float pa = __builtin_amdgcn_exp2f(xs[u][i] - m), pb = __builtin_amdgcn_exp2f(xs[u][i + 1] - m);
+      lsum += pa + pb;
+      const uint32_t hi = bfpk(pa, pb);
+      const uint32_t lo = bfpk(pa - __uint_as_float(hi << 16), pb - __uint_as_float(hi & 0xFFFF0000u));
+      bp[k] = (r16 < 4) ? hi : ((r16 < 8) ? lo : 0u);
     }
-    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");   // the staged V rows are written before the transposed reads
+    const int vrow = 4 * g + (r16 >> 2), vcol = 4 * (r16 & 3);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const s4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&Vs[vrow][16 * j + vcol]);
+      const s4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&Vs[vrow + 16][16 * j + vcol]);
+      const u4v av = {__builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 0, 1)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 2, 3)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(t1, t1, 0, 1)),
+                      __builtin_bit_cast(uint32_t, __builtin_shufflevector(t1, t1, 2, 3))};
+      acc[j] = mfma_bf(as_b8(av), as_b8(bp), acc[j]);
+    }
+    asm volatile("" ::: "memory");   // and read before the next chunk's rows overwrite them
   };
   constexpr int STEP = WPH * XCH;     // tokens between this wave's chunks
   if (ph * XCH < T) {
     XChunk A, Bc;
+    f4 sc[2];
     load(ph * XCH, A);
-    for (int c0 = ph * XCH;;) {   // two chunk buffers, each loaded one chunk ahead of its use
-      if (c0 + STEP < T) load(c0 + STEP, Bc);
-      compute(A);
+    // two chunk buffers, each loaded one chunk ahead of its use; the loads are unconditional (past the row they
+    // request nothing and give zeros), so neither buffer's old contents stay live across the loop
+    for (int c0 = ph * XCH;;) {
+      load(c0 + STEP, Bc);
+      stage(A);
+      qk(A, sc);
+      pv(A, sc);
       c0 += STEP;
       if (c0 >= T) break;
-      if (c0 + STEP < T) load(c0 + STEP, A);
-      compute(Bc);
+      load(c0 + STEP, A);
+      stage(Bc);
+      qk(Bc, sc);
+      pv(Bc, sc);
       c0 += STEP;
       if (c0 >= T) break;
     }
   }
 
-  // ---- l over the 32 token lanes (both halves hold the same values); lane owns dims 2 lane, 2 lane + 1
+  // ---- columns -> rows: row r = column r (hi) + column r + 4 (lo); lane owns dims 2 lane, 2 lane + 1 of each row
+  lsum = sum4rows(lsum);
+  float* Tc = reinterpret_cast<float*>(&Vs[0][0]);   // [8][XTROW] columns, then m and l of rows 0..3
+  if (r16 < 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<f4*>(Tc + r16 * XTROW + 16 * j + 4 * g) = acc[j];
+  }
+  if (lane < 4) { Tc[8 * XTROW + lane] = m; Tc[8 * XTROW + 4 + lane] = lsum; }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
   const int dd = 2 * lane;
-  float Lr[4];
+  float mr[4], Lr[4], ar[4][2];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float L = lsum[r];
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o);
-    Lr[r] = L;
+    const float2 hi2 = *reinterpret_cast<const float2*>(Tc + r * XTROW + dd);
+    const float2 lo2 = *reinterpret_cast<const float2*>(Tc + (r + 4) * XTROW + dd);
+    ar[r][0] = hi2.x + lo2.x;
+    ar[r][1] = hi2.y + lo2.y;
+    mr[r] = Tc[8 * XTROW + r];
+    Lr[r] = Tc[8 * XTROW + 4 + r];
   }
   // (m, l, o0, o1) of query row 4 h + r of this row b -> its partial slot, or merged with the quantized partials
   auto emit = [&](int r, float M, float L, float o0, float o1) {
@@ -358,12 +414,12 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
   };
   if constexpr (NH == 4) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) emit(r, m[r], Lr[r], acc[r][0], acc[r][1]);
+    for (int r = 0; r < 4; ++r) emit(r, mr[r], Lr[r], ar[r][0], ar[r][1]);
   } else {   // the 4 waves' states of each row, merged by wave r for row r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (lane == 0) { X.fm[w][r] = m[r]; X.fl[w][r] = Lr[r]; }
-      *reinterpret_cast<float2*>(&X.facc[w][r][dd]) = make_float2(acc[r][0], acc[r][1]);
+      if (lane == 0) { X.fm[w][r] = mr[r]; X.fl[w][r] = Lr[r]; }
+      *reinterpret_cast<float2*>(&X.facc[w][r][dd]) = make_float2(ar[r][0], ar[r][1]);
     }
     __syncthreads();
     const int r = w;
@@ -383,9 +439,11 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
   }
 }
 
-// KV heads per workgroup of the standalone exact kernel (window layers) and of the exact-tail workgroups of the
-// quantized grid, which must finish early to free their CUs for the split work
+// KV heads per workgroup of the fused exact kernel (window layers) and of the exact-tail workgroups of the quantized
+// grid, which must finish early to free their CUs for the split work. The standalone partial-writing variant uses the
+// tails' split, so its partials are bit-identical to the ones the quantized grid computes in-grid.
 constexpr int XNH = 4, XNH_TAIL = 1;
+template <bool MERGE> constexpr int exact_nh() { return MERGE ? XNH : XNH_TAIL; }
 
 template <bool MERGE>
 __global__ void __launch_bounds__(256)
@@ -394,9 +452,9 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
                     int nsink, uint16_t* __restrict__ out) {
   __shared__ XLds X;
-  constexpr int G = 4 / XNH;   // workgroups per row
+  constexpr int NH = exact_nh<MERGE>(), G = 4 / NH;   // KV heads per workgroup, workgroups per row
   const int b = blockIdx.x / G;
-  exact_row<XNH, MERGE>(X, b, (blockIdx.x % G) * XNH, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
+  exact_row<NH, MERGE>(X, b, (blockIdx.x % G) * NH, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
                         lo_out, ao, ns, (int64_t)b * (ns + 1) + ns, scale, nsink, out);
 }
 
@@ -987,13 +1045,13 @@ int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_
   if (B == 0) return KV800_OK;
   int nsink = 0, rc;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &nsink)) != KV800_OK) return rc;
+  const unsigned grid = (unsigned)(B * (4 / (out ? exact_nh<true>() : exact_nh<false>())));
   if (out)
-    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3((unsigned)(B * (4 / XNH))), dim3(256), 0, (hipStream_t)stream, *P, q,
-                       cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
+    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t, sin_t,
+                       rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
   else
-    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3((unsigned)(B * (4 / XNH))), dim3(256), 0, (hipStream_t)stream, *P,
-                       q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink,
-                       (uint16_t*)nullptr);
+    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t, sin_t,
+                       rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, (uint16_t*)nullptr);
   return check_launch(out ? "decode_exact_merge" : "decode_exact");
 }
 
