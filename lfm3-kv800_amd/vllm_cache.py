@@ -175,10 +175,11 @@ def rope_keys(k, pos, cos_t, sin_t):
     return (kf * c + torch.cat((-kf[..., 64:], kf[..., :64]), -1) * s).to(torch.bfloat16)
 
 
-def prefill_attention(q, K, V, kp, n0, n):
-    """Causal attention of the queries at positions n0 .. n-1 over keys at positions kp (vllm_attn.py:168-184, the
-    quantized layers' mask): q (n - n0, 16, 128), K / V (S, 4, 128) bf16 -> (n - n0, 16, 128) fp32. fp32 products on
-    contiguous operands, 512 queries at a time."""
+def prefill_attention(q, K, V, kp, n0, n, window=0):
+    """Causal attention of the queries at positions n0 .. n-1 over keys at positions kp (vllm_attn.py:168-184):
+    q (n - n0, 16, 128), K / V (S, 4, 128) bf16 -> (n - n0, 16, 128) fp32. window = 0: the quantized layers' mask
+    (kp <= query position); window > 0: the window layers' mask, which also keeps a key only if it is one of the last
+    `window` positions or a sink (kp < NSINK). fp32 products on contiguous operands, 512 queries at a time."""
     Kf = K.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()           # (16, S, 128)
     KT = Kf.transpose(1, 2).contiguous()                                          # (16, 128, S)
     Vf = V.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()
@@ -186,7 +187,10 @@ def prefill_attention(q, K, V, kp, n0, n):
     qp = torch.arange(n0, n, device=q.device)
     out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     for a in range(0, n - n0, 512):
-        m = kp[None] <= qp[a:a + 512, None]
+        qa = qp[a:a + 512, None]
+        m = kp[None] <= qa
+        if window:
+            m = m & ((kp[None] > qa - window) | (kp[None] < kv800.NSINK))
         sc = torch.matmul(qi[:, a:a + 512].contiguous(), KT) * (128 ** -0.5)
         w = sc.masked_fill(~m[None], float("-inf")).softmax(-1)
         out[a:a + 512] = torch.matmul(w, Vf).transpose(0, 1)
@@ -212,4 +216,49 @@ def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
         Vb = torch.cat((Vh[offs[i]:offs[i] + n0], v[s:e].to(torch.bfloat16)))
         kp = torch.arange(n, device=q.device)
         out[s:e] = prefill_attention(q[s:e], Kb, Vb, kp, n0, n).to(torch.bfloat16)
+    return out
+
+
+def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
+    """Prefill / extend rows of a window layer (vllm_attn.py:351-402 with win set): row i has queries
+    q[qsl[i]:qsl[i+1]] (post-RoPE) at positions prev[i] .. prev[i] + (qsl[i+1] - qsl[i]) - 1 and new pre-RoPE keys and
+    values k / v at the same rows. Its history is what the window layer keeps: the sinks (positions < min(NSINK, lo))
+    at P.skoff / P.svoff in P.sk / P.sv, and the exact rows [lo, prev[i]) with lo = max(0, prev[i] - (WIN - 1)) in the
+    exact pages of P (P.eoff element offsets per ebs positions, e_hs / e_ts / e_v strides). All keys are rotated as
+    the reference does, then attention with the window + sinks mask. qsl / prev are host sequences. Returns
+    (T, 16, 128) bf16."""
+    R, dev = len(prev), q.device
+    ef = P.epool.reshape(-1)
+    eoff = P.eoff.cpu()
+    sinks = P.sk is not None
+    skoff = P.skoff.cpu() if sinks else None
+    svoff = P.svoff.cpu() if sinks else None
+    d128 = torch.arange(128, device=dev)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        s, e, n0 = int(qsl[i]), int(qsl[i + 1]), int(prev[i])
+        n = n0 + (e - s)
+        lo = max(0, n0 - (kv800.WIN - 1))
+        ns = min(kv800.NSINK, lo) if sinks else 0
+        ks, vs, ps = [], [], []
+        if ns:
+            rows = (torch.arange(ns, device=dev)[:, None] * 4 + torch.arange(4, device=dev)[None]) * 128   # (ns, 4)
+            ks.append(P.sk.reshape(-1)[int(skoff[i]) + rows[..., None] + d128])
+            vs.append(P.sv.reshape(-1)[int(svoff[i]) + rows[..., None] + d128])
+            ps.append(torch.arange(ns, device=dev))
+        if n0 > lo:
+            pp = torch.arange(lo, n0)
+            base = eoff[i, pp // P.ebs]
+            if bool((base < 0).any()):
+                raise ValueError(f"row {i}: exact page of a window position [{lo}, {n0}) is not mapped")
+            ko = (base + (pp % P.ebs) * P.e_ts).to(dev)[:, None] + torch.arange(4, device=dev)[None] * P.e_hs   # (S, 4)
+            ks.append(ef[ko[..., None] + d128])
+            vs.append(ef[ko[..., None] + P.e_v + d128])
+            ps.append(pp.to(dev))
+        ks.append(k[s:e].to(torch.bfloat16)); vs.append(v[s:e].to(torch.bfloat16))
+        ps.append(torch.arange(n0, n, device=dev))
+        kp = torch.cat(ps)
+        Kb = rope_keys(torch.cat(ks), kp, cos_t, sin_t)
+        Vb = torch.cat(vs)
+        out[s:e] = prefill_attention(q[s:e], Kb, Vb, kp, n0, n, window=kv800.WIN).to(torch.bfloat16)
     return out

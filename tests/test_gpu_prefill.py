@@ -113,3 +113,54 @@ def test_prefill_quant_rows(hip, oracle):
         d = np.abs(o[qsl[b]:qsl[b + 1]] - want)
         say(f"row {b}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
         assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (b, d.max(), d.mean())
+
+
+def upload_window(case):
+    import lfm3_kv800_amd.kv800 as kv
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return kv.Paged(qpool=to_dev_bf16(case.epool), boff=T(case.eoff), epool=to_dev_bf16(case.epool), eoff=T(case.eoff),
+                    ebs=case.ebs, e_hs=case.e_hs, e_ts=case.e_ts, e_v=case.e_v, sk=to_dev_bf16(case.sk),
+                    sv=to_dev_bf16(case.sv), skoff=T(case.skoff), svoff=T(case.svoff), N=T(case.N), NQ=T(case.NQ),
+                    nqmax=0, win=case.win)
+
+
+def test_prefill_window_rows(hip, oracle):
+    """Extend rows of a window layer: queries at positions n0 .. n-1 over the sinks, the last 255 exact positions
+    and the new rows, with the window + sinks mask (vllm_attn.py:351-402, 168-184), against a float64 attention over
+    the same keys / values taken from the inputs (not from the pages)."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    rng = np.random.RandomState(13)
+    prev = [0, 3, 200, 256, 700, 1300]
+    new = [6, 9, 70, 1, 300, 40]
+    lens = [p + t for p, t in zip(prev, new)]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    cos, sin = oracle.rope_tables(1400)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), prev, win=256, ebs=64, shuffle_seed=6)
+    P = upload_window(case)
+    q = oracle.randn_bf16(rng, (sum(new), 16, 128))
+    qsl = np.concatenate([[0], np.cumsum(new)])
+    kn = np.concatenate([K[b][prev[b]:] for b in range(len(prev))])
+    vn = np.concatenate([V[b][prev[b]:] for b in range(len(prev))])
+    say("window prefill rows", prev, new)
+    out = vc.prefill_window_rows(P, to_dev_bf16(q), to_dev_bf16(kn), to_dev_bf16(vn), qsl, prev, to_dev_bf16(cos),
+                                 to_dev_bf16(sin))
+    o = torch.from_numpy(bits_of(out).view(np.int16)).view(torch.bfloat16).float().numpy()
+    W, NS = 256, 4
+    for b in range(len(prev)):
+        n0, n = prev[b], lens[b]
+        lo = max(0, n0 - (W - 1))
+        kp = np.concatenate([np.arange(min(NS, lo)), np.arange(lo, n)])
+        Kr = oracle.bf16_to_f32(rope_np(oracle, K[b][kp], kp, cos, sin)).astype(np.float64)
+        Vf = oracle.bf16_to_f32(V[b][kp]).astype(np.float64)
+        qf = oracle.bf16_to_f32(q[qsl[b]:qsl[b + 1]]).astype(np.float64)
+        Kr, Vf = np.repeat(Kr, 4, axis=1), np.repeat(Vf, 4, axis=1)
+        sc = np.einsum("thd,shd->hts", qf, Kr) * 128 ** -0.5
+        qp = np.arange(n0, n)[None, :, None]
+        keep = (kp[None, None, :] <= qp) & ((kp[None, None, :] > qp - W) | (kp[None, None, :] < NS))
+        sc = np.where(keep, sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
+        want = np.einsum("hts,shd->thd", w, Vf)
+        d = np.abs(o[qsl[b]:qsl[b + 1]] - want)
+        say(f"window row {b} (n0={n0}, {n - n0} new): max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (b, d.max(), d.mean())
