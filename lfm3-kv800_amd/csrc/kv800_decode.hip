@@ -550,6 +550,7 @@ struct RowTab {
   int pre[RTAB + 1];   // pre[b0 + i]
   int b0;
   int wsum[4];
+  int t, f, b;         // T, the next span's first flat index and its row
 };
 __device__ __forceinline__ int row_quads(const int32_t* __restrict__ nq, int r, int cap) {
   return (min(max(nq[r], 0), cap) + QWAVES - 1) / QWAVES;
@@ -888,39 +889,59 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     return;
   }
   const int blk = (int)blockIdx.x - X.nexact;
-  if (S.groups == 0) {   // fixed (row, split) grid
-    const int b = blk / ns, s = blk % ns;
-    const int j1 = min(min((s + 1) * spb, nq[b]), (int)min(bstride, (int64_t)INT32_MAX));
-    quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b, s * spb, j1,
-               ((int64_t)b * (ns + 1) + s) * 16);
-    return;
-  }
-  // balanced schedule: flat indices [fw, f1), split at row boundaries
+  // Fixed grid: one span, (row b, split s). Balanced: flat indices [fw, f1) split at row boundaries; the first span
+  // goes through the same quant_span call as the fixed grid's, and any later ones through the loop below, with the
+  // span state kept in LDS in between (with the balanced schedule in its own copy of quant_span and its state live
+  // across it, the compiler scheduled that copy's chunk loop ~6 % slower than the fixed grid's).
   __shared__ RowTab R;
-  int base;
-  const int T = scan_rows(nq, S, R, &base);
-  if (blk == 0) write_rows(nq, S, base);
-  if (T <= 0) return;
-  const int C = sched_chunk(S, T);
-  const int fw = (int)min((int64_t)blk * C, (int64_t)T), f1 = min(fw + C, T);
-  if (fw >= f1) return;
-  int f0 = fw;
-  for (bool more = true; more;) {   // rounds of at most RTAB rows
-    fill_rows(nq, S, R, base, f0);
-    const int b0 = R.b0;
-    int b = b0;
-    more = false;
-    for (;;) {
-      const int pb = R.pre[b - b0], e = min(f1, R.pre[b + 1 - b0]);
-      const int nqb = min(max(nq[b], 0), S.cap);
-      quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b,
-                 QWAVES * (f0 - pb), min(QWAVES * (e - pb), nqb), ((int64_t)b + blk) * 16);
-      f0 = e;
-      if (f0 >= f1) break;
-      __syncthreads();   // the next span's q stores reuse the LDS the merge above read
-      do { ++b; } while (b + 1 - b0 <= RTAB && R.pre[b + 1 - b0] <= f0);
-      if (b + 1 - b0 > RTAB) { more = true; break; }
+  int b, j0, j1;
+  int64_t prow;
+  bool more = false;
+  if (S.groups == 0) {
+    b = blk / ns;
+    const int s = blk % ns;
+    j0 = s * spb;
+    j1 = min(min((s + 1) * spb, nq[b]), (int)min(bstride, (int64_t)INT32_MAX));
+    prow = ((int64_t)b * (ns + 1) + s) * 16;
+  } else {
+    int base;
+    const int T = scan_rows(nq, S, R, &base);
+    if (blk == 0) write_rows(nq, S, base);
+    if (T <= 0) return;
+    const int C = sched_chunk(S, T);
+    const int fw = (int)min((int64_t)blk * C, (int64_t)T), f1 = min(fw + C, T);
+    if (fw >= f1) return;
+    fill_rows(nq, S, R, base, fw);
+    b = R.b0;
+    const int e = min(f1, R.pre[1]);
+    j0 = QWAVES * (fw - R.pre[0]);
+    j1 = min(QWAVES * (e - R.pre[0]), min(max(nq[b], 0), S.cap));
+    prow = ((int64_t)b + blk) * 16;
+    more = e < f1;
+    if (threadIdx.x == 0) { R.t = T; R.f = e; R.b = b; }
+  }
+  quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
+  if (!more) return;
+  for (;;) {   // balanced: the workgroup's later spans
+    __syncthreads();   // the next span's q stores reuse the LDS the merge above read
+    asm volatile("" ::: "memory");
+    const int T = __builtin_amdgcn_readfirstlane(R.t), f0 = __builtin_amdgcn_readfirstlane(R.f);
+    const int C = sched_chunk(S, T), f1 = min((int)min((int64_t)blk * C, (int64_t)T) + C, T);
+    int b0 = __builtin_amdgcn_readfirstlane(R.b0), nb = __builtin_amdgcn_readfirstlane(R.b);
+    do { ++nb; } while (nb + 1 - b0 <= RTAB && R.pre[nb + 1 - b0] <= f0);
+    if (nb + 1 - b0 > RTAB) {   // the next round of at most RTAB rows
+      int base;
+      scan_rows(nq, S, R, &base);
+      fill_rows(nq, S, R, base, f0);
+      b0 = nb = R.b0;
     }
+    const int pb = __builtin_amdgcn_readfirstlane(R.pre[nb - b0]);
+    const int e = min(f1, __builtin_amdgcn_readfirstlane(R.pre[nb + 1 - b0]));
+    quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, nb,
+               QWAVES * (f0 - pb), min(QWAVES * (e - pb), min(max(nq[nb], 0), S.cap)), ((int64_t)nb + blk) * 16);
+    if (e >= f1) return;
+    __syncthreads();
+    if (threadIdx.x == 0) { R.f = e; R.b = nb; }
   }
 }
 
