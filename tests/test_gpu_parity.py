@@ -7,7 +7,7 @@ Bars:
   * decode, the reference's own 12 parity cases (K with a 3-sigma per-channel offset, q x 2): the reference's bar,
     rel < 1e-2 against its independent check (tests/test_parity.py:104), and at least as close to the exact attention
     over the quantized cache as torch_decode itself is. On those inputs torch_decode's two bf16 roundings of K move
-    it ~4e-3 mean-abs from the exact result; the HIP kernels do not round K and land closer."""
+    it ~4e-3 mean-abs from the exact result; the HIP kernels do not round the dequantized K and land closer."""
 import hashlib
 import os
 
