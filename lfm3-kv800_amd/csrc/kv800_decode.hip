@@ -532,77 +532,61 @@ struct ExactArgs {
 };
 
 // Balanced schedule (groups > 0): the B rows' sub-blocks in quads of 4 (one per wave; a row's last quad may be
-// partial), laid end to end: row b's quads at flat indices [pre[b], pre[b + 1]), T = pre[B] in all. Workgroup g takes
-// flat indices [g C, g C + C) with C = ceil(T / groups), one partial per row it touches, in slot b + g (distinct for
-// every (row, workgroup) pair, since both only grow along the flat order). The exact partial of row b is slot
-// B + groups + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact partial
+// partial), q_b quads in row b, T = sum q_b. With C = ceil(T / groups), row b is cut into n_b = ceil(q_b / C) slices of
+// at most C quads, and the slices of all rows are laid end to end: row b's at workgroup indices [pre[b], pre[b + 1]).
+// Workgroup g takes one slice and writes its partial to slot g; sum n_b <= T / C + B <= groups + B, so the grid has
+// groups + B workgroups and the ones past the last slice return at once. The exact partial of row b is slot
+// groups + B + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact partial
 // in slot b (ns + 1) + ns (the reference's partial layout).
 struct Sched {
   int32_t* pre;         // pre[0 .. B]: written by workgroup 0 of the decode grid, read by the merge
   int groups, B, cap;   // cap: sub-blocks per row are clamped to [0, cap]
 };
-__device__ __forceinline__ int sched_chunk(const Sched& S, int T) { return (T + S.groups - 1) / S.groups; }
 
-// The decode grid's workgroups each scan NQ themselves (thread t owns rows [t k, t k + k), k = ceil(B / 256)) and keep
-// the offsets of RTAB + 1 consecutive rows, from the row holding the flat index they work on, in a small LDS table.
-constexpr int RTAB = 64;
+// The decode grid's workgroups each scan NQ themselves: thread t owns rows [t k, t k + k), k = ceil(B / 256), reads
+// their counts once (into registers, up to RREG rows, i.e. B <= 1024; later rows are read again) and takes part in
+// two block-wide scans, of the quads (for T) and of the slices.
+constexpr int RREG = 4;
 struct RowTab {
-  int pre[RTAB + 1];   // pre[b0 + i]
-  int b0;
   int wsum[4];
-  int t, f, b;         // T, the next span's first flat index and its row
+  int b, pb, nsb;       // the row of this workgroup's slice, its first slice index, its clamped sub-block count
 };
-__device__ __forceinline__ int row_quads(const int32_t* __restrict__ nq, int r, int cap) {
-  return (min(max(nq[r], 0), cap) + QWAVES - 1) / QWAVES;
+struct RowCache {       // this thread's rows [r0, r1) and their clamped sub-block counts
+  int r0, r1;
+  int v[RREG];
+};
+__device__ __forceinline__ void load_rows(const int32_t* __restrict__ nq, const Sched& S, RowCache& C) {
+  const int k = (S.B + 255) >> 8;
+  C.r0 = min((int)threadIdx.x * k, S.B);
+  C.r1 = min(C.r0 + k, S.B);
+#pragma unroll
+  for (int i = 0; i < RREG; ++i) C.v[i] = (C.r0 + i < C.r1) ? min(max(nq[C.r0 + i], 0), S.cap) : 0;
 }
-// Returns T; *base = the flat offset of this thread's first row.
-__device__ __forceinline__ int scan_rows(const int32_t* __restrict__ nq, const Sched& S, RowTab& R, int* base) {
+__device__ __forceinline__ int nsb_of(const int32_t* __restrict__ nq, const Sched& S, const RowCache& C, int i) {
+  int x = 0;
+#pragma unroll
+  for (int k = 0; k < RREG; ++k)
+    if (k == i) x = C.v[k];
+  return i < RREG ? x : min(max(nq[C.r0 + i], 0), S.cap);
+}
+__device__ __forceinline__ int quads_of(int nsb) { return (nsb + QWAVES - 1) / QWAVES; }
+__device__ __forceinline__ int slices_of(int quads, int C) { return (quads + C - 1) / C; }
+// Exclusive prefix of v over the workgroup's threads (in thread order); *total = the sum over all threads.
+__device__ __forceinline__ int block_scan(int v, RowTab& R, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
-  int sum = 0;
-  for (int r = r0; r < r1; ++r) sum += row_quads(nq, r, S.cap);
-  int v = sum;
+  int x = v;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o);
-    if (lane >= o) v += t;
+    const int t = __shfl_up(x, o);
+    if (lane >= o) x += t;
   }
-  if (lane == 63) R.wsum[w] = v;
+  __syncthreads();   // earlier readers of R.wsum are done
+  if (lane == 63) R.wsum[w] = x;
   __syncthreads();
   int add = 0;
   for (int ww = 0; ww < w; ++ww) add += R.wsum[ww];
-  *base = add + v - sum;
-  return R.wsum[0] + R.wsum[1] + R.wsum[2] + R.wsum[3];
-}
-// pre[0 .. B] to global memory (workgroup 0; the merge reads it after the grid).
-__device__ __forceinline__ void write_rows(const int32_t* __restrict__ nq, const Sched& S, int base) {
-  const int tid = threadIdx.x, k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
-  int p = base;
-  if (tid == 0) S.pre[0] = 0;
-  for (int r = r0; r < r1; ++r) {
-    p += row_quads(nq, r, S.cap);
-    S.pre[r + 1] = p;
-  }
-}
-// R.b0 = the row holding flat index f (f < T), R.pre[i] = pre[b0 + i] for b0 + i <= B, i <= RTAB.
-__device__ __forceinline__ void fill_rows(const int32_t* __restrict__ nq, const Sched& S, RowTab& R, int base, int f) {
-  const int tid = threadIdx.x, k = (S.B + 255) >> 8, r0 = min(tid * k, S.B), r1 = min(r0 + k, S.B);
-  __syncthreads();   // earlier readers of R are done
-  int p = base;
-  for (int r = r0; r < r1; ++r) {
-    const int qd = row_quads(nq, r, S.cap);
-    if (p <= f && f < p + qd) R.b0 = r;   // exactly one row
-    p += qd;
-  }
-  __syncthreads();
-  const int b0 = R.b0;
-  p = base;
-  for (int r = r0; r < r1; ++r) {
-    if (r >= b0 && r - b0 <= RTAB) R.pre[r - b0] = p;
-    p += row_quads(nq, r, S.cap);
-  }
-  if (tid == 255 && S.B - b0 <= RTAB) R.pre[S.B - b0] = p;   // thread 255 ends at T = pre[B]
-  __syncthreads();
+  *total = R.wsum[0] + R.wsum[1] + R.wsum[2] + R.wsum[3];
+  return add + x - v;
 }
 static_assert(sizeof(XLds) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
 
@@ -895,14 +879,9 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     return;
   }
   const int blk = (int)blockIdx.x - X.nexact;
-  // Fixed grid: one span, (row b, split s). Balanced: flat indices [fw, f1) split at row boundaries; the first span
-  // goes through the same quant_span call as the fixed grid's, and any later ones through the loop below, with the
-  // span state kept in LDS in between (with the balanced schedule in its own copy of quant_span and its state live
-  // across it, the compiler scheduled that copy's chunk loop ~6 % slower than the fixed grid's).
-  __shared__ RowTab R;
+  // fixed grid: (row b, split s); balanced: slice blk (one row's quads [c0, c1))
   int b, j0, j1;
   int64_t prow;
-  bool more = false;
   if (S.groups == 0) {
     b = blk / ns;
     const int s = blk % ns;
@@ -910,45 +889,45 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     j1 = min(min((s + 1) * spb, nq[b]), (int)min(bstride, (int64_t)INT32_MAX));
     prow = ((int64_t)b * (ns + 1) + s) * 16;
   } else {
-    int base;
-    const int T = scan_rows(nq, S, R, &base);
-    if (blk == 0) write_rows(nq, S, base);
-    if (T <= 0) return;
-    const int C = sched_chunk(S, T);
-    const int fw = (int)min((int64_t)blk * C, (int64_t)T), f1 = min(fw + C, T);
-    if (fw >= f1) return;
-    fill_rows(nq, S, R, base, fw);
-    b = R.b0;
-    const int e = min(f1, R.pre[1]);
-    j0 = QWAVES * (fw - R.pre[0]);
-    j1 = min(QWAVES * (e - R.pre[0]), min(max(nq[b], 0), S.cap));
-    prow = ((int64_t)b + blk) * 16;
-    more = e < f1;
-    if (threadIdx.x == 0) { R.t = T; R.f = e; R.b = b; }
+    __shared__ RowTab R;
+    RowCache RC;
+    load_rows(nq, S, RC);
+    int qsum = 0;
+    for (int i = 0; i < RC.r1 - RC.r0; ++i) qsum += quads_of(nsb_of(nq, S, RC, i));
+    int T;
+    block_scan(qsum, R, &T);
+    if (T <= 0) {   // no quantized work in any row
+      if (blk == 0)
+        for (int r = threadIdx.x; r <= S.B; r += 256) S.pre[r] = 0;
+      return;
+    }
+    const int C = (T + S.groups - 1) / S.groups;
+    int nsl = 0;
+    for (int i = 0; i < RC.r1 - RC.r0; ++i) nsl += slices_of(quads_of(nsb_of(nq, S, RC, i)), C);
+    int G2;
+    int p = block_scan(nsl, R, &G2);
+    if (blk == 0) {   // pre[0 .. B] for the merge
+      if (threadIdx.x == 0) S.pre[0] = 0;
+      int pp = p;
+      for (int i = 0; i < RC.r1 - RC.r0; ++i) {
+        pp += slices_of(quads_of(nsb_of(nq, S, RC, i)), C);
+        S.pre[RC.r0 + i + 1] = pp;
+      }
+    }
+    if (blk >= G2) return;   // past the last slice (uniform over the workgroup)
+    for (int i = 0; i < RC.r1 - RC.r0; ++i) {   // exactly one thread owns the row of slice blk
+      const int nb = nsb_of(nq, S, RC, i), n = slices_of(quads_of(nb), C);
+      if (p <= blk && blk < p + n) { R.b = RC.r0 + i; R.pb = p; R.nsb = nb; }
+      p += n;
+    }
+    __syncthreads();
+    b = __builtin_amdgcn_readfirstlane(R.b);
+    const int k = blk - __builtin_amdgcn_readfirstlane(R.pb), nb = __builtin_amdgcn_readfirstlane(R.nsb);
+    j0 = QWAVES * C * k;
+    j1 = min(QWAVES * C * (k + 1), nb);
+    prow = (int64_t)blk * 16;
   }
   quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
-  if (!more) return;
-  for (;;) {   // balanced: the workgroup's later spans
-    __syncthreads();   // the next span's q stores reuse the LDS the merge above read
-    asm volatile("" ::: "memory");
-    const int T = __builtin_amdgcn_readfirstlane(R.t), f0 = __builtin_amdgcn_readfirstlane(R.f);
-    const int C = sched_chunk(S, T), f1 = min((int)min((int64_t)blk * C, (int64_t)T) + C, T);
-    int b0 = __builtin_amdgcn_readfirstlane(R.b0), nb = __builtin_amdgcn_readfirstlane(R.b);
-    do { ++nb; } while (nb + 1 - b0 <= RTAB && R.pre[nb + 1 - b0] <= f0);
-    if (nb + 1 - b0 > RTAB) {   // the next round of at most RTAB rows
-      int base;
-      scan_rows(nq, S, R, &base);
-      fill_rows(nq, S, R, base, f0);
-      b0 = nb = R.b0;
-    }
-    const int pb = __builtin_amdgcn_readfirstlane(R.pre[nb - b0]);
-    const int e = min(f1, __builtin_amdgcn_readfirstlane(R.pre[nb + 1 - b0]));
-    quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, nb,
-               QWAVES * (f0 - pb), min(QWAVES * (e - pb), min(max(nq[nb], 0), S.cap)), ((int64_t)nb + blk) * 16);
-    if (e >= f1) return;
-    __syncthreads();
-    if (threadIdx.x == 0) { R.f = e; R.b = nb; }
-  }
 }
 
 
@@ -959,16 +938,10 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
   const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
   // row b's quantized partials: slots first .. first + ns - 1; its exact partial: slot xs
   int64_t first = (int64_t)b * (ns + 1), xs = first + ns;
-  if (S.groups > 0) {
-    const int p0 = S.pre[b], p1 = S.pre[b + 1];
-    first = 0;
-    ns = 0;
-    if (p1 > p0) {
-      const int C = sched_chunk(S, S.pre[S.B]);
-      first = (int64_t)b + p0 / C;
-      ns = (p1 - 1) / C - p0 / C + 1;
-    }
-    xs = (int64_t)S.B + S.groups + b;
+  if (S.groups > 0) {   // row b's slices are workgroups [pre[b], pre[b + 1]), one partial each
+    first = S.pre[b];
+    ns = S.pre[b + 1] - S.pre[b];
+    xs = (int64_t)S.groups + S.B + b;
   }
   const int64_t r0 = first * 16 + r;   // row of the first quantized partial; the next adds 16
   float M = mo[xs * 16 + r];
@@ -1091,7 +1064,7 @@ int launch_quant(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, c
   KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
   if (B == 0 || ns == 0) return KV800_OK;
   KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
-  const int64_t nwork = S.groups ? S.groups : B * ns;
+  const int64_t nwork = S.groups ? S.groups + B : B * ns;
   KV800_REQUIRE(nwork + B * 4 <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
   KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
                 "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
