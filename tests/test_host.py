@@ -72,3 +72,15 @@ def test_plan_rules():
     assert kh.plan(64, 127, spb=16) == (8, 16)
     ns, spb = kh.plan(64, 127, target=1024)            # the reference's rule: spb = ceil(nqmax * B * 4 / target)
     assert spb == 32 and ns == 4
+
+
+def test_prefill_window_rows_on_host(oracle):
+    """The window-layer extend rows (vllm_cache.prefill_window_rows) are host-side gathers + torch attention; the GPU
+    test's cases run here on CPU tensors against the same float64 restatement."""
+    import test_gpu_prefill as tp
+    old = tp.DEV
+    tp.DEV = "cpu"
+    try:
+        tp.test_prefill_window_rows(None, oracle)
+    finally:
+        tp.DEV = old
