@@ -944,14 +944,14 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     xs = (int64_t)S.groups + S.B + b;
   }
   const int64_t r0 = first * 16 + r;   // row of the first quantized partial; the next adds 16
-  float M = mo[xs * 16 + r];
-  for (int s0 = 0; s0 < ns; s0 += 4) {   // 4 partials at a time, loads issued together
-    float mv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) mv[k] = (s0 + k < ns) ? mo[r0 + 16 * (s0 + k)] : NEG_BIG;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) M = fmaxf(M, mv[k]);
-  }
+  // one pass with a running max: each batch of 4 partials (m, l, acc) is requested together, the exact partial with
+  // the first batch, so the row waits on one memory round trip per batch
+  const int64_t xrow = xs * 16 + r;
+  float M = mo[xrow];
+  const float xl = lo[xrow];
+  const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
+  const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
+  const float Mx = M;
   float Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, xe[8];
   for (int s0 = 0; s0 < ns; s0 += 4) {   // quantized splits
     float mv[4], lv[4];
@@ -965,6 +965,12 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
       a0[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
       a1[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
     }
+    const float Mn = fmaxf(fmaxf(M, fmaxf(mv[0], mv[1])), fmaxf(mv[2], mv[3]));
+    const float al = exp2f(M - Mn);   // rescales what the earlier batches added
+    M = Mn;
+    Ls *= al;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xq[e] *= al;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const float wgt = exp2f(mv[k] - M);   // 0 for the padding entries
@@ -975,12 +981,9 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     }
   }
   {   // exact partial
-    const int64_t row = xs * 16 + r;
-    const float wgt = exp2f(mo[row] - M);
-    Ls += wgt * lo[row];
-    const float4 a0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
-    const float4 a1 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
-    const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float wgt = exp2f(Mx - M);
+    Ls += wgt * xl;
+    const float a[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
   }
