@@ -295,6 +295,24 @@ def test_decode_many_rows_few_groups(hip, oracle):
         close(bits_of(out), want, f"150 rows groups={groups}")
 
 
+def test_decode_batch_over_1024_rows(hip, oracle):
+    """Balanced schedule with more than 1024 rows: each scan thread owns 5 rows, more than it keeps in registers, so
+    the later rows' counts are read again; rows with no quantized sub-block among them."""
+    rng = np.random.RandomState(71)
+    lens = [int(x) for x in rng.randint(1, 520, size=1100)]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (len(lens), 16, 128))
+    cos, sin = oracle.rope_tables(1000)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, ebs=64, shuffle_seed=71)
+    say("decode 1100 rows, sub-blocks", int(case.NQ.sum()))
+    P = upload(case)
+    want = oracle.decode(case, q, cos, sin)
+    for groups in (None, 5):
+        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), groups=groups)
+        close(bits_of(out), want, f"1100 rows groups={groups}")
+
+
 def test_decode_stages_and_merge(hip, oracle):
     rng = np.random.RandomState(31)
     lens = [900, 3000, 1500]
