@@ -272,7 +272,7 @@ def main():
     g = torch.Generator(device=dev).manual_seed(7)
     q = torch.randn(B, 16, 128, generator=g, device=dev).to(torch.bfloat16)
     cos, sin = rope_tables(torch, N_CTX, dev)
-    kh.rope_table16(cos, sin)                                          # model-constant table, built once
+    kh.rope_pairs(cos, sin)                                          # model-constant table, built once
     torch.cuda.synchronize()
     log(f"built 2 cache copies in {time.perf_counter() - t_build:.1f} s")
 
@@ -294,14 +294,14 @@ def main():
     MO = torch.empty(B, ns + 1, 16, dtype=torch.float32, device=dev)
     LO = torch.empty_like(MO)
     AO = torch.empty(B, ns + 1, 16, 128, dtype=torch.float32, device=dev)
-    cs16 = kh.rope_table16(cos, sin)
+    cs2 = kh.rope_pairs(cos, sin)
     scale = 128 ** -0.5 * 1.4426950408889634
     structs = [kh.paged_struct(P, B) for P in layers]
 
     def quant(i):
         P, (st, qbytes, _, _) = layers[i & 1], structs[i & 1]
         rc = L.kv800_hip_decode_quant_sized(ctypes.c_void_p(q.data_ptr()), st.qpool, qbytes, st.boff, st.boff_stride,
-                                            ctypes.c_void_p(P.NQ.data_ptr()), ctypes.c_void_p(cs16.data_ptr()),
+                                            ctypes.c_void_p(P.NQ.data_ptr()), ctypes.c_void_p(cs2.data_ptr()),
                                             cos.shape[0], ctypes.c_void_p(MO.data_ptr()), ctypes.c_void_p(LO.data_ptr()),
                                             ctypes.c_void_p(AO.data_ptr()), B, ns, spb, scale,
                                             ctypes.c_void_p(s.cuda_stream))

@@ -81,17 +81,19 @@ int kv800_hip_flush_latency(const uint16_t* epool, const int64_t* eoff, int64_t 
  * k_out: (M, 256, 4, 128) bf16 = bf16(code * ksc + klo); v_out: (M, 256, 4, 128) f32 = (bit * vsc + vlo) @ H. */
 int kv800_hip_dequantize_blocks(const uint8_t* sb, int64_t M, uint16_t* k_out, float* v_out, void* stream);
 
-/* fp16 (cos, sin) pair table used by the quantized-decode kernel: cs16[p * 32 + j] = fp16(cos[p, j]) |
- * fp16(sin[p, j]) << 16 for p < P. cos_t, sin_t: (>= P, 32) bf16. No reference counterpart (it reads the bf16
- * tables per token, kv800.py:146-147); the conversion is exact for every value the tables can hold above 2^-17. */
-int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs16, void* stream);
+/* bf16 (cos, sin) pair table used by the quantized-decode kernel: cs2[p * 32 + j] = cos[p, j] | sin[p, j] << 16 (bf16
+ * bits) for p < P. cos_t, sin_t: (>= P, 32) bf16. No reference counterpart (it reads the two bf16 tables per token,
+ * kv800.py:146-147); the interleave lets one 16-byte load give a lane both values of 4 channels. */
+int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs2, void* stream);
 
 /* Split-K partial attention over the flushed sub-blocks. Replaces torch.ops.kv800.qdecode (kv800_sycl.sycl:510-526,
  * Triton _qdec kv800.py:120-170). For each row b and split s < ns: sub-blocks [s spb, min((s+1) spb, nq[b])) ->
  * mo, lo (B, ns+1, 16) and ao (B, ns+1, 16, 128) at slot s, V in the Hadamard domain (acc + sum p vlo).
- * q: (B, 16, 128) bf16 post-RoPE; cs16: kv800_hip_rope_table of rows >= max(nq) * 256; scale = log2(e)/sqrt(128). */
+ * q: (B, 16, 128) bf16 post-RoPE; cs2: kv800_hip_rope_table of rows >= max(nq) * 256 (the reference op takes the two
+ * bf16 tables instead); scale = log2(e)/sqrt(128). Keys as torch_decode forms them: bf16(code * ksc + klo), rotated in
+ * fp32 and rounded to bf16 (torch_decode.py:16-24). */
 int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
-                           const int32_t* nq, const uint32_t* cs16, float* mo, float* lo, float* ao, int64_t B,
+                           const int32_t* nq, const uint32_t* cs2, float* mo, float* lo, float* ao, int64_t B,
                            int64_t ns, int64_t spb, float scale, void* stream);
 
 /* Sinks + exact tail. Replaces torch.ops.kv800.xdecode (kv800_sycl.sycl:528-542, Triton _xdec kv800.py:197-228):
@@ -110,7 +112,7 @@ int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, in
  * (kv800.py:366-367 plans for the reference kernels). */
 int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb);
 
-/* Workspace bytes kv800_hip_decode needs for B rows, ns splits (spb > 0) and rope rows (0 if cs16 is passed in). */
+/* Workspace bytes kv800_hip_decode needs for B rows, ns splits (spb > 0) and rope rows (0 if cs2 is passed in). */
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows);
 
 /* Balanced schedule of kv800_hip_decode (spb <= 0): the batch's sub-blocks laid end to end and cut into `groups`
@@ -122,11 +124,11 @@ int64_t kv800_hip_decode_workspace_balanced(int64_t B, int64_t groups, int64_t r
 
 /* Fused decode of one layer. Replaces kv800.decode's backend body (kv800.py:352-383): [rope table], the quantized
  * work and the exact tail in one grid, then the merge, all on `stream` (window layers: one launch, the exact tail
- * fused with the merge). cs16 may be NULL (then it is built in the workspace from cos_t / sin_t for the nqmax * 256
+ * fused with the merge). cs2 may be NULL (then it is built in the workspace from cos_t / sin_t for the nqmax * 256
  * rows the quantized kernel reads). spb > 0: fixed grid of ceil(nqmax / spb) splits per row; spb == 0: balanced
  * schedule with kv800_hip_plan_balanced's groups; spb < 0: balanced schedule with -spb groups. */
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
-                     const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
+                     const uint16_t* sin_t, const uint32_t* cs2, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream);
 
 /* Training fake quantization, the forward value of train.py's straight-through 800h K / V (train.py:82-100), on the
@@ -179,18 +181,18 @@ int kv800_hip_page_offsets(const int32_t* bt, int64_t bt_stride, int64_t R, int6
 
 /* Bounds-checked forms used by the Python layer. They take the extent of every pool the kernels read, measured from
  * the pointer passed in: qpool_bytes (bytes), epool_elems / sink_elems (bf16 elements), rope_rows (rows of cos_t /
- * sin_t and of cs16). A sub-block, page or row whose offset falls outside its pool is skipped instead of read, so a
+ * sin_t and of cs2). A sub-block, page or row whose offset falls outside its pool is skipped instead of read, so a
  * malformed table yields a wrong (finite) result rather than a memory fault. The unsized forms above pass
  * INT64_MAX / 2 for every extent. No reference counterpart: the reference's kernels read unchecked. */
 int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
-                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows,
+                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs2, int64_t rope_rows,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
                                  void* stream);
 int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t,
                                  const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream);
 int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
-                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs16, int64_t qpool_bytes,
+                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs2, int64_t qpool_bytes,
                            int64_t epool_elems, int64_t sink_elems, uint16_t* out, void* workspace,
                            int64_t workspace_bytes, int64_t spb, void* stream);
 

@@ -7,26 +7,17 @@
 // log-sum-exp, with the 128-point Hadamard applied once to the merged quantized part.
 //
 // Kernels
-//   rope_table_kernel   bf16 (cos, sin) tables -> packed fp16 pairs (exact for every table value above 2^-17).
-//   decode_quant_kernel one workgroup (4 waves) per (row b, split s); each wave owns whole 256-token sub-blocks,
-//                       32 tokens (one chunk) at a time, the next chunk's bytes prefetched into registers.
-//     QK on MFMA f32_16x16x32_f16, N = the 16 query rows. With the 2-bit codes c as exact fp16 features (one
-//       e2m1 -> fp16 conversion per byte) and per-channel k = klo + ksc c, RoPE is moved onto exact fp16 features:
-//         rope dims: (cos c0, sin c0, cos c2, sin c2) x weights (q0 S0, q2 S0, q2 S2, -q0 S2), S = ksc scale
-//         nope dims: (c1, c3)                         x weights (q1 S1, q3 S3)
-//         klo part : (cos, sin) of the position        x weights (q0 T0 + q2 T2, q2 T0 - q0 T2), T = klo
-//       and the per-row constant sum(q1 T1 + q3 T3) initialises the accumulator.
-//       Rope / nope MFMAs take M = 16 (token, head) rows -- 4 tokens x the 4 KV heads -- so every weight register is
-//       dense (query row n applies head n / 4's scales) and only the output rows of head n / 4 are kept; the klo part
-//       takes M = 16 tokens (head-independent features, weights from head n / 4). Weights are rebuilt per sub-block.
-//     PV on the same MFMA: M = 16 dims (one bit plane), N = the 16 rows, K = 32 tokens. The bit feature is the
-//       fp16 subnormal bit 2^(i - 24) (one AND per two tokens; MFMA keeps fp16 subnormal inputs exactly), the
-//       weights fp16(p vsc) masked to the head's rows; plane i is scaled back by 2^(24 - i) at the end.
-//     Softmax with a lazy running max (rescale only when a tile max exceeds it by more than 8 log2 units).
+//   rope_table_kernel   bf16 (cos, sin) tables -> packed bf16 (cos, sin) pairs, one dword per (position, channel).
+//   decode_quant_kernel one workgroup (4 waves) per span of one row's sub-blocks (a (row, split) of the fixed grid or
+//                       a slice of the balanced schedule); the 4 waves share each sub-block, 64 tokens each, as
+//                       32-token chunks whose bytes are prefetched one chunk ahead. Keys are formed exactly as
+//                       torch_decode forms them (bf16 dequantized K from per-sub-block LDS code tables, RoPE in fp32
+//                       rounded to bf16 again), QK on bf16 MFMA with exact products, PV on fp16 MFMA over the 1-bit
+//                       Hadamard-domain planes (details at quant_span).
 //   decode_exact_kernel one workgroup per row b, one wave per KV head (the exact-tail workgroups of the quantized
 //                       grid: one per (row, KV head), its 4 waves taking turns over the chunks): sinks + exact
-//                       positions in 32-token chunks (loads one chunk ahead), QK on v_dot2 bf16 pairs, PV fp32; the
-//                       fused variant also merges the quantized splits of its rows.
+//                       positions in 32-token chunks (loads one chunk ahead), QK and PV on bf16 MFMA; the fused
+//                       variant also merges the quantized splits of its rows.
 //   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT (staged path).
 #include <math.h>
 
@@ -40,6 +31,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
 
 constexpr float NEG_BIG = -1e30f;
 constexpr float LAZY = 8.f;   // log2 units a tile max may exceed the running max before the state is rescaled
@@ -88,10 +80,10 @@ __device__ __forceinline__ void f8x4(uint32_t w, float* o) {
 
 // ---------------------------------------------------------------- rope table
 __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int64_t n,
-                                  uint32_t* __restrict__ cs16) {
+                                  uint32_t* __restrict__ cs2) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  cs16[i] = pk2(bf2f(cos_t[i]), bf2f(sin_t[i]));
+  cs2[i] = (uint32_t)cos_t[i] | ((uint32_t)sin_t[i] << 16);
 }
 
 // ---------------------------------------------------------------- exact tail + sinks
@@ -459,377 +451,317 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 }
 
 // ---------------------------------------------------------------- quantized sub-blocks
+// A workgroup of 4 waves takes one row's sub-blocks [j0, j1) in order; the 4 waves share each sub-block, wave w taking
+// its tokens 64 w .. 64 w + 63 as two 32-token chunks. Per chunk, lane (g, n) = (lane / 16, lane % 16):
+// - K as torch_decode sees it (torch_decode.py:16-24, 54; kv800.py:79-86): every element of the dequantized K is
+//   bf16(code * ksc + klo), 4 values per (head, dim) and sub-block, and the RoPE pairs (j, j + 64), j < 32, are rotated
+//   in fp32 and rounded to bf16 again. Per sub-block the workgroup writes one 16-entry table per (head, channel j, kind)
+//   into LDS: kind rope holds (bf16 K of dim j for code c0, of dim j + 64 for code c2) at entry (c0, c2); kind nope
+//   (dims j + 32, j + 96) at (c1, c3). A kc byte c0 | c1 << 2 | c2 << 4 | c3 << 6 thus gives both pairs of its channel
+//   with two lookups (one v_perm each to form the LDS address); a rope pair (k0, k2) is rotated by two v_dot2_f32_bf16
+//   against the position's (cos, sin) and rounded by v_cvt_pk_bf16_f32, so the MFMA operands are exactly torch_decode's
+//   rotated bf16 keys.
+// - QK on MFMA f32_16x16x32_bf16: A = 16 tokens (row n = token n of the tile) x 32 K-elements of one KV head h
+//   (lane group g: channels 8 g .. 8 g + 7, their rope pairs (dim j, dim j + 64) in two k-steps and nope pairs
+//   (j + 32, j + 96) in two more), B = q (column n = query row n, the same K order), so products are exact and sums
+//   fp32. Column n is meaningful for head h = n / 4 only; lane (g, n) keeps head n / 4's scores of tokens 4 g .. 4 g + 3.
+// - softmax: fp32, log2 units, lazy running max (rescale only when a chunk max exceeds it by more than QLAZY).
+// - PV on MFMA f32_16x16x32_f16 in the Hadamard domain (kv800.py:157-168): A = 16 dims of one bit plane x the lane
+//   group's 8 tokens, read by one ds_read_b64_tr_b8 per head from the wave's LDS copy of the chunk's vb bytes; a bit
+//   becomes the fp16 subnormal 2^(i - 24) by one AND per two tokens; B = the weights fp16(p vsc) in head h's columns.
+//   Plane i is scaled back by 2^(24 - i) at the end; sum p vlo is kept per row.
+// The table lookups of one instruction touch 4 tables (one per lane group) whose entries sit in disjoint LDS banks.
 constexpr int QWAVES = 4;
+constexpr float QLAZY = 7.f;   // p <= 2^7 and vsc <= 448 keep the fp16 weights p vsc below 65,504
 constexpr int64_t BAL_CHUNK = 16, BAL_GROUPS = 1536;   // balanced schedule: sub-blocks per workgroup, most workgroups
-// LDS row strides are padded (132 floats, 272 floats, 9 x 16 bytes) so that the 16 lanes of a lane group, which read
-// 16 different rows at the same column, fall into distinct banks; the vb chunk is XOR-swizzled instead (below).
-constexpr int QROW = 132, HROW = 132, VROW = 272, CSP = 9;
+constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
+constexpr int QROW = 132;
 struct QWaveLds {
-  float vs[2][VROW];          // decoded vsc per (head group, token)
-  float vl[2][VROW];          // decoded vlo
-  u4v vb[2][32 * 4];          // vb bytes of a 32-token chunk (double buffer), 16-byte pieces placed by vb_at
-  u4v cs[2][32 * CSP];         // fp16 (cos, sin) rows of the chunk's 32 positions (double buffer), placed by cs_at
+  u4v vb[4 * 32];              // the chunk's vb bytes: the 16-byte row of (head h, slot) at vb[32 h + slot]
+  float vs[2][64], vl[2][64];  // decoded vsc / vlo of the wave's 64 tokens, per head group
 };
 struct QLds {
-  float q[16][QROW];
+  uint32_t lut[2][LUT_WORDS];  // code tables of the current and the next sub-block
   QWaveLds wv[QWAVES];
 };
-// Per-sub-block scale staging, scale * ksc and klo as [head][channel] floats, lives in the wave's second
-// rope buffer: it is read only while the weights are built, before chunk 1 (the first user of that buffer) is stored,
-// and a wave's LDS instructions execute in order. This keeps a workgroup under 80 KB (two per CU).
-constexpr int SCALE_FLOATS = 8 * HROW;
-static_assert(SCALE_FLOATS * 4 <= (int)sizeof(u4v) * 32 * CSP, "scale staging must fit one rope buffer");
-struct QFinLds {              // end-of-split merge of the 4 waves (reuses the LDS)
+struct QFinLds {               // end-of-span merge of the 4 waves (reuses the LDS)
   float m[QWAVES][16], l[QWAVES][16], lv[QWAVES][16];
   float acc[QWAVES][16][QROW];
 };
-// 16-byte slot of (token t of the chunk, piece k = head) in a vb chunk buffer: piece k of token t is stored at slot
-// k ^ ((t >> 2) & 3) of the token's 4, so the four lane groups (tokens 4 g + ...) read four different banks
-__device__ __forceinline__ int vb_at(int t, int k) { return 4 * t + (k ^ ((t >> 2) & 3)); }
-// 16-byte slot of piece p (dwords 4 p .. 4 p + 3) of rope row r in a chunk buffer: rows are padded to 9 slots and the
-// pieces of rows with (r / 4) odd are swapped in pairs, so the 16 (row, piece) pairs a rope / nope read touches
-// (4 tokens x 4 lane groups) cover all 16 bank quads
-__device__ __forceinline__ int cs_at(int r, int p) { return r * CSP + (p ^ ((r >> 2) & 1)); }
-
-// rope + nope features of one kc dword x (channels e = 0..3 of the lane's 8, one byte each holding the codes
-// c0 | c1 << 2 | c2 << 4 | c3 << 6 of dims j, j + 32, j + 64, j + 96; cos / sin of channel e in cs4) against weight
-// blocks w0 (channels 0, 1), w1 (channels 2, 3) and wn (nope, channels 0..3). A byte masked to bits 0-1 | 4-5 is two
-// e2m1 nibbles whose values are c0 / 2 and c2 / 2; v_cvt_scalef32_pk_f16_fp4 with scale 2 turns it into the exact
-// fp16 pair (c0, c2) in one instruction (its scale applies the exponent only), and bits 2-3 | 6-7 shifted down give
-// (c1, c3) the same way.
-template <int E>
-__device__ __forceinline__ h2 codes2(uint32_t m) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 2.0f, E); }
-
-__device__ __forceinline__ f4 rope_nope(uint32_t x, u4v cs4, h8 w0, h8 w1, h8 wn, f4 a) {
-  const uint32_t m02 = x & 0x33333333u, m13 = (x >> 2) & 0x33333333u;
-  const h2 F[4] = {codes2<0>(m02), codes2<1>(m02), codes2<2>(m02), codes2<3>(m02)};   // (c0, c2) of channel e
-  const uint32_t f13[4] = {hbits(codes2<0>(m13)), hbits(codes2<1>(m13)), hbits(codes2<2>(m13)),
-                           hbits(codes2<3>(m13))};                                  // (c1, c3) of channel e
-  const uint32_t csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-  uint32_t ga[4], gb[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const h2 CS = as_h2(csv[e]);
-    ga[e] = hbits(CS * h2{F[e].x, F[e].x});   // (cos c0, sin c0)
-    gb[e] = hbits(CS * h2{F[e].y, F[e].y});   // (cos c2, sin c2)
-  }
-  a = mfma16(pack8(ga[0], gb[0], ga[1], gb[1]), w0, a);
-  a = mfma16(pack8(ga[2], gb[2], ga[3], gb[3]), w1, a);
-  return mfma16(pack8(f13[0], f13[1], f13[2], f13[3]), wn, a);
-}
 static_assert(sizeof(QFinLds) <= sizeof(QLds), "fin scratch must fit");
 
-// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one row's
-// KV head(s) (its exact partial slot, as decode_exact_kernel<false>) before the split workgroups, so their memory
-// latency overlaps the splits' VALU work on the same CUs instead of following it.
-struct ExactArgs {
-  kv800_paged_t P;
-  const uint16_t* cos_t;
-  const uint16_t* sin_t;
-  int64_t rope_rows, epool_elems, sink_elems;
-  int64_t xs0, xst;   // exact partial of row b in slot xs0 + b xst
-  int nexact, nsink;
-};
+// Slot of chunk token t in the staged vb rows: slot 8 g + k holds token 4 g + k (k < 4) or 16 + 4 g + k - 4, the 8
+// tokens of lane group g in the K order of the PV MFMA (the tokens whose scores the group's lanes hold).
+__device__ __forceinline__ int vb_slot(int t) { return 8 * ((t >> 2) & 3) + 4 * (t >> 4) + (t & 3); }
 
-// Balanced schedule (groups > 0): the B rows' sub-blocks in quads of 4 (one per wave; a row's last quad may be
-// partial), q_b quads in row b, T = sum q_b. With C = ceil(T / groups), row b is cut into n_b = ceil(q_b / C) slices of
-// at most C quads, and the slices of all rows are laid end to end: row b's at workgroup indices [pre[b], pre[b + 1]).
-// Workgroup g takes one slice and writes its partial to slot g; sum n_b <= T / C + B <= groups + B, so the grid has
-// groups + B workgroups and the ones past the last slice return at once. The exact partial of row b is slot
-// groups + B + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact partial
-// in slot b (ns + 1) + ns (the reference's partial layout).
-struct Sched {
-  int32_t* pre;         // pre[0 .. B]: written by workgroup 0 of the decode grid, read by the merge
-  int groups, B, cap;   // cap: sub-blocks per row are clamped to [0, cap]
-};
+// RoPE of four channels' dequantized key pairs k[e] = (k0, k2) (bf16 lo / hi) against cs[e] = (cos, sin) and
+// sw[e] = (sin, cos): r[e] = (bf16(k0 cos - k2 sin), bf16(k2 cos + k0 sin)), torch_decode.py:22-24. Each sum comes from
+// one v_dot2_f32_bf16 (exact bf16 products; the hardware sum is within one fp32 ulp of the rounded exact sum, which
+// changes the bf16 rounding that follows only for values within that ulp of a bf16 rounding boundary) and the pair is
+// rounded by v_cvt_pk_bf16_f32 (RNE). The compiler does not see inside the block, so the block keeps the hazards of the
+// dot instructions itself: every v_cvt reads dot results written at least three instructions earlier, and the
+// leading / trailing s_nop cover a VALU write of an input just before and an MFMA read of an output just after.
+__device__ __forceinline__ void rope4(const uint32_t (&k)[4], const uint32_t (&cs)[4], const uint32_t (&sw)[4],
+                                      uint32_t (&r)[4]) {
+  uint32_t t0, t1, t2, t3;
+  asm("s_nop 1\n"
+      "v_dot2_f32_bf16 %0, %8, %12, 0 neg_hi:[0,1,0]\n"
+      "v_dot2_f32_bf16 %4, %8, %16, 0\n"
+      "v_dot2_f32_bf16 %1, %9, %13, 0 neg_hi:[0,1,0]\n"
+      "v_dot2_f32_bf16 %5, %9, %17, 0\n"
+      "v_dot2_f32_bf16 %2, %10, %14, 0 neg_hi:[0,1,0]\n"
+      "v_dot2_f32_bf16 %6, %10, %18, 0\n"
+      "v_dot2_f32_bf16 %3, %11, %15, 0 neg_hi:[0,1,0]\n"
+      "v_dot2_f32_bf16 %7, %11, %19, 0\n"
+      "v_cvt_pk_bf16_f32 %0, %0, %4\n"
+      "v_cvt_pk_bf16_f32 %1, %1, %5\n"
+      "v_cvt_pk_bf16_f32 %2, %2, %6\n"
+      "v_cvt_pk_bf16_f32 %3, %3, %7\n"
+      "s_nop 1"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(cs[0]), "v"(cs[1]), "v"(cs[2]), "v"(cs[3]), "v"(sw[0]),
+        "v"(sw[1]), "v"(sw[2]), "v"(sw[3]));
+}
+__device__ __forceinline__ b8 pack8b(const uint32_t (&x)[4]) { return as_b8(u4v{x[0], x[1], x[2], x[3]}); }
 
-// The decode grid's workgroups each scan NQ themselves: thread t owns rows [t k, t k + k), k = ceil(B / 256), reads
-// their counts once (into registers, up to RREG rows, i.e. B <= 1024; later rows are read again) and takes part in
-// two block-wide scans, of the quads (for T) and of the slices.
-constexpr int RREG = 4;
-struct RowTab {
-  int wsum[4];
-  int b, pb, nsb;       // the row of this workgroup's slice, its first slice index, its clamped sub-block count
-};
-struct RowCache {       // this thread's rows [r0, r1) and their clamped sub-block counts
-  int r0, r1;
-  int v[RREG];
-};
-__device__ __forceinline__ void load_rows(const int32_t* __restrict__ nq, const Sched& S, RowCache& C) {
-  const int k = (S.B + 255) >> 8;
-  C.r0 = min((int)threadIdx.x * k, S.B);
-  C.r1 = min(C.r0 + k, S.B);
-#pragma unroll
-  for (int i = 0; i < RREG; ++i) C.v[i] = (C.r0 + i < C.r1) ? min(max(nq[C.r0 + i], 0), S.cap) : 0;
+// The K scale bytes table t needs: klo / ksc of its two dims (kind 0: dims j, j + 64; kind 1: j + 32, j + 96), head h.
+__device__ __forceinline__ uint32_t table_bytes(const uint8_t* __restrict__ sb, int t) {
+  const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31;
+  const uint8_t* p = sb + KLO_O + 128 * h + 32 * kind + j;
+  return (uint32_t)p[0] | ((uint32_t)p[64] << 8) | ((uint32_t)p[KSC_O - KLO_O] << 16) |
+         ((uint32_t)p[KSC_O - KLO_O + 64] << 24);
 }
-__device__ __forceinline__ int nsb_of(const int32_t* __restrict__ nq, const Sched& S, const RowCache& C, int i) {
-  int x = 0;
+// Table t of one LUT buffer: entry (ca, cb) = bf16(ca ksc_a + klo_a) | bf16(cb ksc_b + klo_b) << 16 (kv800.py:84-86:
+// the product is exact in fp32, so the fused multiply-add rounds where torch's add does). Block ((kind 4 + h) 2 + d)
+// 4 + g holds the tables of channels 8 g + 4 d + e, e < 4; table e's entry (ca, cb) at dword ca + 16 cb + 4 ((e + g) % 4),
+// so the four lane groups' tables of one lookup occupy disjoint banks.
+__device__ __forceinline__ void lut_build(uint32_t* lut, int t, uint32_t bytes) {
+  float v[4];
+  f8x4(bytes, v);   // klo_a, klo_b, ksc_a, ksc_b
+  const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31, g = j >> 3, d = (j >> 2) & 1, e = j & 3;
+  uint32_t pa[4];
 #pragma unroll
-  for (int k = 0; k < RREG; ++k)
-    if (k == i) x = C.v[k];
-  return i < RREG ? x : min(max(nq[C.r0 + i], 0), S.cap);
-}
-__device__ __forceinline__ int quads_of(int nsb) { return (nsb + QWAVES - 1) / QWAVES; }
-__device__ __forceinline__ int slices_of(int quads, int C) { return (quads + C - 1) / C; }
-// Exclusive prefix of v over the workgroup's threads (in thread order); *total = the sum over all threads.
-__device__ __forceinline__ int block_scan(int v, RowTab& R, int* total) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int x = v;
+  for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
+  uint32_t* blk = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 4 * ((e + g) & 3);
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(x, o);
-    if (lane >= o) x += t;
+  for (int cb = 0; cb < 4; ++cb) {
+    const uint32_t hi = pa[cb] & 0xFFFF0000u;
+    *reinterpret_cast<u4v*>(blk + 16 * cb) =
+        u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
   }
-  __syncthreads();   // earlier readers of R.wsum are done
-  if (lane == 63) R.wsum[w] = x;
-  __syncthreads();
-  int add = 0;
-  for (int ww = 0; ww < w; ++ww) add += R.wsum[ww];
-  *total = R.wsum[0] + R.wsum[1] + R.wsum[2] + R.wsum[3];
-  return add + x - v;
 }
-static_assert(sizeof(XLds) <= sizeof(QLds), "exact-tail scratch must fit the split workgroup's LDS");
+// vlo / vsc bytes of token t (both head groups)
+__device__ __forceinline__ uint32_t scale_bytes(const uint8_t* __restrict__ sb, int t) {
+  return (uint32_t)*reinterpret_cast<const uint16_t*>(sb + VLO_O + 2 * t) |
+         ((uint32_t)*reinterpret_cast<const uint16_t*>(sb + VSC_O + 2 * t) << 16);
+}
 
-// Attention of row b's 16 query rows over its sub-blocks [j0, j1): wave w takes j0 + w, then every 4th.
-// The workgroup's partial (m, l, acc in the Hadamard domain) goes to partial rows prow .. prow + 15.
+struct QChunk {                // one chunk's data in registers
+  uint2 kc[2][4];              // [tile u][head h]: kc bytes of token 16 u + n, channels 8 g .. 8 g + 7
+  u4v cs[2][2];                // [tile u][d]: (cos, sin) bf16 pairs of channels 8 g + 4 d .. + 3 at the token's position
+  u4v vb[2];                   // vb bytes 32 lane .. 32 lane + 31 of the chunk: token lane / 2, heads 2 (lane % 2), + 1
+};
+__device__ __forceinline__ void qload(QChunk& C, const uint8_t* __restrict__ sb, const uint32_t* __restrict__ csb, int t0,
+                                      int lane) {
+  const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = t0 + 16 * u + n;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) C.kc[u][h] = *reinterpret_cast<const uint2*>(sb + KC_O + t * 128 + 32 * h + 8 * g);
+    const uint32_t* cp = csb + t * 32 + 8 * g;
+    C.cs[u][0] = *reinterpret_cast<const u4v*>(cp);
+    C.cs[u][1] = *reinterpret_cast<const u4v*>(cp + 4);
+  }
+  const uint8_t* vp = sb + VB_O + t0 * 64 + 32 * lane;
+  C.vb[0] = *reinterpret_cast<const u4v*>(vp);
+  C.vb[1] = *reinterpret_cast<const u4v*>(vp + 16);
+}
+
+// Scores of one tile for KV head H (all 16 query-row columns; column n is meaningful for H == n / 4).
+template <int H>
+__device__ __forceinline__ f4 qk_head(const char* lutc, uint2 kc, const u4v (&cs)[2], const u4v (&sw)[2], uint32_t gw,
+                                      uint32_t cg, const b8 (&bq)[4]) {
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t x = d ? kc.y : kc.x;
+    const uint32_t R = ((x << 2) & 0xCCCCCCCCu) | cg;   // byte e: 4 (c0 + 16 c2) + 16 rot, the rope entry's byte offset
+    const uint32_t N = (x & 0xCCCCCCCCu) | cg;          // byte e: 4 (c1 + 16 c3) + 16 rot, the nope entry's
+    uint32_t kk[4], an[4], ar[4], c4[4], s4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t sel = 0x0C0C0104u + (uint32_t)e;   // byte 0 = byte e of the index word, byte 1 = byte 1 of gw
+      const uint32_t ra = __builtin_amdgcn_perm(R, gw, sel), na = __builtin_amdgcn_perm(N, gw, sel);
+      kk[e] = *reinterpret_cast<const uint32_t*>(lutc + ra + 1024 * (H * 2 + d));
+      an[e] = *reinterpret_cast<const uint32_t*>(lutc + na + 1024 * ((4 + H) * 2 + d));
+      c4[e] = cs[d][e];
+      s4[e] = sw[d][e];
+    }
+    rope4(kk, c4, s4, ar);
+    acc = mfma_bf(pack8b(ar), bq[d], acc);
+    acc = mfma_bf(pack8b(an), bq[2 + d], acc);
+  }
+  return acc;
+}
+static_assert(sizeof(XLds) <= 65536, "exact-tail scratch too large");
+
+// Attention of row b's 16 query rows over its sub-blocks [j0, j1). The workgroup's partial (m, l, acc in the Hadamard
+// domain) goes to partial rows prow .. prow + 15. A sub-block whose offset falls outside the pool (or whose positions
+// fall outside the rope table) is skipped; its loads read the pool's first sub-block instead (the host requires the
+// pool to hold one).
 __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __restrict__ q,
                                            const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
                                            const int64_t* __restrict__ boff, int64_t bstride,
-                                           const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
+                                           const uint32_t* __restrict__ cs2, int64_t rope_rows, float* __restrict__ mo,
                                            float* __restrict__ lo_out, float* __restrict__ ao, float scale, const int b,
                                            const int j0, const int j1, const int64_t prow) {
   QLds& L = *reinterpret_cast<QLds*>(lds_raw);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
-  float* const s4w = reinterpret_cast<float*>(W.cs[1]);   // scale staging (see SCALE_FLOATS)
-  float* const tpw = s4w + 4 * HROW;
-  // kc bytes a lane reads for token group tg of a 16-token tile: token 4 (n / 4) + tg, head n % 4, channels 8 g .. + 7
-  const int kofs = (n >> 2) * 512 + (n & 3) * 32 + 8 * g;
+  const char* lutc = reinterpret_cast<const char*>(&L.lut[0][0]);
 
-  for (int i = tid; i < 16 * 128; i += 256) L.q[i >> 7][i & 127] = bf2f(q[(int64_t)b * 2048 + i]);   // padded rows
-  __syncthreads();
+  // q as the QK B operands: k-step d (rope) = (q[j], q[j + 64]) pairs, k-step 2 + d (nope) = (q[j + 32], q[j + 96]),
+  // j = 8 g + 4 d + e in register e
+  b8 bq[4];
+  {
+    const uint16_t* qr = q + ((int64_t)b * 16 + n) * 128 + 8 * g;
+    const u4v Q0 = *reinterpret_cast<const u4v*>(qr), Q1 = *reinterpret_cast<const u4v*>(qr + 32);
+    const u4v Q2 = *reinterpret_cast<const u4v*>(qr + 64), Q3 = *reinterpret_cast<const u4v*>(qr + 96);
+    auto el = [](const u4v& Q, int i) -> uint32_t { return (Q[i >> 1] >> (16 * (i & 1))) & 0xFFFFu; };
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      uint32_t r[4], p[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[e] = el(Q0, 4 * d + e) | (el(Q2, 4 * d + e) << 16);
+        p[e] = el(Q1, 4 * d + e) | (el(Q3, 4 * d + e) << 16);
+      }
+      bq[d] = pack8b(r);
+      bq[2 + d] = pack8b(p);
+    }
+  }
+  // byte e of cg: 16 ((e + g) % 4), the table rotation of lane group g
+  const uint32_t cg = (uint32_t)(16 * ((0 + g) & 3)) | ((uint32_t)(16 * ((1 + g) & 3)) << 8) |
+                      ((uint32_t)(16 * ((2 + g) & 3)) << 16) | ((uint32_t)(16 * ((3 + g) & 3)) << 24);
 
   float m = NEG_BIG, lsum = 0.f, lvs = 0.f;
   f4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int jb = j0 + w; jb < j1; jb += QWAVES) {
+  auto sub_base = [&](int jb) -> int64_t {
     const int64_t base = boff[(int64_t)b * bstride + jb];
-    if (base < 0 || base + SUB > qpool_bytes || (int64_t)(jb + 1) * BLK > rope_rows) continue;   // guard
-    const uint8_t* sb = qpool + base;
-    const uint32_t* csb = cs16 + (int64_t)jb * BLK * 32;
+    return (base < 0 || base > qpool_bytes - SUB || (int64_t)(jb + 1) * BLK > rope_rows) ? -1 : base;
+  };
+  auto stage_scales = [&](uint32_t x) {
+    float v[4];
+    f8x4(x, v);
+    W.vl[0][lane] = v[0]; W.vl[1][lane] = v[1]; W.vs[0][lane] = v[2]; W.vs[1][lane] = v[3];
+  };
 
-    // ---- stage per-sub-block scales as floats: S = scale ksc, T = klo per (head, channel); vlo / vsc
-    {
-      const uint2 lo2 = *reinterpret_cast<const uint2*>(sb + KLO_O + 8 * lane);   // channels 8 lane .. 8 lane + 7
-      const uint2 sc2 = *reinterpret_cast<const uint2*>(sb + KSC_O + 8 * lane);
-      float ksc[8], klo[8];
-      f8x4(sc2.x, ksc); f8x4(sc2.y, ksc + 4);
-      f8x4(lo2.x, klo); f8x4(lo2.y, klo + 4);
-      const int ho = (lane >> 4) * HROW + 8 * (lane & 15);   // head lane / 16, channels 8 (lane % 16) ..
-      // k = klo + ksc * code: the weights act on the integer code features
-      *reinterpret_cast<float4*>(s4w + ho) = make_float4(scale * ksc[0], scale * ksc[1], scale * ksc[2], scale * ksc[3]);
-      *reinterpret_cast<float4*>(s4w + ho + 4) = make_float4(scale * ksc[4], scale * ksc[5], scale * ksc[6], scale * ksc[7]);
-      *reinterpret_cast<float4*>(tpw + ho) = make_float4(klo[0], klo[1], klo[2], klo[3]);
-      *reinterpret_cast<float4*>(tpw + ho + 4) = make_float4(klo[4], klo[5], klo[6], klo[7]);
+  // One chunk of 32 tokens (tokens 64 w + 32 cc ..) of the current sub-block.
+  auto chunk = [&](const QChunk& C, int cc, uint32_t gw) {
+    {   // the chunk's vb rows into the wave's LDS copy (the previous chunk's reads were issued before)
+      const int t = lane >> 1, s = vb_slot(t), h0 = 2 * (lane & 1);
+      asm volatile("" ::: "memory");
+      W.vb[32 * h0 + s] = C.vb[0];
+      W.vb[32 * (h0 + 1) + s] = C.vb[1];
+      asm volatile("" ::: "memory");
     }
-    {
-      const uint2 vl2 = *reinterpret_cast<const uint2*>(sb + VLO_O + 8 * lane);   // bytes 8 lane .. 8 lane + 7
-      const uint2 vs2 = *reinterpret_cast<const uint2*>(sb + VSC_O + 8 * lane);
-      // byte 8 lane + e -> token 4 lane + e / 2, head group e & 1
-      float vl[8], vs[8];
-      f8x4(vl2.x, vl); f8x4(vl2.y, vl + 4);
-      f8x4(vs2.x, vs); f8x4(vs2.y, vs + 4);
-      *reinterpret_cast<float4*>(&W.vl[0][4 * lane]) = make_float4(vl[0], vl[2], vl[4], vl[6]);
-      *reinterpret_cast<float4*>(&W.vl[1][4 * lane]) = make_float4(vl[1], vl[3], vl[5], vl[7]);
-      *reinterpret_cast<float4*>(&W.vs[0][4 * lane]) = make_float4(vs[0], vs[2], vs[4], vs[6]);
-      *reinterpret_cast<float4*>(&W.vs[1][4 * lane]) = make_float4(vs[1], vs[3], vs[5], vs[7]);
+    float sv[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u4v sw[2];
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sw[d][e] = __builtin_amdgcn_alignbit(C.cs[u][d][e], C.cs[u][d][e], 16);   // (sin, cos)
+      const f4 a0 = qk_head<0>(lutc, C.kc[u][0], C.cs[u], sw, gw, cg, bq);
+      const f4 a1 = qk_head<1>(lutc, C.kc[u][1], C.cs[u], sw, gw, cg, bq);
+      const f4 a2 = qk_head<2>(lutc, C.kc[u][2], C.cs[u], sw, gw, cg, bq);
+      const f4 a3 = qk_head<3>(lutc, C.kc[u][3], C.cs[u], sw, gw, cg, bq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = (hn & 2) ? ((hn & 1) ? a3[i] : a2[i]) : ((hn & 1) ? a1[i] : a0[i]);
+        sv[u][i] = x * scale;
+      }
     }
-    // ---- prefetch chunk 0 (vb bytes, rope rows, kc rows of tiles 0 / 1)
-    u4v vbn0 = *reinterpret_cast<const u4v*>(sb + VB_O + 32 * lane);
-    u4v vbn1 = *reinterpret_cast<const u4v*>(sb + VB_O + 32 * lane + 16);
-    u4v csn[4];
+    // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
+    float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+    tmax = max4rows(tmax);
+    if (__any(tmax > m + QLAZY)) {
+      const float mn = fmaxf(m, tmax);
+      const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
+      m = mn; lsum *= al; lvs *= al;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const u4v*>(csb + 256 * u + 4 * lane);
-    const uint8_t* kcb = sb + KC_O + kofs;
-    uint2 kn[2][4];
+      for (int i = 0; i < 8; ++i) acc[i] *= al;
+    }
+    float wt[2][4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u) {
+      const int t0 = 32 * cc + 16 * u + 4 * g;
+      const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
+      const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);
+      const float p0 = __builtin_amdgcn_exp2f(sv[u][0] - m), p1 = __builtin_amdgcn_exp2f(sv[u][1] - m);
+      const float p2 = __builtin_amdgcn_exp2f(sv[u][2] - m), p3 = __builtin_amdgcn_exp2f(sv[u][3] - m);
+      lsum += (p0 + p1) + (p2 + p3);
+      lvs += (p0 * vl4.x + p1 * vl4.y) + (p2 * vl4.z + p3 * vl4.w);
+      wt[u][0] = p0 * vs4.x; wt[u][1] = p1 * vs4.y; wt[u][2] = p2 * vs4.z; wt[u][3] = p3 * vs4.w;
+    }
+    // B in the K order of the A registers: (k0, k2), (k1, k3), (k4, k6), (k5, k7), token k of the group = slot 8 g + k
+    const h8 Bw = pack8(pk2(wt[0][0], wt[0][2]), pk2(wt[0][1], wt[0][3]), pk2(wt[1][0], wt[1][2]), pk2(wt[1][1], wt[1][3]));
+    // ---- PV per head: A row n = dim n of plane i, bytes of the group's 8 tokens by one transposed read
 #pragma unroll
-      for (int tg = 0; tg < 4; ++tg) kn[u][tg] = *reinterpret_cast<const uint2*>(kcb + (16 * u + tg) * 128);
-    __builtin_amdgcn_wave_barrier();
+    for (int h = 0; h < 4; ++h) {
+      const h8 B = (hn == h) ? Bw : pack8(0u, 0u, 0u, 0u);
+      typedef __attribute__((address_space(3))) i2v lds_i2;
+      const i2v X = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (lds_i2*)(reinterpret_cast<char*>(W.vb) + (h * 32 + 8 * g) * 16 + 8 * n));
+      const uint32_t x0 = (uint32_t)X.x, x1 = (uint32_t)X.x >> 8, x2 = (uint32_t)X.y, x3 = (uint32_t)X.y >> 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t msk = (1u << i) | (1u << (16 + i));
+        acc[i] = mfma16(pack8(x0 & msk, x1 & msk, x2 & msk, x3 & msk), B, acc[i]);
+      }
+    }
+    asm volatile("" ::: "memory");   // the transposed reads stay before the next chunk's staging
+  };
 
-    // ---- weights of this sub-block (B operands), scaled by `scale` so the accumulator is in log2 units.
-    // Rope / nope MFMAs: lane (g, n) holds the weights of query row n (head hn's scales) for channels 8 g .. 8 g + 7:
-    // block r < 4 = channels 8 g + 2 r, + 1 (4 rope features each), nope block p = channels 8 g + 4 p .. + 3.
-    const float* qn = L.q[n];
-    const float* sh = s4w + hn * HROW;
-    const float* tpn = tpw + hn * HROW;
-    h8 wr[4], wnp[2], wt[2];
-    {
-      float q0[8], q1[8], q2[8], q3[8], s0[8], s1[8], s2[8], s3[8];
-      auto ld8 = [](const float* p, float* o) {
-        const float4 x = *reinterpret_cast<const float4*>(p), y = *reinterpret_cast<const float4*>(p + 4);
-        o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
-      };
-      ld8(qn + 8 * g, q0); ld8(qn + 32 + 8 * g, q1); ld8(qn + 64 + 8 * g, q2); ld8(qn + 96 + 8 * g, q3);
-      ld8(sh + 8 * g, s0); ld8(sh + 32 + 8 * g, s1); ld8(sh + 64 + 8 * g, s2); ld8(sh + 96 + 8 * g, s3);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e0 = 2 * r, e1 = 2 * r + 1;
-        wr[r] = pack8(pk2(q0[e0] * s0[e0], q2[e0] * s0[e0]), pk2(q2[e0] * s2[e0], -q0[e0] * s2[e0]),
-                      pk2(q0[e1] * s0[e1], q2[e1] * s0[e1]), pk2(q2[e1] * s2[e1], -q0[e1] * s2[e1]));
+  if (j0 < j1) {
+    int64_t base = sub_base(j0);
+    const uint8_t* sb = qpool + (base < 0 ? 0 : base);
+    QChunk C0, C1;
+    qload(C0, sb, cs2 + (int64_t)(base < 0 ? 0 : j0) * BLK * 32, 64 * w, lane);
+    lut_build(L.lut[0], tid, table_bytes(sb, tid));
+    stage_scales(scale_bytes(sb, 64 * w + lane));
+    __syncthreads();
+    uint32_t buf = 0;
+    for (int jb = j0; jb < j1; ++jb) {
+      const bool more = jb + 1 < j1;
+      const int64_t nbase = more ? sub_base(jb + 1) : -1;
+      const uint8_t* nsb = qpool + (nbase < 0 ? 0 : nbase);
+      uint32_t ntb = 0, nsc = 0;
+      if (more) { ntb = table_bytes(nsb, tid); nsc = scale_bytes(nsb, 64 * w + lane); }
+      const uint32_t gw = ((buf << 6) | (uint32_t)g) << 8;   // byte 1: LUT buffer and lane group (256-byte blocks)
+      qload(C1, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * w + 32, lane);
+      if (base >= 0) chunk(C0, 0, gw);
+      if (more) qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : jb + 1) * BLK * 32, 64 * w, lane);
+      if (base >= 0) chunk(C1, 1, gw);
+      if (more) {
+        lut_build(L.lut[buf ^ 1u], tid, ntb);
+        stage_scales(nsc);
       }
-#pragma unroll
-      for (int pq = 0; pq < 2; ++pq) {
-        const int e = 4 * pq;
-        wnp[pq] = pack8(pk2(q1[e] * s1[e], q3[e] * s3[e]), pk2(q1[e + 1] * s1[e + 1], q3[e + 1] * s3[e + 1]),
-                        pk2(q1[e + 2] * s1[e + 2], q3[e + 2] * s3[e + 2]), pk2(q1[e + 3] * s1[e + 3], q3[e + 3] * s3[e + 3]));
-      }
-    }
-    // table part (all 16 rows, dense): lane (g, n) channels 16 kk + 4 g .. + 3, features (cos, sin)
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int jc = 16 * kk + 4 * g;
-      const float4 q0 = *reinterpret_cast<const float4*>(qn + jc), q2 = *reinterpret_cast<const float4*>(qn + 64 + jc);
-      const float4 T0 = *reinterpret_cast<const float4*>(tpn + jc), T2 = *reinterpret_cast<const float4*>(tpn + 64 + jc);
-      const float a0[4] = {q0.x, q0.y, q0.z, q0.w}, a2[4] = {q2.x, q2.y, q2.z, q2.w};
-      const float t0[4] = {T0.x, T0.y, T0.z, T0.w}, t2[4] = {T2.x, T2.y, T2.z, T2.w};
-      uint32_t ht[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        ht[u] = pk2(scale * (a0[u] * t0[u] + a2[u] * t2[u]), scale * (a2[u] * t0[u] - a0[u] * t2[u]));
-      wt[kk] = pack8(ht[0], ht[1], ht[2], ht[3]);
-    }
-    float c13 = 0.f;
-    {
-      const float4 q1a = *reinterpret_cast<const float4*>(qn + 32 + 8 * g), q1b = *reinterpret_cast<const float4*>(qn + 36 + 8 * g);
-      const float4 q3a = *reinterpret_cast<const float4*>(qn + 96 + 8 * g), q3b = *reinterpret_cast<const float4*>(qn + 100 + 8 * g);
-      const float4 t1a = *reinterpret_cast<const float4*>(tpn + 32 + 8 * g), t1b = *reinterpret_cast<const float4*>(tpn + 36 + 8 * g);
-      const float4 t3a = *reinterpret_cast<const float4*>(tpn + 96 + 8 * g), t3b = *reinterpret_cast<const float4*>(tpn + 100 + 8 * g);
-      c13 = q1a.x * t1a.x + q1a.y * t1a.y + q1a.z * t1a.z + q1a.w * t1a.w + q1b.x * t1b.x + q1b.y * t1b.y + q1b.z * t1b.z +
-            q1b.w * t1b.w + q3a.x * t3a.x + q3a.y * t3a.y + q3a.z * t3a.z + q3a.w * t3a.w + q3b.x * t3b.x +
-            q3b.y * t3b.y + q3b.z * t3b.z + q3b.w * t3b.w;
-    }
-    c13 = sum4rows(c13) * scale;
-    asm volatile("" ::: "memory");   // the scale staging reads above stay before the chunk stores below
-
-    // ---- 8 chunks of 32 tokens (2 QK tiles + 1 PV step)
-#pragma unroll 2
-    for (int c = 0; c < 8; ++c) {
-      const int cb = c & 1;   // constant in each of the two unrolled copies
-      // lane holds token lane / 2, pieces 2 (lane % 2) and 2 (lane % 2) + 1; rope dwords 256 u + 4 lane
-      W.vb[cb][vb_at(lane >> 1, 2 * (lane & 1))] = vbn0;
-      W.vb[cb][vb_at(lane >> 1, 2 * (lane & 1) + 1)] = vbn1;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r = 8 * u + (lane >> 3);
-        W.cs[cb][cs_at(r, lane & 7)] = csn[u];
-      }
-      uint2 kc[2][4];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int tg = 0; tg < 4; ++tg) kc[u][tg] = kn[u][tg];
-      if (c + 1 < 8) {   // prefetch the next chunk
-        const uint8_t* vbp = sb + VB_O + (c + 1) * 32 * 64 + 32 * lane;
-        vbn0 = *reinterpret_cast<const u4v*>(vbp);
-        vbn1 = *reinterpret_cast<const u4v*>(vbp + 16);
-        const uint32_t* csp = csb + (c + 1) * 32 * 32;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) csn[u] = *reinterpret_cast<const u4v*>(csp + 256 * u + 4 * lane);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int tg = 0; tg < 4; ++tg)
-            kn[u][tg] = *reinterpret_cast<const uint2*>(kcb + (32 * (c + 1) + 16 * u + tg) * 128);
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-
-      // Wave priority by phase: the QK features (LDS reads feeding VALU feeding MFMA) go first, the softmax next, PV
-      // last, so that of the SIMD's two waves the one still in QK wins the issue slots over one already in PV, whose
-      // MFMA chain then overlaps it; measured 3-4 % faster than equal priority.
-      __builtin_amdgcn_s_setprio(2);
-      f4 sacc2[2];   // lane (g, n) register i: score of token 32 c + 16 u + 4 g + i, query row n
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        // table part: A row n = token 16 u + n
-        const int trow = 16 * u + n;
-        f4 tacc = {c13, c13, c13, c13};
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const u4v t4 = W.cs[cb][cs_at(trow, 4 * kk + g)];
-          tacc = mfma16(__builtin_bit_cast(h8, t4), wt[kk], tacc);
-        }
-        // rope / nope part, 4 token groups: A row n = (token 16 u + 4 (n / 4) + tg, head n % 4); the result for query
-        // row n sits in output register n / 4 (the output rows of other heads are discarded)
-#pragma unroll
-        for (int tg = 0; tg < 4; ++tg) {
-          const int tok = 16 * u + 4 * (n >> 2) + tg;
-          const u4v cA = W.cs[cb][cs_at(tok, 2 * g)];
-          const u4v cB = W.cs[cb][cs_at(tok, 2 * g + 1)];
-          f4 a = {0.f, 0.f, 0.f, 0.f};
-          a = rope_nope(kc[u][tg].x, cA, wr[0], wr[1], wnp[0], a);
-          a = rope_nope(kc[u][tg].y, cB, wr[2], wr[3], wnp[1], a);
-          const float lo = (hn & 1) ? a[1] : a[0], hi = (hn & 1) ? a[3] : a[2];
-          sacc2[u][tg] = tacc[tg] + ((hn & 2) ? hi : lo);
-        }
-      }
-      __builtin_amdgcn_s_setprio(1);
-      // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
-      float tmax = fmaxf(fmaxf(fmaxf(sacc2[0][0], sacc2[0][1]), fmaxf(sacc2[0][2], sacc2[0][3])),
-                         fmaxf(fmaxf(sacc2[1][0], sacc2[1][1]), fmaxf(sacc2[1][2], sacc2[1][3])));
-      tmax = max4rows(tmax);
-      if (__any(tmax > m + LAZY)) {
-        const float mn = fmaxf(m, tmax);
-        const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
-        m = mn; lsum *= al; lvs *= al;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] *= al;
-      }
-      uint32_t bpv[4];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const f4 sacc = sacc2[u];
-        const int t0 = 32 * c + 16 * u + 4 * g;
-        const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
-        const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);
-        const float p0 = __builtin_amdgcn_exp2f(sacc[0] - m), p1 = __builtin_amdgcn_exp2f(sacc[1] - m);
-        const float p2 = __builtin_amdgcn_exp2f(sacc[2] - m), p3 = __builtin_amdgcn_exp2f(sacc[3] - m);
-        lsum += (p0 + p1) + (p2 + p3);
-        lvs += (p0 * vl4.x + p1 * vl4.y) + (p2 * vl4.z + p3 * vl4.w);
-        const h2 w01 = {(_Float16)(p0 * vs4.x), (_Float16)(p1 * vs4.y)};
-        const h2 w23 = {(_Float16)(p2 * vs4.z), (_Float16)(p3 * vs4.w)};
-        bpv[2 * u] = hbits(w01);
-        bpv[2 * u + 1] = hbits(w23);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      // ---- PV: per head hh, plane i. Lane (g, jj = n): bytes jj of tokens 32 c + {4 g + (0..3), 16 + 4 g + (0..3)}
-      const uint8_t* vbc = reinterpret_cast<const uint8_t*>(W.vb[cb]);
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const bool mine = (hn == hh);
-        const h8 B = mine ? pack8(bpv[0], bpv[1], bpv[2], bpv[3]) : pack8(0u, 0u, 0u, 0u);
-        uint32_t D[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int ta = 16 * (v >> 1) + 4 * g + 2 * (v & 1);
-          D[v] = (uint32_t)vbc[16 * vb_at(ta, hh) + n] | ((uint32_t)vbc[16 * vb_at(ta + 1, hh) + n] << 16);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t msk = (1u << i) | (1u << (16 + i));
-          const h8 A = pack8(D[0] & msk, D[1] & msk, D[2] & msk, D[3] & msk);
-          acc[i] = mfma16(A, B, acc[i]);
-        }
-      }
+      __syncthreads();
+      buf ^= 1u;
+      base = nbase;
+      sb = nsb;
     }
   }
 
-  // ---- combine the 4 waves of the split
+  // ---- combine the 4 waves of the span
   lsum = sum4rows(lsum);
   lvs = sum4rows(lvs);
   __syncthreads();
@@ -863,13 +795,84 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   *reinterpret_cast<float4*>(ao + row * 128 + d0 + 4) = r1;
 }
 
+// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one row's
+// KV head(s) (its exact partial slot, as decode_exact_kernel<false>) before the split workgroups, so their memory
+// latency overlaps the splits' VALU work on the same CUs instead of following it.
+struct ExactArgs {
+  kv800_paged_t P;
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  int64_t rope_rows, epool_elems, sink_elems;
+  int64_t xs0, xst;   // exact partial of row b in slot xs0 + b xst
+  int nexact, nsink;
+};
+
+// Balanced schedule (groups > 0): the B rows' sub-blocks laid end to end, q_b sub-blocks in row b, T = sum q_b. With
+// C = ceil(T / groups), row b is cut into n_b = ceil(q_b / C) slices of at most C sub-blocks, and the slices of all rows
+// are laid end to end: row b's at workgroup indices [pre[b], pre[b + 1]). Workgroup g takes one slice and writes its
+// partial to slot g; sum n_b <= T / C + B <= groups + B, so the grid has groups + B workgroups and the ones past the
+// last slice return at once. The exact partial of row b is slot groups + B + b. groups = 0: the fixed (row, split)
+// grid, split s of row b in slot b (ns + 1) + s, the exact partial in slot b (ns + 1) + ns (the reference's partial
+// layout).
+struct Sched {
+  int32_t* pre;         // pre[0 .. B]: written by workgroup 0 of the decode grid, read by the merge
+  int groups, B, cap;   // cap: sub-blocks per row are clamped to [0, cap]
+};
+
+// The decode grid's workgroups each scan NQ themselves: thread t owns rows [t k, t k + k), k = ceil(B / 256), reads
+// their counts once (into registers, up to RREG rows, i.e. B <= 1024; later rows are read again) and takes part in
+// two block-wide scans, of the sub-blocks (for T) and of the slices.
+constexpr int RREG = 4;
+struct RowTab {
+  int wsum[4];
+  int b, pb, nsb;       // the row of this workgroup's slice, its first slice index, its clamped sub-block count
+};
+struct RowCache {       // this thread's rows [r0, r1) and their clamped sub-block counts
+  int r0, r1;
+  int v[RREG];
+};
+__device__ __forceinline__ void load_rows(const int32_t* __restrict__ nq, const Sched& S, RowCache& C) {
+  const int k = (S.B + 255) >> 8;
+  C.r0 = min((int)threadIdx.x * k, S.B);
+  C.r1 = min(C.r0 + k, S.B);
+#pragma unroll
+  for (int i = 0; i < RREG; ++i) C.v[i] = (C.r0 + i < C.r1) ? min(max(nq[C.r0 + i], 0), S.cap) : 0;
+}
+__device__ __forceinline__ int nsb_of(const int32_t* __restrict__ nq, const Sched& S, const RowCache& C, int i) {
+  int x = 0;
+#pragma unroll
+  for (int k = 0; k < RREG; ++k)
+    if (k == i) x = C.v[k];
+  return i < RREG ? x : min(max(nq[C.r0 + i], 0), S.cap);
+}
+__device__ __forceinline__ int slices_of(int nsb, int C) { return (nsb + C - 1) / C; }
+// Exclusive prefix of v over the workgroup's threads (in thread order); *total = the sum over all threads.
+__device__ __forceinline__ int block_scan(int v, RowTab& R, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(x, o);
+    if (lane >= o) x += t;
+  }
+  __syncthreads();   // earlier readers of R.wsum are done
+  if (lane == 63) R.wsum[w] = x;
+  __syncthreads();
+  int add = 0;
+  for (int ww = 0; ww < w; ++ww) add += R.wsum[ww];
+  *total = R.wsum[0] + R.wsum[1] + R.wsum[2] + R.wsum[3];
+  return add + x - v;
+}
+
+constexpr int QLDS_BYTES = sizeof(QLds) > sizeof(XLds) ? (int)sizeof(QLds) : (int)sizeof(XLds);
+
 __global__ void __launch_bounds__(256, 2)
 decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ qpool, int64_t qpool_bytes,
                     const int64_t* __restrict__ boff, int64_t bstride, const int32_t* __restrict__ nq,
-                    const uint32_t* __restrict__ cs16, int64_t rope_rows, float* __restrict__ mo,
+                    const uint32_t* __restrict__ cs2, int64_t rope_rows, float* __restrict__ mo,
                     float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale, ExactArgs X,
                     Sched S) {
-  __shared__ __align__(16) char lds_raw[sizeof(QLds)];
+  __shared__ __align__(16) char lds_raw[QLDS_BYTES];
   if ((int)blockIdx.x < X.nexact) {
     constexpr int G = 4 / XNH_TAIL;   // workgroups per row
     const int b = (int)blockIdx.x / G;
@@ -879,7 +882,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     return;
   }
   const int blk = (int)blockIdx.x - X.nexact;
-  // fixed grid: (row b, split s); balanced: slice blk (one row's quads [c0, c1))
+  // fixed grid: (row b, split s); balanced: slice blk (one row's sub-blocks [j0, j1))
   int b, j0, j1;
   int64_t prow;
   if (S.groups == 0) {
@@ -893,7 +896,7 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     RowCache RC;
     load_rows(nq, S, RC);
     int qsum = 0;
-    for (int i = 0; i < RC.r1 - RC.r0; ++i) qsum += quads_of(nsb_of(nq, S, RC, i));
+    for (int i = 0; i < RC.r1 - RC.r0; ++i) qsum += nsb_of(nq, S, RC, i);
     int T;
     block_scan(qsum, R, &T);
     if (T <= 0) {   // no quantized work in any row
@@ -903,31 +906,31 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     }
     const int C = (T + S.groups - 1) / S.groups;
     int nsl = 0;
-    for (int i = 0; i < RC.r1 - RC.r0; ++i) nsl += slices_of(quads_of(nsb_of(nq, S, RC, i)), C);
+    for (int i = 0; i < RC.r1 - RC.r0; ++i) nsl += slices_of(nsb_of(nq, S, RC, i), C);
     int G2;
     int p = block_scan(nsl, R, &G2);
     if (blk == 0) {   // pre[0 .. B] for the merge
       if (threadIdx.x == 0) S.pre[0] = 0;
       int pp = p;
       for (int i = 0; i < RC.r1 - RC.r0; ++i) {
-        pp += slices_of(quads_of(nsb_of(nq, S, RC, i)), C);
+        pp += slices_of(nsb_of(nq, S, RC, i), C);
         S.pre[RC.r0 + i + 1] = pp;
       }
     }
     if (blk >= G2) return;   // past the last slice (uniform over the workgroup)
     for (int i = 0; i < RC.r1 - RC.r0; ++i) {   // exactly one thread owns the row of slice blk
-      const int nb = nsb_of(nq, S, RC, i), n = slices_of(quads_of(nb), C);
+      const int nb = nsb_of(nq, S, RC, i), n = slices_of(nb, C);
       if (p <= blk && blk < p + n) { R.b = RC.r0 + i; R.pb = p; R.nsb = nb; }
       p += n;
     }
     __syncthreads();
     b = __builtin_amdgcn_readfirstlane(R.b);
     const int k = blk - __builtin_amdgcn_readfirstlane(R.pb), nb = __builtin_amdgcn_readfirstlane(R.nsb);
-    j0 = QWAVES * C * k;
-    j1 = min(QWAVES * C * (k + 1), nb);
+    j0 = C * k;
+    j1 = min(C * (k + 1), nb);
     prow = (int64_t)blk * 16;
   }
-  quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs16, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
+  quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs2, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
 }
 
 
@@ -1061,21 +1064,22 @@ int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_
 // Launches the quantized-split grid; xa != null adds the exact-tail workgroups (arguments checked by
 // check_exact).
 int launch_quant(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
-                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows, float* mo, float* lo,
+                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs2, int64_t rope_rows, float* mo, float* lo,
                  float* ao, int64_t B, int64_t ns, int64_t spb, float scale, const ExactArgs* xa, Sched S,
                  void* stream) {
   KV800_REQUIRE(B >= 0 && ns >= 0 && spb >= 1, "decode_quant: need B >= 0, ns >= 0, spb >= 1");
   if (B == 0 || ns == 0) return KV800_OK;
-  KV800_REQUIRE(q && qpool && boff && nq && cs16 && mo && lo && ao, "decode_quant: null pointer");
+  KV800_REQUIRE(q && qpool && boff && nq && cs2 && mo && lo && ao, "decode_quant: null pointer");
+  KV800_REQUIRE(qpool_bytes >= SUB, "decode_quant: the quant pool must hold at least one sub-block");
   const int64_t nwork = S.groups ? S.groups + B : B * ns;
   KV800_REQUIRE(nwork + B * 4 <= 0x7FFFFFFF && ns * spb <= 0x7FFFFFFF, "decode_quant: grid too large");
-  KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs16 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
-                "decode_quant: qpool / cs16 / ao must be 16-byte aligned");
+  KV800_REQUIRE(((uintptr_t)qpool % 16) == 0 && ((uintptr_t)cs2 % 16) == 0 && ((uintptr_t)ao % 16) == 0,
+                "decode_quant: qpool / cs2 / ao must be 16-byte aligned");
   ExactArgs X{};
   if (xa) X = *xa;
   else X.nexact = 0;
   hipLaunchKernelGGL(decode_quant_kernel, dim3((unsigned)(nwork + X.nexact)), dim3(256), 0, (hipStream_t)stream, q,
-                     qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale, X,
+                     qpool, qpool_bytes, boff, boff_stride, nq, cs2, rope_rows, mo, lo, ao, (int)ns, (int)spb, scale, X,
                      S);
   return check_launch(xa ? "decode_quant_exact" : "decode_quant");
 }
@@ -1087,22 +1091,22 @@ using namespace kv800;
 
 extern "C" {
 
-int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs16, void* stream) {
+int kv800_hip_rope_table(const uint16_t* cos_t, const uint16_t* sin_t, int64_t P, uint32_t* cs2, void* stream) {
   KV800_REQUIRE(P >= 0, "rope_table: P < 0");
   if (P == 0) return KV800_OK;
-  KV800_REQUIRE(cos_t && sin_t && cs16, "rope_table: null pointer");
+  KV800_REQUIRE(cos_t && sin_t && cs2, "rope_table: null pointer");
   const int64_t n = P * 32;
   hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, cos_t,
-                     sin_t, n, cs16);
+                     sin_t, n, cs2);
   return check_launch("rope_table");
 }
 
 int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb) {
   KV800_REQUIRE(B >= 0 && nqmax >= 0 && ns && spb, "plan: bad arguments");
   if (nqmax == 0 || B == 0) { *ns = 0; *spb = 1; return KV800_OK; }
-  // ~512 workgroups (2 per CU), each wave owning whole sub-blocks
+  // ~512 workgroups (2 per CU), each taking whole sub-blocks
   const int64_t want = (512 + B - 1) / B;
-  const int64_t cap = (nqmax + QWAVES - 1) / QWAVES;
+  const int64_t cap = nqmax;
   int64_t n_s = want < cap ? want : cap;
   if (n_s < 1) n_s = 1;
   const int64_t sp = (nqmax + n_s - 1) / n_s;
@@ -1112,17 +1116,17 @@ int kv800_hip_plan(int64_t B, int64_t nqmax, int64_t* ns, int64_t* spb) {
 }
 
 int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_t qpool_bytes, const int64_t* boff,
-                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs16, int64_t rope_rows,
+                                 int64_t boff_stride, const int32_t* nq, const uint32_t* cs2, int64_t rope_rows,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
                                  void* stream) {
-  return launch_quant(q, qpool, qpool_bytes, boff, boff_stride, nq, cs16, rope_rows, mo, lo, ao, B, ns, spb, scale,
+  return launch_quant(q, qpool, qpool_bytes, boff, boff_stride, nq, cs2, rope_rows, mo, lo, ao, B, ns, spb, scale,
                       nullptr, Sched{nullptr, 0, (int)B, 0}, stream);
 }
 
 int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
-                           const int32_t* nq, const uint32_t* cs16, float* mo, float* lo, float* ao, int64_t B,
+                           const int32_t* nq, const uint32_t* cs2, float* mo, float* lo, float* ao, int64_t B,
                            int64_t ns, int64_t spb, float scale, void* stream) {
-  return kv800_hip_decode_quant_sized(q, qpool, INT64_MAX / 2, boff, boff_stride, nq, cs16, INT64_MAX / 2, mo, lo, ao,
+  return kv800_hip_decode_quant_sized(q, qpool, INT64_MAX / 2, boff, boff_stride, nq, cs2, INT64_MAX / 2, mo, lo, ao,
                                       B, ns, spb, scale, stream);
 }
 
@@ -1163,13 +1167,13 @@ int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
   KV800_REQUIRE(B >= 0 && nqmax >= 0 && groups, "plan_balanced: bad arguments");
   // about BAL_CHUNK sub-blocks per workgroup (at most BAL_GROUPS workgroups) at the batch's largest size B * nqmax;
   // ragged batches hold fewer sub-blocks, and each workgroup then takes proportionally fewer
-  const int64_t want = (B * ((nqmax + QWAVES - 1) / QWAVES) * QWAVES + BAL_CHUNK - 1) / BAL_CHUNK;
+  const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK;
   *groups = want < 1 ? 1 : want > BAL_GROUPS ? BAL_GROUPS : want;
   return KV800_OK;
 }
 
 int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
-                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs16, int64_t qpool_bytes,
+                           const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs2, int64_t qpool_bytes,
                            int64_t epool_elems, int64_t sink_elems, uint16_t* out, void* workspace,
                            int64_t workspace_bytes, int64_t spb, void* stream) {
   KV800_REQUIRE(P && B >= 0, "decode: bad arguments");
@@ -1212,8 +1216,8 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
     sp = nqmax;
     slots = 2 * B + G;
   }
-  const int64_t need = S.groups ? kv800_hip_decode_workspace_balanced(B, S.groups, cs16 ? 0 : rows)
-                                : kv800_hip_decode_workspace(B, ns, cs16 ? 0 : rows);
+  const int64_t need = S.groups ? kv800_hip_decode_workspace_balanced(B, S.groups, cs2 ? 0 : rows)
+                                : kv800_hip_decode_workspace(B, ns, cs2 ? 0 : rows);
   KV800_REQUIRE(workspace_bytes >= need, "decode: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
                 (long long)need);
   float* mo = (float*)ws;
@@ -1225,9 +1229,9 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
     tail += align256((B + 1) * 4);
   }
   uint32_t* cst = (uint32_t*)tail;
-  if (!cs16) {
+  if (!cs2) {
     if ((rc = kv800_hip_rope_table(cos_t, sin_t, rows, cst, stream)) != KV800_OK) return rc;
-    cs16 = cst;
+    cs2 = cst;
   }
   // quantized work and the exact tail in one grid, then the merge
   ExactArgs X{};
@@ -1236,7 +1240,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   X.xs0 = S.groups ? B + S.groups : ns;
   X.xst = S.groups ? 1 : ns + 1;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;
-  if ((rc = launch_quant(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs16, rows, mo, lo, ao, B, ns, sp,
+  if ((rc = launch_quant(q, P->qpool, qpool_bytes, P->boff, P->boff_stride, P->NQ, cs2, rows, mo, lo, ao, B, ns, sp,
                          scale, &X, S, stream)) != KV800_OK)
     return rc;
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
@@ -1246,10 +1250,10 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
 }
 
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
-                     const uint16_t* sin_t, const uint32_t* cs16, uint16_t* out, void* workspace,
+                     const uint16_t* sin_t, const uint32_t* cs2, uint16_t* out, void* workspace,
                      int64_t workspace_bytes, int64_t spb, void* stream) {
   const int64_t rows = P ? (P->win ? 0 : P->nqmax) * BLK : 0;
-  return kv800_hip_decode_sized(P, q, B, cos_t, sin_t, rows > 0 ? rows : INT64_MAX / 2, cs16, INT64_MAX / 2,
+  return kv800_hip_decode_sized(P, q, B, cos_t, sin_t, rows > 0 ? rows : INT64_MAX / 2, cs2, INT64_MAX / 2,
                                 INT64_MAX / 2, INT64_MAX / 2, out, workspace, workspace_bytes, spb, stream);
 }
 

@@ -349,24 +349,27 @@ def combine(MO, LO, AO, ns):
 
 
 # ---------------------------------------------------------------- decode
-_CS16 = OrderedDict()      # (device, cos ptr, sin ptr, rows, versions) -> fp16 pair table; tables are model constants
+_PAIRS = OrderedDict()     # (device, cos ptr, sin ptr, rows) -> (cos_t, sin_t, versions, pair table)
 
 
-def rope_table16(cos_t, sin_t):
-    """Packed fp16 (cos, sin) table of every row of the bf16 tables, cached per table tensors (re-built when either
-    tensor is modified in place)."""
-    key = (str(cos_t.device), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0], cos_t._version, sin_t._version)
-    t = _CS16.get(key)
-    if t is None:
-        L = ops()
-        P = cos_t.shape[0]
-        t = torch.empty(P, 32, dtype=torch.int32, device=cos_t.device)
-        _check(L.kv800_hip_rope_table(_ptr(cos_t), _ptr(sin_t), P, _ptr(t), _stream(cos_t.device)))
-        _CS16[key] = t
-        while len(_CS16) > 8:
-            _CS16.popitem(last=False)
-    else:
-        _CS16.move_to_end(key)
+def rope_pairs(cos_t, sin_t):
+    """Packed bf16 (cos, sin) pair table of every row of the bf16 tables (kv800_hip_rope_table), cached per table
+    tensors. The entry holds the two tables themselves, so their storage cannot be freed and reused by other tensors
+    while it is cached; it is rebuilt when either tensor is modified in place (version counter) or replaced."""
+    key = (str(cos_t.device), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0])
+    ent = _PAIRS.get(key)
+    ver = (cos_t._version, sin_t._version)
+    if ent is not None and ent[0] is cos_t and ent[1] is sin_t and ent[2] == ver:
+        _PAIRS.move_to_end(key)
+        return ent[3]
+    L = ops()
+    P = cos_t.shape[0]
+    t = torch.empty(P, 32, dtype=torch.int32, device=cos_t.device)
+    _check(L.kv800_hip_rope_table(_ptr(cos_t), _ptr(sin_t), P, _ptr(t), _stream(cos_t.device)))
+    _PAIRS[key] = (cos_t, sin_t, ver, t)
+    _PAIRS.move_to_end(key)
+    while len(_PAIRS) > 8:
+        _PAIRS.popitem(last=False)
     return t
 
 
@@ -441,7 +444,7 @@ def decode(P, q, cos_t, sin_t, spb=None, target=None, groups=None):
     out = torch.empty(B, 16, 128, dtype=torch.bfloat16, device=dev)
     if B == 0:
         return out
-    cs16 = rope_table16(cos_t, sin_t) if s.nqmax else None
+    cs2 = rope_pairs(cos_t, sin_t) if s.nqmax else None
     if not s.nqmax:
         arg, wsb = 0, int(L.kv800_hip_decode_workspace(B, 0, 0))
     elif spb is None and not target:
@@ -453,7 +456,7 @@ def decode(P, q, cos_t, sin_t, spb=None, target=None, groups=None):
         ns, arg = plan(B, s.nqmax, spb, target)
         wsb = int(L.kv800_hip_decode_workspace(B, ns, 0))
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-    _check(L.kv800_hip_decode_sized(ctypes.byref(s), _ptr(q), B, _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], _ptr(cs16),
+    _check(L.kv800_hip_decode_sized(ctypes.byref(s), _ptr(q), B, _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], _ptr(cs2),
                                     qbytes, eelems, selems, _ptr(out), _ptr(ws), wsb, arg, _stream(dev)))
     return out
 
@@ -473,8 +476,8 @@ def decode_parts(P, q, cos_t, sin_t, spb=None, target=None):
     scale = 128 ** -0.5 * LOG2E
     st = _stream(dev)
     if ns:
-        cs16 = rope_table16(cos_t, sin_t)
-        _check(L.kv800_hip_decode_quant_sized(_ptr(q), s.qpool, qbytes, s.boff, s.boff_stride, _ptr(P.NQ), _ptr(cs16),
+        cs2 = rope_pairs(cos_t, sin_t)
+        _check(L.kv800_hip_decode_quant_sized(_ptr(q), s.qpool, qbytes, s.boff, s.boff_stride, _ptr(P.NQ), _ptr(cs2),
                                               cos_t.shape[0], _ptr(MO), _ptr(LO), _ptr(AO), B, ns, sp, scale, st))
     _check(L.kv800_hip_decode_exact_sized(ctypes.byref(s), _ptr(q), _ptr(cos_t), _ptr(sin_t), cos_t.shape[0], eelems,
                                           selems, _ptr(MO), _ptr(LO), _ptr(AO), B, ns, scale, st))

@@ -2,12 +2,10 @@
 
 Bars:
   * quantizer / flush / dequantizer: bit-exact with the oracle and the golden fixtures;
-  * decode, inputs of the BASELINE configs (q, K, V ~ N(0, 1)): within 2e-2 max-abs and 1e-3 mean-abs of the oracle's
-    restatement of torch_decode.py (both bf16 outputs, same cache bytes);
-  * decode, the reference's own 12 parity cases (K with a 3-sigma per-channel offset, q x 2): the reference's bar,
-    rel < 1e-2 against its independent check (tests/test_parity.py:104), and at least as close to the exact attention
-    over the quantized cache as torch_decode itself is. On those inputs torch_decode's two bf16 roundings of K move
-    it ~4e-3 mean-abs from the exact result; the HIP kernels do not round the dequantized K and land closer."""
+  * decode, every input (the BASELINE configs' N(0, 1) q / K / V, the reference's own 12 parity cases with K offset
+    per channel by 3 N(0, 1) and q x 2, ragged batches, fp8 range edges): within 2e-2 max-abs and 1e-3 mean-abs of the
+    oracle's restatement of torch_decode.py (both bf16 outputs, same cache bytes), and for the 12 parity cases also the
+    reference's own bar, rel < 1e-2 against its independent check (tests/test_parity.py:104)."""
 import hashlib
 import os
 
@@ -233,15 +231,7 @@ def test_decode_reference_cases(hip, oracle, win, n):
     rel = np.linalg.norm(o - ref) / np.linalg.norm(ref)
     say(f"win={win} n={n}: rel {rel:.2e} vs the independent check")
     assert rel < 1e-2
-    if win or n < 384:                      # no quantized sub-block read: the exact path matches torch_decode closely
-        close(ob, want, f"win={win} n={n} vs oracle")
-        return
-    exact = oracle.reference_f64(q, K, V, cos, sin, window=win, round_k=False)
-    w = oracle.bf16_to_f32(want).astype(np.float64)
-    dh, dt = np.abs(o - exact), np.abs(w - exact)
-    say(f"win={win} n={n}: vs exact: hip max {dh.max():.3e} mean {dh.mean():.3e} | torch_decode max {dt.max():.3e} "
-        f"mean {dt.mean():.3e} | hip vs torch_decode mean {np.abs(o - w).mean():.3e}")
-    assert dh.mean() <= 1.25 * dt.mean() and dh.max() <= max(MAX_ABS, dt.max())
+    close(ob, want, f"win={win} n={n} vs oracle")
 
 
 @pytest.mark.parametrize("B,n", [(4, 1024), (2, 384), (3, 5000), (1, 9000)])
