@@ -522,31 +522,39 @@ __device__ __forceinline__ void rope4(const uint32_t (&k)[4], const uint32_t (&c
       : "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(cs[0]), "v"(cs[1]), "v"(cs[2]), "v"(cs[3]), "v"(sw[0]),
         "v"(sw[1]), "v"(sw[2]), "v"(sw[3]));
 }
+// (a & m) | (b & ~m) as one v_bfi_b32
+__device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ b8 pack8b(const uint32_t (&x)[4]) { return as_b8(u4v{x[0], x[1], x[2], x[3]}); }
 
-// The K scale bytes table t needs: klo / ksc of its two dims (kind 0: dims j, j + 64; kind 1: j + 32, j + 96), head h.
-__device__ __forceinline__ uint32_t table_bytes(const uint8_t* __restrict__ sb, int t) {
+// The K scale bytes table t needs: klo / ksc of its two dims (kind 0: dims j, j + 64; kind 1: j + 32, j + 96), head h,
+// as four separate loads (combined only when the table is built, a sub-block after they are issued).
+struct TabBytes { uint32_t la, lb, sa, sb; };
+__device__ __forceinline__ TabBytes table_bytes(const uint8_t* __restrict__ sb, int t) {
   const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31;
   const uint8_t* p = sb + KLO_O + 128 * h + 32 * kind + j;
-  return (uint32_t)p[0] | ((uint32_t)p[64] << 8) | ((uint32_t)p[KSC_O - KLO_O] << 16) |
-         ((uint32_t)p[KSC_O - KLO_O + 64] << 24);
+  return TabBytes{p[0], p[64], p[KSC_O - KLO_O], p[KSC_O - KLO_O + 64]};
 }
 // Table t of one LUT buffer: entry (ca, cb) = bf16(ca ksc_a + klo_a) | bf16(cb ksc_b + klo_b) << 16 (kv800.py:84-86:
-// the product is exact in fp32, so the fused multiply-add rounds where torch's add does). Block ((kind 4 + h) 2 + d)
-// 4 + g holds the tables of channels 8 g + 4 d + e, e < 4; table e's entry (ca, cb) at dword ca + 16 cb + 4 ((e + g) % 4),
-// so the four lane groups' tables of one lookup occupy disjoint banks.
-__device__ __forceinline__ void lut_build(uint32_t* lut, int t, uint32_t bytes) {
+// the product is exact in fp32, so the fused multiply-add rounds where torch's add does). The tables of channels
+// 8 g + 4 d + e, e < 4, fill the 256-byte block ((kind 4 + h) 2 + d) 4 + g, table e in its 64-byte slot e ^ (g & 1),
+// entry (ca, cb) at dword ca + 4 cb of the slot: the 32 lanes of a half-wave read two lane groups' tables, whose 16
+// entries each occupy one half of the 32 LDS banks.
+__device__ __forceinline__ void lut_build(uint32_t* lut, int t, const TabBytes& tb) {
   float v[4];
-  f8x4(bytes, v);   // klo_a, klo_b, ksc_a, ksc_b
+  f8x4(tb.la | (tb.lb << 8) | (tb.sa << 16) | (tb.sb << 24), v);   // klo_a, klo_b, ksc_a, ksc_b
   const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31, g = j >> 3, d = (j >> 2) & 1, e = j & 3;
   uint32_t pa[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
-  uint32_t* blk = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 4 * ((e + g) & 3);
+  uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 16 * (e ^ (g & 1));
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
     const uint32_t hi = pa[cb] & 0xFFFF0000u;
-    *reinterpret_cast<u4v*>(blk + 16 * cb) =
+    *reinterpret_cast<u4v*>(tab + 4 * cb) =
         u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
   }
 }
@@ -642,19 +650,14 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       bq[2 + d] = pack8b(p);
     }
   }
-  // byte e of cg: 16 ((e + g) % 4), the table rotation of lane group g
-  const uint32_t cg = (uint32_t)(16 * ((0 + g) & 3)) | ((uint32_t)(16 * ((1 + g) & 3)) << 8) |
-                      ((uint32_t)(16 * ((2 + g) & 3)) << 16) | ((uint32_t)(16 * ((3 + g) & 3)) << 24);
+  // byte e of cg: 64 (e ^ (g & 1)), the slot of channel e's table in lane group g's block
+  const uint32_t cg = (g & 1) ? 0x80C00040u : 0xC0804000u;
 
   float m = NEG_BIG, lsum = 0.f, lvs = 0.f;
   f4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  auto sub_base = [&](int jb) -> int64_t {
-    const int64_t base = boff[(int64_t)b * bstride + jb];
-    return (base < 0 || base > qpool_bytes - SUB || (int64_t)(jb + 1) * BLK > rope_rows) ? -1 : base;
-  };
   auto stage_scales = [&](uint32_t x) {
     float v[4];
     f8x4(x, v);
@@ -670,31 +673,65 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       W.vb[32 * (h0 + 1) + s] = C.vb[1];
       asm volatile("" ::: "memory");
     }
-    float sv[2][4];
+    // QK in 8 steps (head h, kc dword d), both tiles per step; each step's table reads are issued one step ahead
+    u4v sw[2][2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      u4v sw[2];
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int d = 0; d < 2; ++d)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sw[d][e] = __builtin_amdgcn_alignbit(C.cs[u][d][e], C.cs[u][d][e], 16);   // (sin, cos)
-      const f4 a0 = qk_head<0>(lutc, C.kc[u][0], C.cs[u], sw, gw, cg, bq);
-      const f4 a1 = qk_head<1>(lutc, C.kc[u][1], C.cs[u], sw, gw, cg, bq);
-      const f4 a2 = qk_head<2>(lutc, C.kc[u][2], C.cs[u], sw, gw, cg, bq);
-      const f4 a3 = qk_head<3>(lutc, C.kc[u][3], C.cs[u], sw, gw, cg, bq);
+        for (int e = 0; e < 4; ++e) sw[u][d][e] = __builtin_amdgcn_alignbit(C.cs[u][d][e], C.cs[u][d][e], 16);
+    f4 qa[2][4];
+    uint32_t kk[2][2][4], an[2][2][4];   // [step parity][tile][e]
+    auto lookup = [&](const int st, const int pb) {
+      const int h = st >> 1, d = st & 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = (hn & 2) ? ((hn & 1) ? a3[i] : a2[i]) : ((hn & 1) ? a1[i] : a0[i]);
-        sv[u][i] = x * scale;
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t x = d ? C.kc[u][h].y : C.kc[u][h].x;
+        // byte e: 4 ca + 16 cb + 64 slot, the entry's byte offset in the block (rope: ca = c0, cb = c2; nope: c1, c3)
+        const uint32_t R = bfi32(0x0C0C0C0Cu, x << 2, (x & 0x30303030u) | cg);
+        const uint32_t N = bfi32(0x0C0C0C0Cu, x, ((x >> 2) & 0x30303030u) | cg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sel = 0x0C0C0104u + (uint32_t)e;
+          const uint32_t ra = __builtin_amdgcn_perm(R, gw, sel), na = __builtin_amdgcn_perm(N, gw, sel);
+          kk[pb][u][e] = *reinterpret_cast<const uint32_t*>(lutc + ra + 1024 * (h * 2 + d));
+          an[pb][u][e] = *reinterpret_cast<const uint32_t*>(lutc + na + 1024 * ((4 + h) * 2 + d));
+        }
+      }
+    };
+    lookup(0, 0);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      if (st + 1 < 8) lookup(st + 1, (st + 1) & 1);
+      const int h = st >> 1, d = st & 1, pb = st & 1;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t c4[4], s4[4], ar[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { c4[e] = C.cs[u][d][e]; s4[e] = sw[u][d][e]; }
+        rope4(kk[pb][u], c4, s4, ar);
+        const f4 z = (d == 0) ? f4{0.f, 0.f, 0.f, 0.f} : qa[u][h];
+        qa[u][h] = mfma_bf(pack8b(ar), bq[d], z);
+        qa[u][h] = mfma_bf(pack8b(an[pb][u]), bq[2 + d], qa[u][h]);
       }
     }
+    float sv[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = (hn & 2) ? ((hn & 1) ? qa[u][3][i] : qa[u][2][i]) : ((hn & 1) ? qa[u][1][i] : qa[u][0][i]);
+        sv[u][i] = x * scale;
+      }
     // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
     float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                        fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
     tmax = max4rows(tmax);
-    if (__any(tmax > m + QLAZY)) {
-      const float mn = fmaxf(m, tmax);
-      const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
+    {   // lazy running max without a branch: al = 1 unless a chunk max exceeds m by more than QLAZY
+      const bool up = __any(tmax > m + QLAZY);
+      const float mn = up ? fmaxf(m, tmax) : m;
+      const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; exp2(0) = 1, tiny results flush to 0
       m = mn; lsum *= al; lvs *= al;
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] *= al;
@@ -731,7 +768,12 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   };
 
   if (j0 < j1) {
-    int64_t base = sub_base(j0);
+    const int64_t* brow = boff + (int64_t)b * bstride;
+    auto sanitize = [&](int64_t raw, int jb) -> int64_t {
+      return (raw < 0 || raw > qpool_bytes - SUB || (int64_t)(jb + 1) * BLK > rope_rows) ? -1 : raw;
+    };
+    int64_t base = sanitize(brow[j0], j0);
+    int64_t nraw = brow[min(j0 + 1, j1 - 1)];   // the next sub-block's offset, loaded one sub-block ahead of its use
     const uint8_t* sb = qpool + (base < 0 ? 0 : base);
     QChunk C0, C1;
     qload(C0, sb, cs2 + (int64_t)(base < 0 ? 0 : j0) * BLK * 32, 64 * w, lane);
@@ -741,14 +783,16 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     uint32_t buf = 0;
     for (int jb = j0; jb < j1; ++jb) {
       const bool more = jb + 1 < j1;
-      const int64_t nbase = more ? sub_base(jb + 1) : -1;
+      const int64_t nbase = more ? sanitize(nraw, jb + 1) : -1;
+      nraw = brow[min(jb + 2, j1 - 1)];
       const uint8_t* nsb = qpool + (nbase < 0 ? 0 : nbase);
-      uint32_t ntb = 0, nsc = 0;
-      if (more) { ntb = table_bytes(nsb, tid); nsc = scale_bytes(nsb, 64 * w + lane); }
+      // the next sub-block's scale bytes (read unconditionally; used after this sub-block's chunks)
+      const TabBytes ntb = table_bytes(nsb, tid);
+      const uint32_t nsc = scale_bytes(nsb, 64 * w + lane);
       const uint32_t gw = ((buf << 6) | (uint32_t)g) << 8;   // byte 1: LUT buffer and lane group (256-byte blocks)
       qload(C1, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * w + 32, lane);
       if (base >= 0) chunk(C0, 0, gw);
-      if (more) qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : jb + 1) * BLK * 32, 64 * w, lane);
+      qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : jb + 1) * BLK * 32, 64 * w, lane);
       if (base >= 0) chunk(C1, 1, gw);
       if (more) {
         lut_build(L.lut[buf ^ 1u], tid, ntb);
