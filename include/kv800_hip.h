@@ -196,6 +196,18 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
                            int64_t epool_elems, int64_t sink_elems, uint16_t* out, void* workspace,
                            int64_t workspace_bytes, int64_t spb, void* stream);
 
+/* kv800_hip_decode_sized without a workspace argument and without any allocation: the partials (and the rope pair table
+ * when cs2 is NULL) go to a static per-device scratch of 32 MiB inside the library, resolved with hipGetSymbolAddress on
+ * the first call on each device. No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Limit: a call whose schedule
+ * needs more than 32 MiB (kv800_hip_decode_workspace / _balanced) is rejected with KV800_EINVAL. Every call on one device
+ * shares that device's scratch: calls that overlap on one device (concurrent streams or threads) race. The stream must
+ * belong to the current device. Nothing in the scratch has to start at zero (every slot a kernel reads is written by
+ * the same call). */
+int kv800_hip_decode_noalloc(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                             const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs2, int64_t qpool_bytes,
+                             int64_t epool_elems, int64_t sink_elems, uint16_t* out, int64_t spb, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

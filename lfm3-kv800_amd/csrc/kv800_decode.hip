@@ -21,6 +21,8 @@
 //   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT (staged path).
 #include <math.h>
 
+#include <mutex>
+
 #include "kv800_common.h"
 #include "../../include/kv800_hip.h"
 
@@ -1302,3 +1304,72 @@ int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free decode
+// Scratch of kv800_hip_decode_noalloc: the decode's split partials (m, l, acc), the balanced schedule's row offsets and,
+// without a prebuilt pair table, the rope pair table live here instead of in a caller workspace. Every device the
+// library runs on holds its own copy until the process ends. In host code `scratch` names a host-side stand-in: its
+// device address is resolved per device with hipGetSymbolAddress and only that address is handed to the kernels.
+static constexpr int64_t KV800_SCRATCH_BYTES = 32ll << 20;
+static __device__ __align__(256) char scratch[KV800_SCRATCH_BYTES];
+
+namespace {
+constexpr int KV800_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[KV800_MAX_DEVICES];   // device address of `scratch` on each device, resolved on its first call
+}  // namespace
+
+extern "C" int kv800_hip_decode_noalloc(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
+                                        const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs2,
+                                        int64_t qpool_bytes, int64_t epool_elems, int64_t sink_elems, uint16_t* out,
+                                        int64_t spb, void* stream) {
+  KV800_REQUIRE(P && B >= 0, "decode_noalloc: bad arguments");
+  if (B == 0) return KV800_OK;
+  // bytes this call's schedule needs (the same carving as kv800_hip_decode's workspace)
+  const int64_t nqmax = P->win ? 0 : P->nqmax;
+  KV800_REQUIRE(nqmax >= 0, "decode_noalloc: nqmax < 0");
+  int64_t need;
+  if (!nqmax) {
+    need = kv800_hip_decode_workspace(B, 0, 0);
+  } else if (spb > 0) {
+    need = kv800_hip_decode_workspace(B, (nqmax + spb - 1) / spb, cs2 ? 0 : nqmax * BLK);
+  } else {
+    int64_t G = -spb;
+    int rc;
+    if (!G && (rc = kv800_hip_plan_balanced(B, nqmax, &G)) != KV800_OK) return rc;
+    need = kv800_hip_decode_workspace_balanced(B, G, cs2 ? 0 : nqmax * BLK);
+  }
+  KV800_REQUIRE(need <= KV800_SCRATCH_BYTES,
+                "decode_noalloc: this call needs %lld bytes of scratch, the per-device scratch holds %lld (pass a "
+                "prebuilt cs2 table, or decode fewer rows / groups per call)",
+                (long long)need, (long long)KV800_SCRATCH_BYTES);
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= KV800_MAX_DEVICES) {
+    kv800::set_error("decode_noalloc: hipGetDevice: %s (device %d)", hipGetErrorString(e), dev);
+    return KV800_EHIP;
+  }
+  if (stream) {   // the scratch address is the current device's: the stream must run there
+    int sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    KV800_REQUIRE(e == hipSuccess && sdev == dev, "decode_noalloc: the stream is not on the current device (%d vs %d)",
+                  sdev, dev);
+  }
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        kv800::set_error("decode_noalloc: hipGetSymbolAddress of the scratch on device %d: %s", dev,
+                         hipGetErrorString(e));
+        return KV800_EHIP;
+      }
+      g_scratch_ptr[dev] = p;
+    }
+    ws = g_scratch_ptr[dev];
+  }
+  return kv800_hip_decode_sized(P, q, B, cos_t, sin_t, rope_rows, cs2, qpool_bytes, epool_elems, sink_elems, out, ws,
+                                KV800_SCRATCH_BYTES, spb, stream);
+}

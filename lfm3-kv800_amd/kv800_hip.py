@@ -69,6 +69,8 @@ SIGNATURES = {
     "kv800_hip_flush_latency": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP,
                                        _I64, _I64, _VP]),
     "kv800_hip_fake_quant_v": (_I32, [_VP, _I64, _VP, _VP]),
+    "kv800_hip_decode_noalloc": (_I32, [ctypes.POINTER(Paged), _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _VP,
+                                        _I64, _VP]),
 }
 
 
