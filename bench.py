@@ -3,15 +3,16 @@ over 64 sequences x 32,768 tokens (127 quantized 256-token sub-blocks + 256 exac
 tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape; same bytes and flops per token as
 32 / 8 / 64).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--calib]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--e2e-only] [--e2e-steps S] [--calib]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
 JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
 duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
 cpu_baseline: the CPU oracle (a C restatement of torch_decode.py) on a bounded sample of the same workload. Extra
-fields: flush_c2 (the flush kernel alone) and c4 (config 4, one decode step of all 6 attention
-layers over 398 ragged sequences). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
+fields: flush_c2 (the flush kernel alone), c4 (config 4, one decode step of all 6 attention
+layers over 398 ragged sequences) and e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
+sequences). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
 import argparse
 import json
 import os
@@ -198,6 +199,52 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
             "gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+E2E_R, E2E_MIN, E2E_MAX = 256, 1024, 32768
+
+
+def bench_e2e(torch, dev, steps, seed=51):
+    """greedy decode of a random-init LFM3-1.7B-shaped model (lfm3-kv800_amd/model.py: 24 layers,
+    13 short-conv, 6 full-attention on the 800h caches, 5 sliding-window; weights N(0, 0.02) bf16) over 256 sequences
+    with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps. tok/s = c (steps - 1) / time, time from the end of
+    the first step to the end of the last (the reference's decode tok/s, RESULTS_RELEASE.md:83-85). The prompts' K / V
+    histories are synthetic N(0, 1), written into the caches (quantized by the HIP quantizer) before the first step:
+    prompt processing is not part of the measurement."""
+    import numpy as np
+    from lfm3_kv800_amd import model as M
+    cfg = M.Lfm3Config()
+    L0 = np.random.RandomState(seed).randint(E2E_MIN, E2E_MAX + 1, size=E2E_R).astype(np.int64)
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def history(l, r, p0, p1):
+        shape = (p1 - p0, 4, 128)
+        return (torch.randn(shape, generator=g, device=dev).to(torch.bfloat16),
+                torch.randn(shape, generator=g, device=dev).to(torch.bfloat16))
+
+    t = time.perf_counter()
+    attn = M.PagedAttention800(L0.tolist(), steps + 1, dev, seed=seed)
+    attn.fill(history)
+    model = M.Lfm3Decoder(cfg, attn, E2E_R, dev, seed=seed)
+    model.randomize_conv_states(seed)
+    tokens = torch.randint(0, cfg.vocab, (E2E_R,), generator=g, device=dev)
+    torch.cuda.synchronize()
+    log(f"e2e: caches of {E2E_R} prompts ({int(L0.sum())} tokens) and weights ready in {time.perf_counter() - t:.1f} s")
+    tokens = model.step(tokens, attn.begin_step()).argmax(-1)        # first step: outside the measured window
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps - 1):
+        tokens = model.step(tokens, attn.begin_step()).argmax(-1)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    assert bool(((tokens >= 0) & (tokens < cfg.vocab)).all())
+    ctx = L0 + steps
+    return {"workload": f"C5: greedy decode, random-init LFM3-1.7B-shaped model (hidden 2048, 24 layers: 13 conv, "
+                        f"6 full attention on 800h caches, 5 sliding 256; vocab {cfg.vocab}, ffn {cfg.ffn}), "
+                        f"{E2E_R} seqs, prompts U[1K, 32K], {steps} steps",
+            "data": "synthetic N(0,1) K/V prompt histories, random token ids",
+            "tok_s": round(E2E_R * (steps - 1) / dt, 1), "ms_per_step": round(dt * 1e3 / (steps - 1), 3),
+            "steps": steps, "seqs": E2E_R, "context_tokens_end": int(ctx.sum())}
+
+
 def rope_tables(torch, n, dev):
     """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
     inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
@@ -239,7 +286,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
-    ap.add_argument("--c3-only", action="store_true", help="skip the C2 / C4 workloads (counter passes of the C3 kernel)")
+    ap.add_argument("--c3-only", action="store_true", help="skip the C2 / C4 / C5 workloads (counter passes of the C3 kernel)")
+    ap.add_argument("--e2e-only", action="store_true", help="only the C5 decode loop; prints its record")
+    ap.add_argument("--e2e-steps", type=int, default=128)
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the 800h path shards by "
@@ -250,6 +299,10 @@ def main():
     kh.ops()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+
+    if a.e2e_only:
+        print(json.dumps({"e2e": bench_e2e(torch, dev, a.e2e_steps)}), flush=True)
+        return
 
     if a.calib:
         x = torch.empty(1 << 28, dtype=torch.int32, device=dev)      # 1 GiB
@@ -338,11 +391,14 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = c4 = None
+    flush_c2 = c4 = e2e = None
     if not a.c3_only:
         flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
         cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
         c4 = bench_c4(torch, kh, dev, extra_steps, 3, cos4, sin4)
+        del cos4, sin4
+        torch.cuda.empty_cache()
+        e2e = bench_e2e(torch, dev, a.e2e_steps)
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -359,6 +415,7 @@ def main():
         "cpu_baseline": cpu,
         "flush_c2": flush_c2,
         "c4": c4,
+        "e2e": e2e,
     }
     print(json.dumps(res), flush=True)
 

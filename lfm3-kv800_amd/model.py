@@ -1,0 +1,267 @@
+"""Decode loop of an LFM3-1.7B-shaped model whose attention layers run on the 800h path, without
+vLLM.
+
+The layer stack follows the reference's vLLM model (vllm_model.py:542-653) and its attention routing with
+LFM3_KV800=1 (vllm_model.py:268-304): 24 layers of width 2048, each `h += post_norm(op(norm(h)))` then
+`h += post_ffn_norm(ffn(ffn_norm(h)))` (sandwich norms, vllm_model.py:446-471), then a final norm and the tied LM head.
+  * 13 gated short-conv layers (width 7, vllm_model.py:327-431): in_proj -> B, C, x; y = C * conv(B * x); out_proj.
+  * 6 full-attention layers, 16 query / 4 KV heads of 128, QK RMSNorm per head, RoPE theta 1e6 on 32 of the 64
+    frequencies (zero tail), per-head sigmoid output gate (vllm_model.py:195-304): quantized 6, 10, 14, 22 and window +
+    sinks 2, 18 on the 800h caches (vllm_cache.KV800DecodeLayer), keys handed over before RoPE.
+  * 5 native sliding layers 4, 8, 12, 16, 20 (RoPE theta 1e4 on all frequencies, window 256) on exact window caches
+    (vllm_cache.KV800SlideLayer), keys handed over after RoPE.
+The vocabulary and feed-forward sizes are not in the reference (its weights are not available offline): 65,536 and
+8,192 here, about 1.67 B parameters. Weights are random N(0, 0.02) in bf16, norm weights 1.
+
+Attention goes through an object with begin_step(seq_lens_cpu) and attend(layer, q, k_pre, k_post, v) -> (R, 16, 128):
+PagedAttention800 (below) keeps vLLM's page geometry and runs every layer on libkv800_hip.so; tests substitute an
+oracle implementation to check the logits."""
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import kv800, kv800_hip
+from . import vllm_cache as vc
+
+CONV, FULL, SLIDE = "conv", "full", "slide"
+EXACT_GROUPS = {"A": (2, 10, 18), "B": (6, 14, 22)}       # exact KV groups of the full layers (sliding window 640)
+SLIDE_GROUPS = {"C": (4, 12, 20), "D": (8, 16)}           # KV groups of the native sliding layers (window 256)
+
+
+@dataclass
+class Lfm3Config:
+    hidden: int = 2048
+    heads: int = 16
+    kv_heads: int = 4
+    head_dim: int = 128
+    ffn: int = 8192
+    vocab: int = 65536
+    layers: int = 24
+    conv_len: int = 7
+    window: int = 256
+    eps: float = 1e-5
+
+    def layer_type(self, l):
+        if l in vc.QUANT_LAYERS or l in vc.WINDOW_LAYERS:
+            return FULL
+        if l in vc.SLIDE_LAYERS:
+            return SLIDE
+        return CONV
+
+
+def rms_norm(x, w, eps):
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), -1)
+
+
+class Rope:
+    """Neox RoPE over head_dim 128 as the reference computes it (vllm_model.py:106-151): angles in fp32, cos / sin rounded
+    to bf16, q / k rotated in fp32 and cast back. Full layers rotate 32 of the 64 frequencies (the rest are 0)."""
+
+    def __init__(self, theta, angles, device):
+        inv = 1.0 / (theta ** (torch.arange(0, 2 * angles, 2, dtype=torch.float32) / 128))
+        self.inv = torch.cat((inv, torch.zeros(64 - angles))).to(device)
+
+    def __call__(self, pos, *xs):
+        fr = pos.to(torch.float32)[:, None] * self.inv[None]
+        emb = torch.cat((fr, fr), -1)
+        c = emb.cos().to(torch.bfloat16).float()[:, None]
+        s = emb.sin().to(torch.bfloat16).float()[:, None]
+        return tuple((x.float() * c + _rotate_half(x.float()) * s).to(x.dtype) for x in xs)
+
+
+def kernel_tables(n, device):
+    """(cos, sin) (n, 32) bf16 of the full layers' 32 rotating frequencies, the tables the decode kernels read
+    (vllm_attn.py:147-159)."""
+    inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
+    fr = torch.arange(n, dtype=torch.float32)[:, None] * inv[None]
+    return fr.cos().to(torch.bfloat16).to(device), fr.sin().to(torch.bfloat16).to(device)
+
+
+class Lfm3Decoder:
+    """Random-init LFM3-shaped model for batched decode: step(tokens) appends one token to every row and returns the
+    logits. conv_state: per conv layer (R, hidden, conv_len - 1) bf16."""
+
+    def __init__(self, cfg: Lfm3Config, attention, rows, device, seed=0):
+        self.cfg, self.attn, self.R, self.dev = cfg, attention, rows, device
+        g = torch.Generator(device=device).manual_seed(seed)
+        H, D, G = cfg.hidden, cfg.head_dim, cfg.heads
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=device) * 0.02).to(torch.bfloat16)
+
+        ones = lambda n: torch.ones(n, dtype=torch.bfloat16, device=device)
+        self.embed = w(cfg.vocab, H)
+        self.final_norm = ones(H)
+        self.layers = []
+        for l in range(cfg.layers):
+            t = cfg.layer_type(l)
+            L = {"type": t, "norm": ones(H), "post_norm": ones(H), "ffn_norm": ones(H), "post_ffn_norm": ones(H),
+                 "w13": w(2 * cfg.ffn, H), "w2": w(H, cfg.ffn)}
+            if t == CONV:
+                L.update(in_proj=w(3 * H, H), conv=w(H, cfg.conv_len), out_proj=w(H, H),
+                         state=torch.zeros(rows, H, cfg.conv_len - 1, dtype=torch.bfloat16, device=device))
+            else:
+                L.update(qkv=w((G + 2 * cfg.kv_heads) * D, H), q_norm=ones(D), k_norm=ones(D), gate=w(G, H),
+                         o_proj=w(H, G * D), rope=Rope(1e6, 32, device) if t == FULL else Rope(1e4, 64, device))
+            self.layers.append(L)
+
+    def randomize_conv_states(self, seed):
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        for L in self.layers:
+            if L["type"] == CONV:
+                L["state"].copy_(torch.randn(L["state"].shape, generator=g, device=self.dev) * 0.1)
+
+    def _conv(self, L, h):
+        B_, C_, x = F.linear(h, L["in_proj"]).chunk(3, -1)
+        win = torch.cat((L["state"], (B_ * x).unsqueeze(-1)), -1)                 # (R, hidden, conv_len)
+        y = (win * L["conv"]).sum(-1)
+        L["state"].copy_(win[..., 1:])
+        return F.linear(C_ * y, L["out_proj"])
+
+    def _attention(self, l, L, h, pos):
+        cfg = self.cfg
+        R, G, KV, D = h.shape[0], cfg.heads, cfg.kv_heads, cfg.head_dim
+        q, k, v = F.linear(h, L["qkv"]).split([G * D, KV * D, KV * D], -1)
+        q = rms_norm(q.reshape(R, G, D), L["q_norm"], cfg.eps)
+        k = rms_norm(k.reshape(R, KV, D), L["k_norm"], cfg.eps)
+        qr, kr = L["rope"](pos, q, k)
+        o = self.attn.attend(l, qr.contiguous(), k.contiguous(), kr.contiguous(), v.reshape(R, KV, D).contiguous())
+        o = o * torch.sigmoid(F.linear(h, L["gate"]).float()).to(o.dtype).unsqueeze(-1)
+        return F.linear(o.reshape(R, G * D), L["o_proj"])
+
+    def step(self, tokens, pos):
+        """tokens (R,) int64, pos (R,) int64 the new tokens' positions (device); the attention object's begin_step
+        has been called with the rows' lengths including this token. Returns (R, vocab) fp32 logits."""
+        cfg = self.cfg
+        x = self.embed[tokens]
+        for l, L in enumerate(self.layers):
+            h = rms_norm(x, L["norm"], cfg.eps)
+            h = self._conv(L, h) if L["type"] == CONV else self._attention(l, L, h, pos)
+            x = x + rms_norm(h, L["post_norm"], cfg.eps)
+            h = F.linear(rms_norm(x, L["ffn_norm"], cfg.eps), L["w13"])
+            gte, up = h.chunk(2, -1)
+            x = x + rms_norm(F.linear(F.silu(gte) * up, L["w2"]), L["post_ffn_norm"], cfg.eps)
+        return F.linear(rms_norm(x, self.final_norm, cfg.eps), self.embed).float()
+
+
+class PagedAttention800:
+    """The model's 11 attention layers on libkv800_hip.so with vLLM's page geometry: one quant KV group (1280-token
+    pages of 262,144 B) for layers 6, 10, 14, 22; exact KV groups A (2, 10, 18) and B (6, 14, 22) of ebs-token pages
+    holding each row's last positions (window 640); sliding KV groups C (4, 12, 20) and D (8, 16) (window 256). Pages
+    are given to rows through shuffled block tables; only the positions a row can still read get a page of their own,
+    the rest of its logical pages point at a shared spare page that is never read.
+
+    lens0: the rows' history lengths; steps: decode steps to provide for."""
+
+    def __init__(self, lens0, steps, device, ebs=128, seed=0):
+        self.dev, self.ebs = device, ebs
+        self.lens = torch.tensor([int(x) for x in lens0], dtype=torch.int64)
+        R = self.R = len(lens0)
+        nmax = int(self.lens.max()) + steps + 1
+        self.cos, self.sin = kernel_tables(nmax + 64, device)
+        rng = torch.Generator().manual_seed(seed)
+        lp = nmax // ebs + 1                                                   # logical exact pages per row
+
+        def table(first_pos):
+            """block table (R, lp) int32 with unique shuffled pages for logical pages >= first_pos // ebs, page 0 spare."""
+            need = [lp - int(f) // ebs for f in first_pos]
+            perm = (torch.randperm(sum(need), generator=rng) + 1).tolist()
+            bt = torch.zeros(R, lp, dtype=torch.int32)
+            c = 0
+            for r in range(R):
+                f = int(first_pos[r]) // ebs
+                bt[r, f:] = torch.tensor(perm[c:c + need[r]], dtype=torch.int32)
+                c += need[r]
+            return bt.to(device), sum(need) + 1
+
+        nq0 = torch.clamp(self.lens - kv800.LAG, min=0) // kv800.BLK
+        self.bt, npages = {}, {}
+        for grp in EXACT_GROUPS:
+            # quantized layers read exact positions >= 256 NQ, window layers >= n - 256: both >= n - 384
+            self.bt[grp], npages[grp] = table(torch.minimum(nq0 * kv800.BLK, torch.clamp(self.lens - 256, min=0)))
+        for grp in SLIDE_GROUPS:
+            self.bt[grp], npages[grp] = table(torch.clamp(self.lens - 256, min=0))
+        qlp = nmax // vc.QBLOCK + 1
+        self.qbt = (torch.randperm(R * qlp, generator=rng).view(R, qlp).to(torch.int32)).to(device)
+        self.group_of = {l: g for g, ls in {**EXACT_GROUPS, **SLIDE_GROUPS}.items() for l in ls}
+        self.layers = {}
+        for l in (2, 6, 10, 14, 18, 22):
+            ev = torch.zeros(npages[self.group_of[l]], 4, ebs, 256, dtype=torch.bfloat16, device=device)
+            qv = None if l in vc.WINDOW_LAYERS else torch.zeros(R * qlp, vc.QPAGE, dtype=torch.uint8, device=device)
+            self.layers[l] = vc.KV800DecodeLayer(l, ev, qv)
+        for l in vc.SLIDE_LAYERS:
+            ev = torch.zeros(npages[self.group_of[l]], 4, ebs, 256, dtype=torch.bfloat16, device=device)
+            self.layers[l] = vc.KV800SlideLayer(l, ev)
+        self.metas = None
+
+    # ---- prompt history
+    def fill(self, history):
+        """Write every row's history into the caches. history(l, r, p0, p1) -> (K, V) (p1 - p0, 4, 128) bf16 on the
+        device: pre-RoPE K for full layers, post-RoPE K for sliding layers. Quant layers get sub-blocks j < NQ(n)
+        quantized by the HIP quantizer and the positions from 256 NQ(n) on in exact pages; window layers the positions
+        from n - 256 on and their sinks (positions < 4) in the hosts' aux areas; sliding layers the last 256 positions."""
+        ebs, per_page = self.ebs, vc.QBLOCK // kv800.BLK
+        for l, layer in self.layers.items():
+            bt = self.bt[self.group_of[l]].cpu()
+            quant = l in vc.QUANT_LAYERS
+            # a quant page as its 5 sub-block slots (the aux area after them is not part of this view)
+            qslots = layer.qv[:, :vc.AUX_BYTES].view(-1, per_page, kv800.SUB) if quant else None
+            for r in range(self.R):
+                n = int(self.lens[r])
+                nq = max(0, n - kv800.LAG) // kv800.BLK
+                lo = nq * kv800.BLK if quant else max(0, n - 256)
+                if quant and nq:
+                    K, V = history(l, r, 0, nq * kv800.BLK)
+                    sb = kv800_hip.quantize_blocks(K.view(nq, kv800.BLK, 4, 128), V.view(nq, kv800.BLK, 4, 128))
+                    j = torch.arange(nq, device=self.dev)
+                    qslots[self.qbt[r, j // per_page].long(), j % per_page] = sb
+                if n > lo:
+                    K, V = history(l, r, lo, n)
+                    pos = torch.arange(lo, n)
+                    pages = bt[r, pos // ebs].long().to(self.dev)
+                    slots = (pos % ebs).to(self.dev)
+                    layer.ev[pages, :, slots, :128] = K
+                    layer.ev[pages, :, slots, 128:] = V
+                if l in vc.WINDOW_LAYERS and n > 0:
+                    K, V = history(l, r, 0, min(kv800.NSINK, n))
+                    page0 = int(self.qbt[r, 0])
+                    for src, host in zip((K, V), vc.SINK_HOST[l]):
+                        aux = self.layers[host].qv[page0, vc.AUX_BYTES:].view(torch.bfloat16)
+                        aux[:src.numel()] = src.reshape(-1)
+
+    # ---- decode steps
+    def begin_step(self):
+        """Metadata of the next decode step (every row appends one token) and the start of its flushes."""
+        self.lens += 1
+        dl = vc.step_lens(self.lens, self.dev)
+        me = {g: vc.step_meta(self.bt[g], self.lens, self.ebs, self.dev, dl) for g in self.bt}
+        mq = vc.step_meta(self.qbt, self.lens, vc.QBLOCK, self.dev, dl)
+        self.metas = (me, mq)
+        full = [self.layers[l] for l in (2, 6, 10, 14, 18, 22)]
+        vc.launch_flushes(full, {l.l: me[self.group_of[l.l]] for l in full}, mq)
+        return mq.positions
+
+    def attend(self, l, q, k_pre, k_post, v):
+        me, mq = self.metas
+        layer = self.layers[l]
+        if isinstance(layer, vc.KV800SlideLayer):
+            return layer.forward(q, k_post, v, me[self.group_of[l]])
+        return layer.forward(q, k_pre, v, me[self.group_of[l]], mq, hosts=self.layers, cos_t=self.cos, sin_t=self.sin)
+
+
+def decode_loop(model, attention, tokens, steps, sync_every=0):
+    """Greedy decode: `steps` steps from `tokens` (R,) int64; returns the (steps, R) generated tokens."""
+    out = []
+    for _ in range(steps):
+        pos = attention.begin_step()
+        logits = model.step(tokens, pos)
+        tokens = logits.argmax(-1)
+        out.append(tokens)
+    return torch.stack(out)

@@ -20,6 +20,7 @@ import torch
 from . import kv800, kv800_hip
 
 QUANT_LAYERS, WINDOW_LAYERS = (6, 10, 14, 22), (2, 18)
+SLIDE_LAYERS = (4, 8, 12, 16, 20)              # LFM3's native sliding-window layers (vllm_attn.py:217-222)
 SINK_HOST = {2: (6, 10), 18: (14, 22)}     # window layer -> (layer whose aux holds the sink K, ... the sink V)
 EXACT_WINDOW = 640
 QBLOCK, QPAGE = 1280, 262144
@@ -40,14 +41,24 @@ class StepMeta:
     cache: dict = field(default_factory=dict)
 
 
-def step_meta(block_table, seq_lens_cpu, ebs, device):
-    """StepMeta of a decode step in which every row appends one token at position seq_len - 1."""
+def step_lens(seq_lens_cpu, device):
+    """The rows' lengths on the device (int64). On a GPU the copy goes through freshly pinned host memory and does not
+    block the host, so the next step can be prepared while the GPU still runs this one."""
     sl = seq_lens_cpu.to(torch.int64)
-    pos = (sl - 1).to(device)
+    device = torch.device(device)
+    return sl.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else sl.to(device)
+
+
+def step_meta(block_table, seq_lens_cpu, ebs, device, seq_lens_dev=None):
+    """StepMeta of a decode step in which every row appends one token at position seq_len - 1. seq_lens_dev: the same
+    lengths already on the device (step_lens), shared by the KV groups of a step."""
+    sl = seq_lens_cpu.to(torch.int64)
+    dsl = step_lens(sl, device) if seq_lens_dev is None else seq_lens_dev
+    pos = dsl - 1
     bt = block_table.to(device=device, dtype=torch.int32)
     page = bt.gather(1, (pos // ebs)[:, None].long())[:, 0].long()
     slot = page * ebs + pos % ebs
-    return StepMeta(bt, slot, sl.to(device=device, dtype=torch.int32), sl, pos)
+    return StepMeta(bt, slot, dsl.to(torch.int32), sl, pos)
 
 
 class KV800DecodeLayer:
@@ -118,6 +129,47 @@ class KV800DecodeLayer:
         _, NQ, NP, qbt64, _, _ = _step_tables(mq)
         kv800_hip.flush(ev, self._eoff(mx), self.ebs, ev.stride(1), ev.stride(2), 128, self.qv, qbt64, QBLOCK, QPAGE, NP,
                         NQ, max_new, latency=True)
+
+
+class KV800SlideLayer:
+    """One LFM3 native sliding-window layer's decode step (vllm_attn.py:217-222, 253-254, 325-326 with slide=True):
+    window 256 without sinks, K stored after the layer's own RoPE (theta 1e4, all 64 frequencies) and read with the
+    identity tables, so the exact-window kernel only attends. exact: (pages, 4, ebs, 256) bf16 [K | V] of the layer's
+    own sliding KV group."""
+
+    def __init__(self, layer_idx, exact):
+        if exact.dtype != torch.bfloat16 or exact.dim() != 4 or exact.shape[1] != 4 or exact.shape[3] != 256:
+            raise ValueError("exact cache must be (pages, 4, ebs, 256) bf16")
+        self.l, self.ev, self.ebs = layer_idx, exact, exact.shape[2]
+        self.win = True
+        self._zeros = None
+        self._ident = None
+
+    def identity_tables(self, rows):
+        """(cos, sin) (rows, 32) bf16 of ones / zeros: the kernel's RoPE then leaves the stored keys as they are."""
+        if self._ident is None or self._ident[0].shape[0] < rows:
+            n = max(rows, 64)
+            self._ident = (torch.ones(n, 32, dtype=torch.bfloat16, device=self.ev.device),
+                           torch.zeros(n, 32, dtype=torch.bfloat16, device=self.ev.device))
+        return self._ident
+
+    def forward(self, q, k, v, mx: StepMeta):
+        """q (R, 16, 128) post-RoPE, k (R, 4, 128) POST-RoPE, v (R, 4, 128), bf16, one decode token per row;
+        mx: the layer's sliding-group metadata."""
+        ev, ebs = self.ev, self.ebs
+        R = q.shape[0]
+        key = ("eoff", ev.stride(0))
+        if key not in mx.cache:
+            mx.cache[key] = kv800_hip.page_offsets(mx.block_table, ev.stride(0))
+        eoff = mx.cache[key]
+        kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        if self._zeros is None or self._zeros.shape[0] < R:
+            self._zeros = torch.zeros(max(R, 64), dtype=torch.int32, device=ev.device)
+        cos1, sin0 = self.identity_tables(int(mx.seq_lens_cpu.max()) + 1)
+        P = kv800.Paged(qpool=ev, boff=eoff, epool=ev, eoff=eoff, ebs=ebs, e_hs=ev.stride(1), e_ts=ev.stride(2),
+                        e_v=128, sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens, NQ=self._zeros[:R], nqmax=0,
+                        win=kv800.WIN)
+        return kv800_hip.decode(P, q, cos1, sin0)
 
 
 def _step_tables(mq):
