@@ -148,6 +148,25 @@ int kv800_hip_history(const kv800_paged_t* P, int64_t R, int64_t max_n, const ui
                       int64_t rope_rows, int64_t qpool_bytes, int64_t epool_elems, const int64_t* out_off,
                       uint16_t* k_out, uint16_t* v_out, void* stream);
 
+/* Keys (S, 4, 128) bf16 rotated at positions pos (S,) int64 with the (rope_rows, 32) bf16 tables of the 32 rotating
+ * frequencies, replacing the reference's _rope over its 128-wide tables (vllm_attn.py:160-163): per element
+ * k * c + rot(k) * s in fp32 with c = 1, s = 0 on dims without a frequency, rounded to bf16 -- bit-identical. out may
+ * not alias k. Positions outside the table are clamped into it (a caller error that stays in bounds). */
+int kv800_hip_rope_rows(const uint16_t* k, const int64_t* pos, int64_t S, const uint16_t* cos_t,
+                        const uint16_t* sin_t, int64_t rope_rows, uint16_t* out, void* stream);
+
+/* Prefill / extend attention of R ragged rows, replacing the reference's prefill attention (vllm_attn.py:168-211 with
+ * the masks of 176-184): row r has queries q[qsl[r], qsl[r+1]) ((T, 16, 128) bf16, post-RoPE) at positions
+ * qpos0[r] + 0, 1, ... and keys / values K, V[ksl[r], ksl[r+1]) ((S, 4, 128) bf16, rotated as the layer stores them for
+ * attention) at positions kp (int32, ascending within a row); query head h reads KV head h / 4. A key is kept when
+ * kp <= the query's position and, with window > 0, kp > position - window or kp < nsink (nsink 4 for window + sinks
+ * layers, 0 for sliding layers; window 0 for quantized layers). Scale 128^-0.5, fp32 scores and softmax, bf16
+ * probabilities times bf16 V with fp32 accumulation, bf16 out (T, 16, 128). tile_off (R + 1, int64) is the prefix sum of
+ * ceil((qsl[r+1] - qsl[r]) / 16) (the rows' 16-query tiles), ntiles = tile_off[R]. */
+int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
+                      const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off, int64_t R,
+                      int64_t ntiles, int64_t window, int64_t nsink, uint16_t* out, void* stream);
+
 /* Step bookkeeping in vLLM's page geometry (exact page [4 heads, ebs, K128 | V128] bf16 with element strides s0 (page),
  * s1 (head), s2 (token); quant page = 5 x 51,200-byte sub-blocks per 1280 tokens, qs0 bytes apart). */
 

@@ -18,7 +18,6 @@ Backends: this package provides one, "hip" (ROCm torch, device type "cuda", gfx9
 "triton" and "torch" are recognised by LFM3KV_BACKEND / set_backend but are not part of this build: forcing one
 raises, as forcing an unavailable backend does in the reference (kv800.py:306-317). auto on a device the hip backend
 cannot serve raises too -- the product path never falls back to a CPU implementation."""
-import math
 import os
 
 import torch
@@ -92,121 +91,116 @@ class Paged:
 
 
 # ---------------------------------------------------------------- backend selection (kv800.py:251-359)
-_FORCED = None
-_CHOSEN = {}
-_VERIFIED = set()
-_LAST = [None]
+class _Selection:
+    """Decode-backend choice with the reference's controls: the LFM3KV_BACKEND environment variable (read at every
+    resolution) and set_backend() name a backend or 'auto'; the choice is made once per device type and remembered
+    until set_backend() is called again. This build serves one backend, 'hip', on ROCm devices (torch device type
+    'cuda'). The reference's own names are valid values but cannot be served, so forcing one raises RuntimeError, and
+    'auto' raises too on a device the HIP library cannot serve: there is no CPU path to fall back to."""
 
+    def __init__(self):
+        self.override = None          # set by set_backend(); None: the environment decides
+        self.chosen = {}              # device type -> backend name resolved for it
+        self.last = None              # backend of the most recent decode()
 
-def _requested():
-    v = _FORCED if _FORCED is not None else os.environ.get("LFM3KV_BACKEND", "auto")
-    v = (v or "auto").strip().lower()
-    if v not in BACKENDS + REFERENCE_BACKENDS + ("auto",):
-        raise ValueError(f"LFM3KV_BACKEND={v!r}: expected one of {', '.join(BACKENDS + REFERENCE_BACKENDS)}, auto")
-    return v
+    @staticmethod
+    def normalise(name):
+        key = "auto" if name is None else (str(name).strip().lower() or "auto")
+        known = BACKENDS + REFERENCE_BACKENDS + ("auto",)
+        if key not in known:
+            raise ValueError(f"LFM3KV_BACKEND={key!r}: expected one of {', '.join(known)}")
+        return key
 
+    def wanted(self):
+        return self.normalise(self.override if self.override is not None else os.environ.get("LFM3KV_BACKEND"))
 
-def set_backend(name=None):
-    """Force a decode backend ('hip'), or 'auto' / None to pick per device (env LFM3KV_BACKEND is read when None)."""
-    global _FORCED
-    _FORCED = None if name is None else str(name).strip().lower()
-    _requested()
-    _CHOSEN.clear(); _VERIFIED.clear()
-
-
-def get_backend(device_type=None):
-    """Backend used by the last decode() (or the one in use on `device_type`)."""
-    return _CHOSEN.get(device_type) if device_type else _LAST[0]
-
-
-def _available(name, dt):
-    """(ok, detail) for backend `name` on device type `dt`."""
-    if name in REFERENCE_BACKENDS:
-        return False, f"the {name} backend is not part of the MI355X build (use the reference package for it)"
-    if name == "hip":
-        if dt != "cuda":
-            return False, f"the HIP backend runs on ROCm GPUs (torch device type 'cuda'), not {dt!r}"
+    @staticmethod
+    def refusal(name, device_type):
+        """None when backend `name` can run on `device_type`, else why it cannot."""
+        if name in REFERENCE_BACKENDS:
+            return f"the {name} backend is not part of the MI355X build (use the reference package for it)"
+        if device_type != "cuda":
+            return f"the HIP backend runs on ROCm GPUs (torch device type 'cuda'), not {device_type!r}"
         from . import kv800_hip
         try:
             kv800_hip.ops()
         except ImportError as e:
-            return False, str(e)
-        return True, kv800_hip.SOURCE
-    raise ValueError(name)
+            return str(e)
+        return None
+
+    def backend_for(self, device_type):
+        if device_type in self.chosen:
+            return self.chosen[device_type]
+        wanted = self.wanted()
+        name = "hip" if wanted == "auto" else wanted
+        why = self.refusal(name, device_type)
+        if why is not None and wanted == "auto":
+            raise RuntimeError(f"no 800h decode backend for device type {device_type!r} ({why})")
+        if why is not None:
+            raise RuntimeError(f"800h decode backend {wanted!r} was requested (LFM3KV_BACKEND / set_backend) but is "
+                               f"not available on {device_type}: {why}")
+        _log.info("decode backend on %s: %s (%s)", device_type, name, "forced" if wanted != "auto" else "auto")
+        self.chosen[device_type] = name
+        return name
 
 
-def _chain(dt):
-    return ("hip",) if dt == "cuda" else ()
+_SEL = _Selection()
 
 
-def _resolve(dt):
-    if dt in _CHOSEN:
-        return _CHOSEN[dt]
-    req = _requested()
-    if req != "auto":
-        ok, why = _available(req, dt)
-        if not ok:
-            raise RuntimeError(f"800h decode backend {req!r} was requested (LFM3KV_BACKEND / set_backend) but is not "
-                               f"available on {dt}: {why}")
-        _log.info("decode backend on %s: %s (forced; %s)", dt, req, why)
-        _CHOSEN[dt] = req
-        return req
-    skipped = []
-    for name in _chain(dt):
-        ok, why = _available(name, dt)
-        if ok:
-            _log.info("decode backend on %s: %s (%s)", dt, name, why)
-            _CHOSEN[dt] = name
-            return name
-        skipped.append(f"{name}: {why}")
-    raise RuntimeError(f"no 800h decode backend for device type {dt!r}"
-                       + (f" ({'; '.join(skipped)})" if skipped else " (the MI355X build serves ROCm GPUs only)"))
+def set_backend(name=None):
+    """Force a decode backend ('hip'), or 'auto' / None to pick per device (env LFM3KV_BACKEND is read when None).
+    An unknown name raises ValueError and leaves the current setting as it was."""
+    _SEL.override = None if name is None else _SEL.normalise(name)
+    _SEL.chosen.clear()
+
+
+def get_backend(device_type=None):
+    """Backend used by the last decode() (or the one in use on `device_type`)."""
+    return _SEL.chosen.get(device_type) if device_type else _SEL.last
 
 
 def decode(P, q, cos_t, sin_t, H=None, spb=None, target=None):
     """q: (B, 16, 128) bf16 post-RoPE -> (B, 16, 128) bf16 (kv800.py:330-349). cos_t / sin_t: (P, 32) bf16 tables of
     the 32 rotating frequencies (dims d and d + 64 share frequency d, d < 32). H: the normalized 128 Hadamard (implicit
     in the kernels). spb / target: split planning overrides (kv800.py:366-367)."""
-    dt = q.device.type
-    be = _resolve(dt)
-    _LAST[0] = be
-    out = _run(be, P, q, cos_t, sin_t, spb, target)
-    _VERIFIED.add(dt)
-    return out
-
-
-def _run(be, P, q, cos_t, sin_t, spb, target):
-    if be != "hip":
-        raise RuntimeError(f"backend {be!r} is not part of this build")
+    _SEL.last = _SEL.backend_for(q.device.type)
     from . import kv800_hip
     return kv800_hip.decode(P, q, cos_t, sin_t, spb, target)
 
 
 # ---------------------------------------------------------------- harness store with the paged layout
 class PagedStore:
-    """Test/bench store with the vLLM-style paged layout for `batch` equal-length sequences (kv800.py:387-441). Exact
-    pages form a ring of `nring` pages of `ebs` tokens per sequence; sub-blocks are flushed by the HIP paged flush
-    (one launch per append) with the same rule as the vLLM cache."""
+    """Cache of one layer for `batch` sequences of equal length, in the paged layout the decode reads (the reference's
+    test/bench store, kv800.py:387-441, same constructor and methods).
+
+    Exact pages: sequence b owns pages [b nring, (b + 1) nring) of `epool` and uses them as a ring, position p living
+    in page b nring + (p // ebs) % nring, slot p % ebs. Quantized layers: sequence b's sub-block j lives at byte
+    BOFF[b, j] = (b nsub + j) 51,200 of `qpool`. append() moves rows in with the HIP row-write kernel (one launch per
+    step of at most 128 tokens, sinks included) and flushes the sub-blocks that became eligible (n >= 256 j + 384) with
+    one HIP flush launch. A step of at most 128 tokens ends at most 511 positions after the first row of the oldest
+    sub-block still to flush, so a ring of at least 512 + ebs tokens never overwrites a row before its flush."""
+
+    STEP = 128
 
     def __init__(self, batch, max_len, device, window=0, ebs=64, nring=10):
+        if nring * ebs < 512 + ebs:
+            raise ValueError(f"the exact ring of {nring} x {ebs} tokens must hold at least 512 + ebs tokens")
         self.B, self.win, self.dev, self.ebs, self.nring = batch, window, device, ebs, nring
         self.H = hadamard(128, device)
-        nsub = 0 if window else max_len // BLK + 1
-        self.qpool = torch.zeros(max(1, batch * nsub), SUB, dtype=torch.uint8, device=device)
-        self.boff = (torch.arange(batch * max(nsub, 1), device=device, dtype=torch.int64) * SUB).view(batch, max(nsub, 1))
+        nsub = 1 if window else max_len // BLK + 1
+        self.qpool = torch.zeros(batch * nsub, SUB, dtype=torch.uint8, device=device)
+        self.boff = torch.arange(batch * nsub, dtype=torch.int64, device=device).view(batch, nsub) * SUB
         self.epool = torch.zeros(batch * nring, 4, ebs, 256, dtype=torch.bfloat16, device=device)
-        npg = max_len // ebs + 2
-        pg = torch.arange(npg, device=device) % nring
-        self.eoff = ((torch.arange(batch, device=device)[:, None] * nring + pg[None]) * (4 * ebs * 256)).to(torch.int64)
-        self.e_hs, self.e_ts, self.e_v = ebs * 256, 256, 128
+        self.e_hs, self.e_ts, self.e_v = self.epool.stride(1), self.epool.stride(2), 128
+        self._ring0 = torch.arange(batch, dtype=torch.int64, device=device) * nring   # first ring page of each row
+        logical = torch.arange(max_len // ebs + 2, dtype=torch.int64, device=device)
+        self.eoff = (self._ring0[:, None] + logical % nring) * self.epool.stride(0)
         self.sk = torch.zeros(batch, NSINK, 4, 128, dtype=torch.bfloat16, device=device)
         self.sv = torch.zeros_like(self.sk)
-        self.skoff = torch.arange(batch, device=device, dtype=torch.int64) * NSINK * 512
+        self.skoff = self._ring0 // nring * self.sk.stride(0)
         self.N = torch.zeros(batch, dtype=torch.int32, device=device)
-        self.NQ = torch.zeros_like(self.N)
-        self.n, self.nq = 0, 0
-        if nring * ebs < 512 + ebs:
-            raise ValueError("the exact ring must hold at least 512 + ebs tokens")
+        self.NQ = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.n = self.nq = 0
 
     def paged(self):
         return Paged(qpool=self.qpool, boff=self.boff, epool=self.epool, eoff=self.eoff, ebs=self.ebs,
@@ -214,32 +208,29 @@ class PagedStore:
                      sv=self.sv if self.win else None, skoff=self.skoff, svoff=self.skoff, N=self.N, NQ=self.NQ,
                      nqmax=self.nq, win=self.win)
 
-    def _exact_index(self, pos):
-        """element offsets (B, len(pos), 4) of the K rows of positions `pos` for each head."""
-        pg = self.eoff[:, pos // self.ebs]
-        return pg[..., None] + torch.arange(4, device=self.dev) * self.e_hs + (pos % self.ebs)[None, :, None] * self.e_ts
-
     def append(self, k, v):
-        """k: pre-RoPE keys, v: values, (B, T, 4, 128)."""
+        """k: pre-RoPE keys, v: values, (B, T, 4, 128), any float dtype (cast to bf16)."""
+        kh = _hip()
         T = k.shape[1]
-        ef = flat(self.epool)
-        for s in range(0, T, 128):
-            kk, vv = k[:, s:s + 128].to(self.dev, torch.bfloat16), v[:, s:s + 128].to(self.dev, torch.bfloat16)
-            t = kk.shape[1]
-            pos = torch.arange(self.n, self.n + t, device=self.dev)
-            idx = self._exact_index(pos)[..., None] + torch.arange(128, device=self.dev)
-            ef[idx] = kk
-            ef[idx + self.e_v] = vv
+        for t0 in range(0, T, self.STEP):
+            t1 = min(T, t0 + self.STEP)
+            pos = torch.arange(self.n, self.n + t1 - t0, dtype=torch.int64, device=self.dev)
+            slot = (self._ring0[:, None] + (pos // self.ebs) % self.nring) * self.ebs + pos % self.ebs      # (B, t)
+            rows_k = k[:, t0:t1].to(self.dev, torch.bfloat16).reshape(-1, 4, 128)
+            rows_v = v[:, t0:t1].to(self.dev, torch.bfloat16).reshape(-1, 4, 128)
+            sinks = {}
             if self.win and self.n < NSINK:
-                m = pos < NSINK
-                self.sk[:, pos[m]], self.sv[:, pos[m]] = kk[:, m], vv[:, m]
-            self.n += t
-            nq_new = 0 if self.win else max(0, (self.n - LAG) // BLK)
-            if nq_new > self.nq:                     # one launch flushes every newly eligible sub-block of every row
-                prev = torch.full((self.B,), self.nq, dtype=torch.int32, device=self.dev)
-                new = torch.full((self.B,), nq_new, dtype=torch.int32, device=self.dev)
-                _hip().flush(self.epool, self.eoff, self.ebs, self.e_hs, self.e_ts, self.e_v, self.qpool, self.boff,
-                             BLK, 1, prev, new, nq_new - self.nq)
-                self.nq = nq_new
+                sinks = dict(pos=pos.expand(self.B, -1).reshape(-1), sk=self.sk, sv=self.sv,
+                             skoff=self.skoff[:, None].expand(-1, t1 - t0).reshape(-1))
+                sinks["svoff"] = sinks["skoff"]
+            kh.write_exact(self.epool, slot.reshape(-1), rows_k, rows_v, **sinks)
+            self.n += t1 - t0
+            eligible = 0 if self.win else max(0, self.n - LAG) // BLK
+            if eligible > self.nq:
+                nq0 = torch.full((self.B,), self.nq, dtype=torch.int32, device=self.dev)
+                nq1 = torch.full((self.B,), eligible, dtype=torch.int32, device=self.dev)
+                kh.flush(self.epool, self.eoff, self.ebs, self.e_hs, self.e_ts, self.e_v, self.qpool, self.boff,
+                         BLK, 1, nq0, nq1, eligible - self.nq)
+                self.nq = eligible
         self.N.fill_(self.n)
         self.NQ.fill_(self.nq)

@@ -65,6 +65,8 @@ SIGNATURES = {
                                      _VP]),
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
     "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
+    "kv800_hip_rope_rows": (_I32, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _VP]),
+    "kv800_hip_prefill": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _VP]),
     "kv800_hip_fake_quant_k": (_I32, [_VP, _I64, _I64, _VP, _VP]),
     "kv800_hip_flush_latency": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP,
                                        _I64, _I64, _VP]),
@@ -301,6 +303,61 @@ def history(P, lens, cos_t=None, sin_t=None):
                                _ptr(sin_t) if rot else None, cos_t.shape[0] if rot else 0, qbytes, _extent(P.epool),
                                _ptr(offt), _ptr(K), _ptr(V), _stream(dev)))
     return K, V, offs
+
+
+
+def rope_rows(k, pos, cos_t, sin_t):
+    """Keys k (S, 4, 128) bf16 rotated at positions pos (S,) int64 with the (P, 32) bf16 tables (kv800_hip_rope_rows,
+    bit-identical to vllm_attn.py:160-163's _rope over its 128-wide tables). Returns a new (S, 4, 128) bf16 tensor."""
+    L = ops()
+    dev = k.device
+    k = k.contiguous()
+    _need(k, "k", torch.bfloat16, dev); _need(pos, "pos", torch.int64, dev)
+    _need(cos_t, "cos_t", torch.bfloat16, dev); _need(sin_t, "sin_t", torch.bfloat16, dev)
+    if k.dim() != 3 or k.shape[1:] != (4, 128) or pos.shape != (k.shape[0],):
+        raise ValueError(f"k must be (S, 4, 128) with pos (S,), got {tuple(k.shape)}, {tuple(pos.shape)}")
+    if cos_t.shape != sin_t.shape or cos_t.dim() != 2 or cos_t.shape[1] != 32:
+        raise ValueError("cos_t / sin_t must be (P, 32)")
+    out = torch.empty_like(k)
+    _check(L.kv800_hip_rope_rows(_ptr(k), _ptr(pos.contiguous()), k.shape[0], _ptr(cos_t.contiguous()),
+                                 _ptr(sin_t.contiguous()), cos_t.shape[0], _ptr(out), _stream(dev)))
+    return out
+
+
+def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
+    """Prefill attention of ragged rows (kv800_hip_prefill): row r's queries q[qsl[r]:qsl[r+1]] ((T, 16, 128) bf16) at
+    positions qpos0[r], qpos0[r] + 1, ... over keys / values K, V[ksl[r]:ksl[r+1]] ((S, 4, 128) bf16) at positions kp
+    (S,) (ascending within a row). qsl / ksl / qpos0: host sequences (R + 1, R + 1, R). Mask: kp <= query position,
+    and with window > 0 also kp > position - window or kp < nsink. Returns (T, 16, 128) bf16."""
+    L = ops()
+    dev = q.device
+    q, K, V = q.contiguous(), K.contiguous(), V.contiguous()
+    _need(q, "q", torch.bfloat16, dev); _need(K, "K", torch.bfloat16, dev); _need(V, "V", torch.bfloat16, dev)
+    qsl, ksl, qpos0 = [int(x) for x in qsl], [int(x) for x in ksl], [int(x) for x in qpos0]
+    R = len(qpos0)
+    if len(qsl) != R + 1 or len(ksl) != R + 1:
+        raise ValueError("qsl and ksl need R + 1 entries")
+    if q.dim() != 3 or q.shape[1:] != (16, 128) or qsl[0] != 0 or qsl[-1] != q.shape[0]:
+        raise ValueError(f"q must be (qsl[-1], 16, 128), got {tuple(q.shape)}")
+    if K.shape != V.shape or K.dim() != 3 or K.shape[1:] != (4, 128) or ksl[0] != 0 or ksl[-1] != K.shape[0]:
+        raise ValueError(f"K / V must be (ksl[-1], 4, 128), got {tuple(K.shape)}, {tuple(V.shape)}")
+    if any(b < a for a, b in zip(qsl, qsl[1:])) or any(b < a for a, b in zip(ksl, ksl[1:])):
+        raise ValueError("qsl / ksl must be non-decreasing")
+    kp = kp.to(device=dev, dtype=torch.int32).contiguous()
+    if kp.shape != (K.shape[0],):
+        raise ValueError("kp must be (S,)")
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
+    tiles = [0]
+    for a, b in zip(qsl, qsl[1:]):
+        tiles.append(tiles[-1] + (b - a + 15) // 16)
+    if R == 0 or tiles[-1] == 0:
+        return out
+    meta = torch.tensor(qsl + ksl + qpos0 + tiles, dtype=torch.int64).to(dev)
+    m_qsl, m_ksl = meta[:R + 1], meta[R + 1:2 * R + 2]
+    m_pos, m_tiles = meta[2 * R + 2:3 * R + 2], meta[3 * R + 2:]
+    _check(L.kv800_hip_prefill(_ptr(q), _ptr(m_qsl), _ptr(m_pos), _ptr(K), _ptr(V), _ptr(kp), _ptr(m_ksl),
+                               _ptr(m_tiles), R, tiles[-1], int(window), int(nsink), _ptr(out), _stream(dev)))
+    return out
 
 
 def fake_quant_k(x):

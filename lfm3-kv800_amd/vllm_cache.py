@@ -15,6 +15,7 @@ tables and the fused decode. Every piece is a launch of libkv800_hip.so on the c
 are the ones the reference also reads on the host (the rows' sequence lengths, for nqmax and the flush width)."""
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import kv800, kv800_hip
@@ -217,36 +218,13 @@ def launch_flushes(layers, metas, mq, max_new=1):
 
 
 # ---------------------------------------------------------------- prefill / extend rows over compressed history
-def rope_keys(k, pos, cos_t, sin_t):
-    """vllm_attn.py:160-163: keys k (S, 4, 128) bf16 at positions pos (S,) rotated with the 128-wide tables
-    (cos32 | 1 | cos32 | 1), (sin32 | 0 | sin32 | 0) built from the (P, 32) bf16 tables; fp32, then bf16."""
-    c32, s32 = cos_t[pos].float(), sin_t[pos].float()
-    c = torch.cat((c32, torch.ones_like(c32), c32, torch.ones_like(c32)), 1)[:, None]
-    s = torch.cat((s32, torch.zeros_like(s32), s32, torch.zeros_like(s32)), 1)[:, None]
-    kf = k.float()
-    return (kf * c + torch.cat((-kf[..., 64:], kf[..., :64]), -1) * s).to(torch.bfloat16)
-
-
-def prefill_attention(q, K, V, kp, n0, n, window=0):
-    """Causal attention of the queries at positions n0 .. n-1 over keys at positions kp (vllm_attn.py:168-184):
-    q (n - n0, 16, 128), K / V (S, 4, 128) bf16 -> (n - n0, 16, 128) fp32. window = 0: the quantized layers' mask
-    (kp <= query position); window > 0: the window layers' mask, which also keeps a key only if it is one of the last
-    `window` positions or a sink (kp < NSINK). fp32 products on contiguous operands, 512 queries at a time."""
-    Kf = K.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()           # (16, S, 128)
-    KT = Kf.transpose(1, 2).contiguous()                                          # (16, 128, S)
-    Vf = V.float().repeat_interleave(4, 1).transpose(0, 1).contiguous()
-    qi = q.float().transpose(0, 1).contiguous()                                   # (16, Tq, 128)
-    qp = torch.arange(n0, n, device=q.device)
-    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
-    for a in range(0, n - n0, 512):
-        qa = qp[a:a + 512, None]
-        m = kp[None] <= qa
-        if window:
-            m = m & ((kp[None] > qa - window) | (kp[None] < kv800.NSINK))
-        sc = torch.matmul(qi[:, a:a + 512].contiguous(), KT) * (128 ** -0.5)
-        w = sc.masked_fill(~m[None], float("-inf")).softmax(-1)
-        out[a:a + 512] = torch.matmul(w, Vf).transpose(0, 1)
-    return out
+def _ranges(starts, counts):
+    """Concatenation of range(s, s + c) over the pairs, as an int64 numpy array."""
+    starts, counts = np.asarray(starts, np.int64), np.asarray(counts, np.int64)
+    if counts.sum() == 0:
+        return np.zeros(0, np.int64)
+    base = np.repeat(starts - np.concatenate(([0], np.cumsum(counts)[:-1])), counts)
+    return base + np.arange(int(counts.sum()), dtype=np.int64)
 
 
 def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
@@ -254,63 +232,77 @@ def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     q[qsl[i]:qsl[i+1]] (post-RoPE) at positions prev[i] .. prev[i] + (qsl[i+1] - qsl[i]) - 1, new pre-RoPE keys and
     values k / v at the same rows, and a history of prev[i] positions in the cache P (its first (prev - 128) // 256
     sub-blocks flushed, P.NQ, the rest in the exact pages). The history comes out of one kv800_hip_history launch
-    (dequantized, rotated, bf16); the new keys are rotated as the reference does; then causal attention per row.
-    qsl / prev are host sequences. Returns (T, 16, 128) bf16."""
+    (dequantized, rotated, bf16), the new keys out of one kv800_hip_rope_rows launch; each row's keys are its history
+    followed by its new rows, and one kv800_hip_prefill launch attends all rows. qsl / prev are host sequences.
+    Returns (T, 16, 128) bf16."""
+    dev = q.device
+    prev, qsl = [int(x) for x in prev], [int(x) for x in qsl]
     R = len(prev)
-    Kh, Vh, offs = kv800_hip.history(P, [int(x) for x in prev], cos_t, sin_t)
-    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
-    for i in range(R):
-        s, e, n0 = int(qsl[i]), int(qsl[i + 1]), int(prev[i])
-        n = n0 + (e - s)
-        pos = torch.arange(n0, n, device=q.device)
-        Kn = rope_keys(k[s:e], pos, cos_t, sin_t)
-        Kb = torch.cat((Kh[offs[i]:offs[i] + n0], Kn))
-        Vb = torch.cat((Vh[offs[i]:offs[i] + n0], v[s:e].to(torch.bfloat16)))
-        kp = torch.arange(n, device=q.device)
-        out[s:e] = prefill_attention(q[s:e], Kb, Vb, kp, n0, n).to(torch.bfloat16)
-    return out
+    new = [b - a for a, b in zip(qsl, qsl[1:])]
+    Kh, Vh, offs = kv800_hip.history(P, prev, cos_t, sin_t)
+    pos_new = torch.from_numpy(_ranges(prev, new)).to(dev)
+    Kn = kv800_hip.rope_rows(k[:qsl[-1]].to(torch.bfloat16), pos_new, cos_t, sin_t)
+    # key order: row 0's history, row 0's new rows, row 1's history, ... as rows of cat(Kh, Kn)
+    H = Kh.shape[0]
+    order = np.concatenate([np.concatenate((o + np.arange(n0), H + q0 + np.arange(c)))
+                            for o, n0, q0, c in zip(offs, prev, qsl[:-1], new)]) if R else np.zeros(0, np.int64)
+    ksl = np.concatenate(([0], np.cumsum(np.asarray(prev) + np.asarray(new)))).astype(np.int64)
+    idx = torch.from_numpy(order).to(dev)
+    Kc = torch.cat((Kh, Kn)).index_select(0, idx)
+    Vc = torch.cat((Vh, v[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
+    kp = torch.from_numpy(_ranges([0] * R, np.asarray(prev) + np.asarray(new)).astype(np.int32))
+    return kv800_hip.prefill(q, qsl, prev, Kc, Vc, kp, ksl, window=0)
 
 
 def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     """Prefill / extend rows of a window layer (vllm_attn.py:351-402 with win set): row i has queries
-    q[qsl[i]:qsl[i+1]] (post-RoPE) at positions prev[i] .. prev[i] + (qsl[i+1] - qsl[i]) - 1 and new pre-RoPE keys and
-    values k / v at the same rows. Its history is what the window layer keeps: the sinks (positions < min(NSINK, lo))
-    at P.skoff / P.svoff in P.sk / P.sv, and the exact rows [lo, prev[i]) with lo = max(0, prev[i] - (WIN - 1)) in the
-    exact pages of P (P.eoff element offsets per ebs positions, e_hs / e_ts / e_v strides). All keys are rotated as
-    the reference does, then attention with the window + sinks mask. qsl / prev are host sequences. Returns
-    (T, 16, 128) bf16."""
-    R, dev = len(prev), q.device
-    ef = P.epool.reshape(-1)
-    eoff = P.eoff.cpu()
+    q[qsl[i]:qsl[i+1]] (post-RoPE) at positions prev[i] .. prev[i] + (qsl[i+1] - qsl[i]) - 1 and new keys and values
+    k / v at the same rows. Its history is what the layer keeps: the sinks (positions < min(NSINK, lo), when P.sk is
+    set) at P.skoff / P.svoff in P.sk / P.sv, and the exact rows [lo, prev[i]) with lo = max(0, prev[i] - (WIN - 1)) in
+    the exact pages of P (P.eoff element offsets per ebs positions, e_hs / e_ts / e_v strides). With cos_t / sin_t all
+    keys are rotated at their positions (window + sinks layers keep pre-RoPE keys); None leaves them as stored (sliding
+    layers keep post-RoPE keys). One gather of the history, then one kv800_hip_prefill launch with the window mask
+    (and the sinks). qsl / prev are host sequences. Returns (T, 16, 128) bf16."""
+    dev = q.device
+    prev, qsl = [int(x) for x in prev], [int(x) for x in qsl]
+    R = len(prev)
+    new = np.asarray([b - a for a, b in zip(qsl, qsl[1:])], np.int64)
+    p0 = np.asarray(prev, np.int64)
+    lo = np.maximum(0, p0 - (kv800.WIN - 1))
     sinks = P.sk is not None
-    skoff = P.skoff.cpu() if sinks else None
-    svoff = P.svoff.cpu() if sinks else None
+    ns = np.minimum(kv800.NSINK, lo) if sinks else np.zeros(R, np.int64)
+    nx = p0 - lo
+    rows = np.arange(R)
+    # ---- exact rows [lo, prev): element offset of each (position, head) K row through the page table
+    xr = np.repeat(rows, nx)
+    xp = _ranges(lo, nx)
+    page = P.eoff[torch.from_numpy(xr).to(dev), torch.from_numpy(xp // P.ebs).to(dev)]        # (Sx,) element offsets
+    ko = (page + torch.from_numpy((xp % P.ebs) * P.e_ts).to(dev))[:, None] + torch.arange(4, device=dev) * P.e_hs
     d128 = torch.arange(128, device=dev)
-    out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
-    for i in range(R):
-        s, e, n0 = int(qsl[i]), int(qsl[i + 1]), int(prev[i])
-        n = n0 + (e - s)
-        lo = max(0, n0 - (kv800.WIN - 1))
-        ns = min(kv800.NSINK, lo) if sinks else 0
-        ks, vs, ps = [], [], []
-        if ns:
-            rows = (torch.arange(ns, device=dev)[:, None] * 4 + torch.arange(4, device=dev)[None]) * 128   # (ns, 4)
-            ks.append(P.sk.reshape(-1)[int(skoff[i]) + rows[..., None] + d128])
-            vs.append(P.sv.reshape(-1)[int(svoff[i]) + rows[..., None] + d128])
-            ps.append(torch.arange(ns, device=dev))
-        if n0 > lo:
-            pp = torch.arange(lo, n0)
-            base = eoff[i, pp // P.ebs]
-            if bool((base < 0).any()):
-                raise ValueError(f"row {i}: exact page of a window position [{lo}, {n0}) is not mapped")
-            ko = (base + (pp % P.ebs) * P.e_ts).to(dev)[:, None] + torch.arange(4, device=dev)[None] * P.e_hs   # (S, 4)
-            ks.append(ef[ko[..., None] + d128])
-            vs.append(ef[ko[..., None] + P.e_v + d128])
-            ps.append(pp.to(dev))
-        ks.append(k[s:e].to(torch.bfloat16)); vs.append(v[s:e].to(torch.bfloat16))
-        ps.append(torch.arange(n0, n, device=dev))
-        kp = torch.cat(ps)
-        Kb = rope_keys(torch.cat(ks), kp, cos_t, sin_t)
-        Vb = torch.cat(vs)
-        out[s:e] = prefill_attention(q[s:e], Kb, Vb, kp, n0, n, window=kv800.WIN).to(torch.bfloat16)
-    return out
+    ef = kv800.flat(P.epool)
+    Kx, Vx = ef[ko[..., None] + d128], ef[ko[..., None] + P.e_v + d128]                          # (Sx, 4, 128)
+    # ---- sink rows
+    if sinks:
+        sr = np.repeat(rows, ns)
+        st = _ranges(np.zeros(R, np.int64), ns)
+        so = torch.from_numpy(st * 512).to(dev)[:, None] + torch.arange(4, device=dev) * 128
+        Ks = kv800.flat(P.sk)[(P.skoff[torch.from_numpy(sr).to(dev)][:, None] + so)[..., None] + d128]
+        Vs = kv800.flat(P.sv)[(P.svoff[torch.from_numpy(sr).to(dev)][:, None] + so)[..., None] + d128]
+    else:
+        Ks = Vs = torch.empty(0, 4, 128, dtype=torch.bfloat16, device=dev)
+    # ---- per row: sinks, exact rows, new rows, as rows of cat(sinks, exact, new)
+    cnt = ns + nx + new
+    ksl = np.concatenate(([0], np.cumsum(cnt))).astype(np.int64)
+    order = np.concatenate([np.concatenate((_ranges([s0], [a]), len(Ks) + _ranges([x0], [b]),
+                                            len(Ks) + len(Kx) + _ranges([q0], [c])))
+                            for s0, x0, q0, a, b, c in zip(np.cumsum(ns) - ns, np.cumsum(nx) - nx, qsl[:-1], ns, nx,
+                                                           new)]) if R else np.zeros(0, np.int64)
+    kpos = np.concatenate([np.concatenate((np.arange(a), np.arange(l0, n0), np.arange(n0, n0 + c)))
+                           for a, l0, n0, c in zip(ns, lo, p0, new)]) if R else np.zeros(0, np.int64)
+    idx = torch.from_numpy(order.astype(np.int64)).to(dev)
+    Kc = torch.cat((Ks, Kx, k[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
+    Vc = torch.cat((Vs, Vx, v[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
+    if cos_t is not None:
+        Kc = kv800_hip.rope_rows(Kc, torch.from_numpy(kpos).to(dev), cos_t, sin_t)
+    return kv800_hip.prefill(q, qsl, prev, Kc, Vc, torch.from_numpy(kpos.astype(np.int32)), ksl, window=kv800.WIN,
+                             nsink=kv800.NSINK if sinks else 0)

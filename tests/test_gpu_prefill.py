@@ -164,3 +164,95 @@ def test_prefill_window_rows(hip, oracle):
         d = np.abs(o[qsl[b]:qsl[b + 1]] - want)
         say(f"window row {b} (n0={n0}, {n - n0} new): max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
         assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (b, d.max(), d.mean())
+
+
+def test_rope_rows_bitexact(hip, oracle):
+    """kv800_hip_rope_rows against vllm_attn.py:160-163 restated in numpy float32, bit for bit, on offset keys at
+    random positions (signed zeros included)."""
+    rng = np.random.RandomState(21)
+    S = 3000
+    k = oracle.randn_bf16(rng, (S, 4, 128), offset=3 * rng.standard_normal((1, 4, 128)))
+    k[::97, 1, 40] = 0x8000                                   # -0.0 on a dim without a frequency
+    k[::89, 2, 5] = 0x8000                                    # -0.0 on a rotating dim
+    cos, sin = oracle.rope_tables(40000)
+    pos = rng.randint(0, 40000, size=S).astype(np.int64)
+    got = bits_of(hip.rope_rows(to_dev_bf16(k), torch.from_numpy(pos).to(DEV), to_dev_bf16(cos), to_dev_bf16(sin)))
+    want = rope_np(oracle, k, pos, cos, sin)
+    say("rope_rows", S, "rows, mismatches", int((got != want).sum()))
+    assert np.array_equal(got, want)
+
+
+def test_prefill_slide_rows(hip, oracle):
+    """Extend rows of a native sliding layer: window 256 without sinks, keys stored after RoPE and used as stored
+    (cos_t None), against a float64 attention over the same keys / values taken from the inputs."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    import lfm3_kv800_amd.kv800 as kv
+    rng = np.random.RandomState(17)
+    prev = [0, 2, 255, 256, 900]
+    new = [3, 40, 1, 77, 130]
+    lens = [p + t for p, t in zip(prev, new)]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), prev, win=256, ebs=64, shuffle_seed=2,
+                              sinks=False)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    P = kv.Paged(qpool=None, boff=None, epool=to_dev_bf16(case.epool), eoff=T(case.eoff), ebs=case.ebs, e_hs=case.e_hs,
+                 e_ts=case.e_ts, e_v=case.e_v, sk=None, sv=None, skoff=None, svoff=None, N=T(case.N), NQ=T(case.NQ),
+                 nqmax=0, win=256)
+    q = oracle.randn_bf16(rng, (sum(new), 16, 128))
+    qsl = np.concatenate([[0], np.cumsum(new)])
+    kn = np.concatenate([K[b][prev[b]:] for b in range(len(prev))])
+    vn = np.concatenate([V[b][prev[b]:] for b in range(len(prev))])
+    say("slide prefill rows", prev, new)
+    out = vc.prefill_window_rows(P, to_dev_bf16(q), to_dev_bf16(kn), to_dev_bf16(vn), qsl, prev, None, None)
+    o = torch.from_numpy(bits_of(out).view(np.int16)).view(torch.bfloat16).float().numpy()
+    W = 256
+    for b in range(len(prev)):
+        n0, n = prev[b], lens[b]
+        kp = np.arange(max(0, n0 - (W - 1)), n)
+        Kf = np.repeat(oracle.bf16_to_f32(K[b][kp]).astype(np.float64), 4, axis=1)
+        Vf = np.repeat(oracle.bf16_to_f32(V[b][kp]).astype(np.float64), 4, axis=1)
+        qf = oracle.bf16_to_f32(q[qsl[b]:qsl[b + 1]]).astype(np.float64)
+        sc = np.einsum("thd,shd->hts", qf, Kf) * 128 ** -0.5
+        qp = np.arange(n0, n)[None, :, None]
+        sc = np.where((kp[None, None, :] <= qp) & (kp[None, None, :] > qp - W), sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
+        want = np.einsum("hts,shd->thd", w, Vf)
+        d = np.abs(o[qsl[b]:qsl[b + 1]] - want)
+        say(f"slide row {b} (n0={n0}, {n - n0} new): max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (b, d.max(), d.mean())
+
+
+def test_prefill_long_chunk(hip, oracle):
+    """One 2048-query chunk over a 6,000-token quantized history (the reference's 2048-query prefill chunk): property
+    checks at full size (finite, |out| <= max |V|), and 64 sampled queries against float64."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    rng = np.random.RandomState(31)
+    n0, t = 6000, 2048
+    n = n0 + t
+    K = oracle.randn_bf16(rng, (n, 4, 128))
+    V = oracle.randn_bf16(rng, (n, 4, 128))
+    cos, sin = oracle.rope_tables(n + 8)
+    case = oracle.build_paged(lambda b, p0, p1: (K[p0:p1], V[p0:p1]), [n0], ebs=64, shuffle_seed=9)
+    P = upload(case)
+    q = oracle.randn_bf16(rng, (t, 16, 128))
+    say("long prefill chunk", n0, t)
+    out = vc.prefill_quant_rows(P, to_dev_bf16(q), to_dev_bf16(K[n0:]), to_dev_bf16(V[n0:]), [0, t], [n0],
+                                to_dev_bf16(cos), to_dev_bf16(sin))
+    o = torch.from_numpy(bits_of(out).view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.isfinite(o).all()
+    kb, vb = history_np(oracle, K, V, n0)
+    kb = np.concatenate([kb, K[n0:]]); vb = np.concatenate([vb, V[n0:]])
+    Vf = oracle.bf16_to_f32(vb).astype(np.float64)
+    assert np.abs(o).max() <= np.abs(Vf).max() + 1e-2
+    Kr = np.repeat(oracle.bf16_to_f32(rope_np(oracle, kb, np.arange(n), cos, sin)).astype(np.float64), 4, axis=1)
+    Vr = np.repeat(Vf, 4, axis=1)
+    pick = np.sort(rng.choice(t, 64, replace=False))
+    qf = oracle.bf16_to_f32(q[pick]).astype(np.float64)
+    sc = np.einsum("thd,shd->hts", qf, Kr) * 128 ** -0.5
+    sc = np.where(np.arange(n)[None, None, :] <= (n0 + pick)[None, :, None], sc, -np.inf)
+    w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
+    want = np.einsum("hts,shd->thd", w, Vr)
+    d = np.abs(o[pick] - want)
+    say(f"long chunk: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+    assert d.max() < MAX_ABS and d.mean() < MEAN_ABS

@@ -40,19 +40,23 @@ def test_cpu_decode_raises_no_fallback():
 def test_reference_backends_are_not_in_this_build(name):
     kv.set_backend(name)
     with pytest.raises(RuntimeError, match="not part of the MI355X build"):
-        kv._resolve("cuda")
+        kv._SEL.backend_for("cuda")
 
 
 def test_unknown_backend_rejected():
+    kv.set_backend("hip")
     with pytest.raises(ValueError):
         kv.set_backend("cuda-graphs")
+    assert kv._SEL.wanted() == "hip"           # the rejected name left the setting as it was
 
 
 def test_env_backend(monkeypatch):
     monkeypatch.setenv("LFM3KV_BACKEND", "hip")
-    assert kv._requested() == "hip"
-    ok, why = kv._available("hip", "cpu")
-    assert not ok and "ROCm" in why
+    assert kv._SEL.wanted() == "hip"
+    why = kv._SEL.refusal("hip", "cpu")
+    assert why is not None and "ROCm" in why
+    with pytest.raises(RuntimeError, match="was requested"):
+        kv._SEL.backend_for("cpu")
 
 
 def test_hip_ops_raises_importerror_without_gpu():
@@ -74,13 +78,10 @@ def test_plan_rules():
     assert spb == 32 and ns == 4
 
 
-def test_prefill_window_rows_on_host(oracle):
-    """The window-layer extend rows (vllm_cache.prefill_window_rows) are host-side gathers + torch attention; the GPU
-    test's cases run here on CPU tensors against the same float64 restatement."""
-    import test_gpu_prefill as tp
-    old = tp.DEV
-    tp.DEV = "cpu"
-    try:
-        tp.test_prefill_window_rows(None, oracle)
-    finally:
-        tp.DEV = old
+def test_ranges_helper():
+    """vllm_cache._ranges: the concatenated key / position ranges the prefill rows assemble on the host."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    got = vc._ranges([5, 0, 100, 7], [3, 0, 2, 1])
+    assert got.tolist() == [5, 6, 7, 100, 101, 7]
+    assert vc._ranges([], []).tolist() == []
+    assert vc._ranges([3], [0]).tolist() == []
