@@ -9,7 +9,8 @@ A step = one kv800.decode call over one layer (the quantized-split grid with the
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
 JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
 duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
-cpu_baseline: the CPU oracle (a C restatement of torch_decode.py) on a bounded sample of the same workload. Extra
+cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on a sample of the same rows (the C
+oracle's time beside it). Extra
 fields: flush_c2 (the flush kernel alone), c4 (config 4, one decode step of all 6 attention
 layers over 398 ragged sequences) and e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
 sequences). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
@@ -187,6 +188,11 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
         step(i)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
+    # one more step (past the timed ones) whose layer outputs are checked
+    me, mq = metas[-1]
+    outs = [layers[l].forward(*qkv[l], me[C4_GROUP[l]], mq, hosts=layers, cos_t=cos, sin_t=sin)
+            for l in (2, 6, 10, 14, 18, 22)]
+    finite = all(bool(torch.isfinite(o.float()).all()) for o in outs)
     # algorithmic bytes of one step (the reference's accounting), at the mean step length
     nmid = L0 + 1 + warmup + steps // 2
     nq = np.maximum(nmid - 128, 0) // 256
@@ -196,7 +202,7 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
     return {"workload": "C4: 6 attention layers (4 quantized + 2 window+sinks), 398 seqs, lengths U[1K, 32K], vLLM "
                         "page geometry, two exact KV groups, new-token write + flush + decode per layer",
             "ms_per_step": round(ms, 4), "tok_s": round(C4_R / (ms * 1e-3), 1), "bytes_per_step": qbytes + wbytes,
-            "gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBS, 4)}
+            "gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBS, 4), "outputs_finite": finite}
 
 
 E2E_R, E2E_MIN, E2E_MAX = 256, 1024, 32768
@@ -252,30 +258,53 @@ def rope_tables(torch, n, dev):
     return fr.cos().to(torch.bfloat16).to(dev), fr.sin().to(torch.bfloat16).to(dev)
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, P, q, cos, sin, rows):
-    """Oracle decode (oracle/kv800_oracle.c, torch_decode.py semantics) of `rows` rows, on this host's cores."""
+    """The reference's pure-torch decode restated on CPU torch (oracle/torch_port.py, torch_decode.py:27-80) over
+    rows 0 .. rows-1 of the layer, on this host's cores (at most 16, the box's CPU share); and the C oracle
+    (oracle/kv800_oracle.c, OpenMP) over the same rows. Returns ((port s, threads), (C oracle s, threads))."""
     import numpy as np
+    from types import SimpleNamespace
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    C = lambda t: t.detach().cpu().contiguous().numpy()
-    B16 = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    import torch_port
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    C = lambda t: t.detach().cpu()
+    cp = SimpleNamespace(qpool=C(P.qpool), boff=C(P.boff), epool=C(P.epool), eoff=C(P.eoff), ebs=P.ebs, e_hs=P.e_hs,
+                         e_ts=P.e_ts, e_v=P.e_v, sk=None, sv=None, skoff=None, svoff=None, N=C(P.N), NQ=C(P.NQ),
+                         nqmax=P.nqmax, win=P.win)
+    qc, cc, sc = C(q), C(cos), C(sin)
+    torch_port.decode(cp, qc, cc, sc, rows=[0])                      # page in, warm the allocator
+    t0 = time.perf_counter()
+    torch_port.decode(cp, qc, cc, sc, rows=range(rows))
+    t_port = time.perf_counter() - t0
+    # the C oracle over the same rows (its sub-blocks re-addressed into a compact pool)
+    N2 = lambda t: t.detach().cpu().contiguous().numpy()
+    B16 = lambda t: N2(t).view(np.uint16)
     sel = list(range(rows))
-    # the rows' sub-blocks only, re-addressed into a compact pool
-    boff = C(P.boff)[sel]
-    qp = P.qpool.view(-1, 51200)
-    blocks = torch.from_numpy((boff // 51200).reshape(-1)).to(P.qpool.device)
-    qpool = C(qp.index_select(0, blocks))
-    boff_c = (np.arange(rows * NQ, dtype=np.int64) * 51200).reshape(rows, NQ)
-    case = oracle.PagedCase(qpool=qpool, boff=boff_c, epool=B16(P.epool), eoff=C(P.eoff)[sel], ebs=P.ebs, e_hs=P.e_hs,
+    blocks = torch.from_numpy((N2(P.boff)[sel] // 51200).reshape(-1)).to(P.qpool.device)
+    qpool = N2(P.qpool.view(-1, 51200).index_select(0, blocks))
+    case = oracle.PagedCase(qpool=qpool, boff=(np.arange(rows * NQ, dtype=np.int64) * 51200).reshape(rows, NQ),
+                            epool=B16(P.epool.view(torch.int16)), eoff=N2(P.eoff)[sel], ebs=P.ebs, e_hs=P.e_hs,
                             e_ts=P.e_ts, e_v=P.e_v, sk=np.zeros(1, np.uint16), sv=np.zeros(1, np.uint16),
                             skoff=np.zeros(rows, np.int64), svoff=np.zeros(rows, np.int64), sinks=False,
-                            N=C(P.N)[sel], NQ=C(P.NQ)[sel], nqmax=NQ, win=0, B=rows)
-    qb, cb, sb = B16(q)[sel], B16(cos), B16(sin)
-    oracle.decode(case, qb[:1], cb, sb) if rows > 1 else None        # page in
+                            N=N2(P.N)[sel], NQ=N2(P.NQ)[sel], nqmax=NQ, win=0, B=rows)
+    qb, cb, sb = B16(q.view(torch.int16))[sel], B16(cos.view(torch.int16)), B16(sin.view(torch.int16))
     t0 = time.perf_counter()
     oracle.decode(case, qb, cb, sb)
-    dt = time.perf_counter() - t0
-    return dt, oracle.num_threads()
+    t_c = time.perf_counter() - t0
+    return (t_port, threads), (t_c, oracle.num_threads())
 
 
 def main():
@@ -382,10 +411,12 @@ def main():
     cpu = None
     if not a.no_cpu:
         rows = max(1, min(B, a.cpu_rows))
-        dt, cores = cpu_baseline(torch, layers[0], q, cos, sin, rows)
-        cpu = {"value": dt * 1e3 * B / rows, "unit": "ms/layer (64x32K, extrapolated from the sample)", "cores": cores,
-               "kind": "port", "sample": f"oracle decode of rows 0..{rows - 1} of the 64 x 32768 layer "
-                                         f"({dt:.2f} s), scaled by 64/{rows}"}
+        (dt, cores), (dt_c, cores_c) = cpu_baseline(torch, layers[0], q, cos, sin, rows)
+        cpu = {"value": round(dt * 1e3 * B / rows, 1), "unit": "ms/layer (64x32K, scaled from the sample)",
+               "cores": cores, "cpu_model": cpu_model(), "kind": "port",
+               "sample": f"pure-torch restatement of torch_decode.decode (oracle/torch_port.py) on rows 0..{rows - 1} "
+                         f"of the 64 x 32768 layer, {cores} torch threads: {dt:.2f} s, scaled by 64/{rows}",
+               "c_oracle_ms_per_layer": round(dt_c * 1e3 * B / rows, 1), "c_oracle_threads": cores_c}
 
     # ---- the other BASELINE configs with a GPU workload: C2 (flush alone) and C4 (6-layer decode step)
     del layers, structs

@@ -162,6 +162,45 @@ def test_oracle_decode_planted_mistakes_fail(oracle, mutate):
     assert rel > 3e-2, (mutate, rel)
 
 
+def _torch_case(case):
+    """An oracle PagedCase as CPU torch tensors with the kv800.Paged field names."""
+    from types import SimpleNamespace
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    bf = lambda a: T(a.view(np.int16)).view(torch.bfloat16)
+    return SimpleNamespace(qpool=T(case.qpool), boff=T(case.boff), epool=bf(case.epool), eoff=T(case.eoff),
+                           ebs=case.ebs, e_hs=case.e_hs, e_ts=case.e_ts, e_v=case.e_v,
+                           sk=bf(case.sk) if case.sinks else None, sv=bf(case.sv) if case.sinks else None,
+                           skoff=T(case.skoff), svoff=T(case.svoff), N=T(case.N), NQ=T(case.NQ), nqmax=case.nqmax,
+                           win=case.win)
+
+
+@pytest.mark.parametrize("win,n", [(0, 1024), (0, 5000), (256, 1500), (256, 3)])
+def test_torch_port_matches_c_oracle(oracle, win, n):
+    """oracle/torch_port.py (the pure-torch CPU baseline) and the C oracle restate the same decode: on the
+    reference's parity inputs they agree to the bf16 rounding of their different summation orders."""
+    import torch_port
+    q, K, V = parity_inputs(oracle, n, win, seed=5)
+    cos, sin = oracle.rope_tables(n + 8)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b, p0:p1], V[b, p0:p1]), [n, n], win=win, shuffle_seed=n)
+    want = oracle.bf16_to_f32(oracle.decode(case, q, cos, sin))
+    got = torch_port.decode(_torch_case(case), t_bf16(q), t_bf16(cos), t_bf16(sin)).float().numpy()
+    d = np.abs(got - want)
+    assert d.max() <= np.abs(want).max() * 2 ** -7 and d.mean() < 1e-4, (d.max(), d.mean())
+
+
+def test_torch_port_dequantize_matches_statement():
+    """torch_port.dequantize against the golden generator's dequantizer (tests/golden/torch_statement.py)."""
+    import torch_port
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(3, 256, 4, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(3, 256, 4, 128, generator=g).to(torch.bfloat16)
+    sb = ts.quantize(k, v)
+    k1, v1 = torch_port.dequantize(sb, torch_port.hadamard128())
+    k2, v2 = ts.dequantize(sb)
+    assert torch.equal(k1, k2.float()) and torch.equal(v1, v2)
+    assert torch.equal(torch_port.hadamard128(), ts.sylvester())
+
+
 def test_oracle_combine():
     import oracle as o
     rng = np.random.RandomState(3)
