@@ -588,32 +588,6 @@ __device__ __forceinline__ void qload(QChunk& C, const uint8_t* __restrict__ sb,
   C.vb[1] = *reinterpret_cast<const u4v*>(vp + 16);
 }
 
-// Scores of one tile for KV head H (all 16 query-row columns; column n is meaningful for H == n / 4).
-template <int H>
-__device__ __forceinline__ f4 qk_head(const char* lutc, uint2 kc, const u4v (&cs)[2], const u4v (&sw)[2], uint32_t gw,
-                                      uint32_t cg, const b8 (&bq)[4]) {
-  f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const uint32_t x = d ? kc.y : kc.x;
-    const uint32_t R = ((x << 2) & 0xCCCCCCCCu) | cg;   // byte e: 4 (c0 + 16 c2) + 16 rot, the rope entry's byte offset
-    const uint32_t N = (x & 0xCCCCCCCCu) | cg;          // byte e: 4 (c1 + 16 c3) + 16 rot, the nope entry's
-    uint32_t kk[4], an[4], ar[4], c4[4], s4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t sel = 0x0C0C0104u + (uint32_t)e;   // byte 0 = byte e of the index word, byte 1 = byte 1 of gw
-      const uint32_t ra = __builtin_amdgcn_perm(R, gw, sel), na = __builtin_amdgcn_perm(N, gw, sel);
-      kk[e] = *reinterpret_cast<const uint32_t*>(lutc + ra + 1024 * (H * 2 + d));
-      an[e] = *reinterpret_cast<const uint32_t*>(lutc + na + 1024 * ((4 + H) * 2 + d));
-      c4[e] = cs[d][e];
-      s4[e] = sw[d][e];
-    }
-    rope4(kk, c4, s4, ar);
-    acc = mfma_bf(pack8b(ar), bq[d], acc);
-    acc = mfma_bf(pack8b(an), bq[2 + d], acc);
-  }
-  return acc;
-}
 static_assert(sizeof(XLds) <= 65536, "exact-tail scratch too large");
 
 // Attention of row b's 16 query rows over its sub-blocks [j0, j1). The workgroup's partial (m, l, acc in the Hadamard
@@ -675,15 +649,10 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       W.vb[32 * (h0 + 1) + s] = C.vb[1];
       asm volatile("" ::: "memory");
     }
-    // QK in 8 steps (head h, kc dword d), both tiles per step; each step's table reads are issued one step ahead
-    u4v sw[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sw[u][d][e] = __builtin_amdgcn_alignbit(C.cs[u][d][e], C.cs[u][d][e], 16);
-    f4 qa[2][4];
+    // QK in 8 steps (head h, kc dword d), both tiles per step; each step's table reads are issued one step ahead. The
+    // lane keeps only its own head's scores: after head h's two k-step pairs, column n's values move to sv when h == hn.
+    f4 qa[2];
+    float sv[2][4];   // raw scores (scale > 0 is applied inside the exponent)
     uint32_t kk[2][2][4], an[2][2][4];   // [step parity][tile][e]
     auto lookup = [&](const int st, const int pb) {
       const int h = st >> 1, d = st & 1;
@@ -711,29 +680,27 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       for (int u = 0; u < 2; ++u) {
         uint32_t c4[4], s4[4], ar[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { c4[e] = C.cs[u][d][e]; s4[e] = sw[u][d][e]; }
+        for (int e = 0; e < 4; ++e) {
+          c4[e] = C.cs[u][d][e];
+          s4[e] = __builtin_amdgcn_alignbit(C.cs[u][d][e], C.cs[u][d][e], 16);
+        }
         rope4(kk[pb][u], c4, s4, ar);
-        const f4 z = (d == 0) ? f4{0.f, 0.f, 0.f, 0.f} : qa[u][h];
-        qa[u][h] = mfma_bf(pack8b(ar), bq[d], z);
-        qa[u][h] = mfma_bf(pack8b(an[pb][u]), bq[2 + d], qa[u][h]);
+        const f4 z = (d == 0) ? f4{0.f, 0.f, 0.f, 0.f} : qa[u];
+        qa[u] = mfma_bf(pack8b(ar), bq[d], z);
+        qa[u] = mfma_bf(pack8b(an[pb][u]), bq[2 + d], qa[u]);
+        if (d == 1) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[u][i] = (h == 0 || hn == h) ? qa[u][i] : sv[u][i];
+        }
       }
     }
-    float sv[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = (hn & 2) ? ((hn & 1) ? qa[u][3][i] : qa[u][2][i]) : ((hn & 1) ? qa[u][1][i] : qa[u][0][i]);
-        sv[u][i] = x * scale;
-      }
     // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
     float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                        fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
-    tmax = max4rows(tmax);
-    {   // lazy running max without a branch: al = 1 unless a chunk max exceeds m by more than QLAZY
-      const bool up = __any(tmax > m + QLAZY);
-      const float mn = up ? fmaxf(m, tmax) : m;
-      const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; exp2(0) = 1, tiny results flush to 0
+    tmax = max4rows(tmax) * scale;
+    if (__any(tmax > m + QLAZY)) {   // lazy running max: rescale only when a chunk max exceeds m by more than QLAZY
+      const float mn = fmaxf(m, tmax);
+      const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
       m = mn; lsum *= al; lvs *= al;
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] *= al;
@@ -744,8 +711,10 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       const int t0 = 32 * cc + 16 * u + 4 * g;
       const float4 vs4 = *reinterpret_cast<const float4*>(&W.vs[n >> 3][t0]);
       const float4 vl4 = *reinterpret_cast<const float4*>(&W.vl[n >> 3][t0]);
-      const float p0 = __builtin_amdgcn_exp2f(sv[u][0] - m), p1 = __builtin_amdgcn_exp2f(sv[u][1] - m);
-      const float p2 = __builtin_amdgcn_exp2f(sv[u][2] - m), p3 = __builtin_amdgcn_exp2f(sv[u][3] - m);
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[u][0], scale, -m));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[u][1], scale, -m));
+      const float p2 = __builtin_amdgcn_exp2f(fmaf(sv[u][2], scale, -m));
+      const float p3 = __builtin_amdgcn_exp2f(fmaf(sv[u][3], scale, -m));
       lsum += (p0 + p1) + (p2 + p3);
       lvs += (p0 * vl4.x + p1 * vl4.y) + (p2 * vl4.z + p3 * vl4.w);
       wt[u][0] = p0 * vs4.x; wt[u][1] = p1 * vs4.y; wt[u][2] = p2 * vs4.z; wt[u][3] = p3 * vs4.w;
