@@ -478,8 +478,9 @@ constexpr float QLAZY = 7.f;   // p <= 2^7 and vsc <= 448 keep the fp16 weights 
 constexpr int64_t BAL_CHUNK = 16, BAL_GROUPS = 1536;   // balanced schedule: sub-blocks per workgroup, most workgroups
 constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
 constexpr int QROW = 132;
+constexpr int VBH = 34;        // staged vb rows per head: 32 + 2 of padding put head h + 2 16 banks away from head h
 struct QWaveLds {
-  u4v vb[4 * 32];              // the chunk's vb bytes: the 16-byte row of (head h, slot) at vb[32 h + slot]
+  u4v vb[4 * VBH];             // the chunk's vb bytes: the 16-byte row of (head h, slot) at vb[VBH h + slot]
   float vs[2][64], vl[2][64];  // decoded vsc / vlo of the wave's 64 tokens, per head group
 };
 struct QLds {
@@ -553,9 +554,13 @@ __device__ __forceinline__ void lut_build(uint32_t* lut, int t, const TabBytes& 
 #pragma unroll
   for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
   uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 16 * (e ^ (g & 1));
+  // row cb of the table at dword 4 cb; write k stores row (k + r) & 3 with r = (j >> 1) & 3, so that the 8 lanes of
+  // one 128-byte write cycle (same g, e and d varying) cover the 32 banks once: bank 16 (slot & 1) + 4 row + 0..3
+  const int r = (j >> 1) & 3;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const uint32_t hi = pa[cb] & 0xFFFF0000u;
+  for (int k = 0; k < 4; ++k) {
+    const int cb = (k + r) & 3;
+    const uint32_t hi = (cb & 2 ? (cb & 1 ? pa[3] : pa[2]) : (cb & 1 ? pa[1] : pa[0])) & 0xFFFF0000u;
     *reinterpret_cast<u4v*>(tab + 4 * cb) =
         u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
   }
@@ -645,8 +650,8 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     {   // the chunk's vb rows into the wave's LDS copy (the previous chunk's reads were issued before)
       const int t = lane >> 1, s = vb_slot(t), h0 = 2 * (lane & 1);
       asm volatile("" ::: "memory");
-      W.vb[32 * h0 + s] = C.vb[0];
-      W.vb[32 * (h0 + 1) + s] = C.vb[1];
+      W.vb[VBH * h0 + s] = C.vb[0];
+      W.vb[VBH * (h0 + 1) + s] = C.vb[1];
       asm volatile("" ::: "memory");
     }
     // QK in 8 steps (head h, kc dword d), both tiles per step; each step's table reads are issued one step ahead. The
@@ -727,7 +732,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       const h8 B = (hn == h) ? Bw : pack8(0u, 0u, 0u, 0u);
       typedef __attribute__((address_space(3))) i2v lds_i2;
       const i2v X = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-          (lds_i2*)(reinterpret_cast<char*>(W.vb) + (h * 32 + 8 * g) * 16 + 8 * n));
+          (lds_i2*)(reinterpret_cast<char*>(W.vb) + (h * VBH + 8 * g) * 16 + 8 * n));
       const uint32_t x0 = (uint32_t)X.x, x1 = (uint32_t)X.x >> 8, x2 = (uint32_t)X.y, x3 = (uint32_t)X.y >> 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
