@@ -12,8 +12,8 @@ duration, one HIP event pair per launch on its own stream; traffic from the comm
 cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on a sample of the same rows (the C
 oracle's time beside it). Extra
 fields: flush_c2 (the flush kernel alone), c4 (config 4, one decode step of all 6 attention
-layers over 398 ragged sequences) and e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
-sequences). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
+layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
+sequences) and e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
 import argparse
 import json
 import os
@@ -208,17 +208,20 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
 E2E_R, E2E_MIN, E2E_MAX = 256, 1024, 32768
 
 
-def bench_e2e(torch, dev, steps, seed=51):
+def bench_e2e(torch, dev, steps, lens=None, seed=51):
     """greedy decode of a random-init LFM3-1.7B-shaped model (lfm3-kv800_amd/model.py: 24 layers,
     13 short-conv, 6 full-attention on the 800h caches, 5 sliding-window; weights N(0, 0.02) bf16) over 256 sequences
-    with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps. tok/s = c (steps - 1) / time, time from the end of
-    the first step to the end of the last (the reference's decode tok/s, RESULTS_RELEASE.md:83-85). The prompts' K / V
-    histories are synthetic N(0, 1), written into the caches (quantized by the HIP quantizer) before the first step:
-    prompt processing is not part of the measurement."""
+    with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps; `lens` replaces the prompt lengths (the reference's
+    published throughput point is 398 sequences of 32,768 tokens, RESULTS_RELEASE.md:90-96). tok/s = c (steps - 1) /
+    time, time from the end of the first step to the end of the last (the reference's decode tok/s,
+    RESULTS_RELEASE.md:83-85). The prompts' K / V histories are synthetic N(0, 1), written into the caches (quantized by
+    the HIP quantizer) before the first step: prompt processing is not part of the measurement."""
     import numpy as np
     from lfm3_kv800_amd import model as M
     cfg = M.Lfm3Config()
-    L0 = np.random.RandomState(seed).randint(E2E_MIN, E2E_MAX + 1, size=E2E_R).astype(np.int64)
+    L0 = (np.random.RandomState(seed).randint(E2E_MIN, E2E_MAX + 1, size=E2E_R) if lens is None
+          else np.asarray(lens)).astype(np.int64)
+    R = len(L0)
     g = torch.Generator(device=dev).manual_seed(seed)
 
     def history(l, r, p0, p1):
@@ -229,11 +232,11 @@ def bench_e2e(torch, dev, steps, seed=51):
     t = time.perf_counter()
     attn = M.PagedAttention800(L0.tolist(), steps + 1, dev, seed=seed)
     attn.fill(history)
-    model = M.Lfm3Decoder(cfg, attn, E2E_R, dev, seed=seed)
+    model = M.Lfm3Decoder(cfg, attn, R, dev, seed=seed)
     model.randomize_conv_states(seed)
-    tokens = torch.randint(0, cfg.vocab, (E2E_R,), generator=g, device=dev)
+    tokens = torch.randint(0, cfg.vocab, (R,), generator=g, device=dev)
     torch.cuda.synchronize()
-    log(f"e2e: caches of {E2E_R} prompts ({int(L0.sum())} tokens) and weights ready in {time.perf_counter() - t:.1f} s")
+    log(f"e2e: caches of {R} prompts ({int(L0.sum())} tokens) and weights ready in {time.perf_counter() - t:.1f} s")
     tokens = model.step(tokens, attn.begin_step()).argmax(-1)        # first step: outside the measured window
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -243,12 +246,16 @@ def bench_e2e(torch, dev, steps, seed=51):
     dt = time.perf_counter() - t0
     assert bool(((tokens >= 0) & (tokens < cfg.vocab)).all())
     ctx = L0 + steps
-    return {"workload": f"C5: greedy decode, random-init LFM3-1.7B-shaped model (hidden 2048, 24 layers: 13 conv, "
-                        f"6 full attention on 800h caches, 5 sliding 256; vocab {cfg.vocab}, ffn {cfg.ffn}), "
-                        f"{E2E_R} seqs, prompts U[1K, 32K], {steps} steps",
-            "data": "synthetic N(0,1) K/V prompt histories, random token ids",
-            "tok_s": round(E2E_R * (steps - 1) / dt, 1), "ms_per_step": round(dt * 1e3 / (steps - 1), 3),
-            "steps": steps, "seqs": E2E_R, "context_tokens_end": int(ctx.sum())}
+    prompts = "U[1K, 32K]" if lens is None else f"{int(L0.min())}..{int(L0.max())} tokens"
+    out = {"workload": f"greedy decode, random-init LFM3-1.7B-shaped model (hidden 2048, 24 layers: 13 conv, "
+                       f"6 full attention on 800h caches, 5 sliding 256; vocab {cfg.vocab}, ffn {cfg.ffn}), "
+                       f"{R} seqs, prompts {prompts}, {steps} steps",
+           "data": "synthetic N(0,1) K/V prompt histories, random token ids",
+           "tok_s": round(R * (steps - 1) / dt, 1), "ms_per_step": round(dt * 1e3 / (steps - 1), 3),
+           "steps": steps, "seqs": R, "context_tokens_end": int(ctx.sum())}
+    del attn, model
+    torch.cuda.empty_cache()
+    return out
 
 
 def rope_tables(torch, n, dev):
@@ -330,7 +337,8 @@ def main():
     torch.cuda.set_device(dev)
 
     if a.e2e_only:
-        print(json.dumps({"e2e": bench_e2e(torch, dev, a.e2e_steps)}), flush=True)
+        print(json.dumps({"e2e": bench_e2e(torch, dev, a.e2e_steps),
+                          "e2e_398x32k": bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)}), flush=True)
         return
 
     if a.calib:
@@ -422,7 +430,7 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = c4 = e2e = None
+    flush_c2 = c4 = e2e = e2e_398 = None
     if not a.c3_only:
         flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
         cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
@@ -430,6 +438,8 @@ def main():
         del cos4, sin4
         torch.cuda.empty_cache()
         e2e = bench_e2e(torch, dev, a.e2e_steps)
+        e2e["workload"] = "C5: " + e2e["workload"]
+        e2e_398 = bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -447,6 +457,7 @@ def main():
         "flush_c2": flush_c2,
         "c4": c4,
         "e2e": e2e,
+        "e2e_398x32k": e2e_398,
     }
     print(json.dumps(res), flush=True)
 
