@@ -676,6 +676,9 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
         }
       }
     };
+    // wave priority by phase: of a SIMD's two waves, the one in its LDS -> VALU -> MFMA QK chain (3) or softmax (2)
+    // wins the issue slots over one in PV (0), whose MFMA chain then runs under it
+    __builtin_amdgcn_s_setprio(3);
     lookup(0, 0);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
@@ -699,6 +702,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
         }
       }
     }
+    __builtin_amdgcn_s_setprio(2);
     // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
     float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                        fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
@@ -726,6 +730,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     }
     // B in the K order of the A registers: (k0, k2), (k1, k3), (k4, k6), (k5, k7), token k of the group = slot 8 g + k
     const h8 Bw = pack8(pk2(wt[0][0], wt[0][2]), pk2(wt[0][1], wt[0][3]), pk2(wt[1][0], wt[1][2]), pk2(wt[1][1], wt[1][3]));
+    __builtin_amdgcn_s_setprio(0);
     // ---- PV per head: A row n = dim n of plane i, bytes of the group's 8 tokens by one transposed read
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
