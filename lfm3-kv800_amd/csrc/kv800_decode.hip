@@ -658,7 +658,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     // lane keeps only its own head's scores: after head h's two k-step pairs, column n's values move to sv when h == hn.
     f4 qa[2];
     float sv[2][4];   // raw scores (scale > 0 is applied inside the exponent)
-    uint32_t kk[2][2][4], an[2][2][4];   // [step parity][tile][e]
+    uint32_t kk[3][2][4], an[3][2][4];   // [step % 3][tile][e]
     auto lookup = [&](const int st, const int pb) {
       const int h = st >> 1, d = st & 1;
 #pragma unroll
@@ -680,10 +680,11 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     // wins the issue slots over one in PV (0), whose MFMA chain then runs under it
     __builtin_amdgcn_s_setprio(3);
     lookup(0, 0);
+    lookup(1, 1);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      if (st + 1 < 8) lookup(st + 1, (st + 1) & 1);
-      const int h = st >> 1, d = st & 1, pb = st & 1;
+      if (st + 2 < 8) lookup(st + 2, (st + 2) % 3);
+      const int h = st >> 1, d = st & 1, pb = st % 3;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         uint32_t c4[4], s4[4], ar[4];
