@@ -13,15 +13,17 @@ LFM3_KV800=1 (vllm_model.py:268-304): 24 layers of width 2048, each `h += post_n
 The vocabulary and feed-forward sizes are not in the reference (its weights are not available offline): 65,536 and
 8,192 here, about 1.67 B parameters. Weights are random N(0, 0.02) in bf16, norm weights 1.
 
-Attention goes through an object with begin_step(seq_lens_cpu) and attend(layer, q, k_pre, k_post, v) -> (R, 16, 128):
-PagedAttention800 (below) keeps vLLM's page geometry and runs every layer on libkv800_hip.so; tests substitute an
-oracle implementation to check the logits."""
+Attention goes through an object with begin_step() -> the new tokens' positions and attend(layer, q, k_pre, k_post, v)
+-> (R, 16, 128): PagedAttention800 (below) keeps vLLM's page geometry and runs every layer on libkv800_hip.so; tests
+substitute an oracle implementation to check the logits. Between the GEMMs, the model's elementwise work runs on the
+fused kernels of model_ops (include/lfm3_model.h)."""
 from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
 
 from . import kv800, kv800_hip
+from . import model_ops as mo
 from . import vllm_cache as vc
 
 CONV, FULL, SLIDE = "conv", "full", "slide"
@@ -50,30 +52,13 @@ class Lfm3Config:
         return CONV
 
 
-def rms_norm(x, w, eps):
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
-
-
-def _rotate_half(x):
-    h = x.shape[-1] // 2
-    return torch.cat((-x[..., h:], x[..., :h]), -1)
-
-
-class Rope:
-    """Neox RoPE over head_dim 128 as the reference computes it (vllm_model.py:106-151): angles in fp32, cos / sin rounded
-    to bf16, q / k rotated in fp32 and cast back. Full layers rotate 32 of the 64 frequencies (the rest are 0)."""
-
-    def __init__(self, theta, angles, device):
-        inv = 1.0 / (theta ** (torch.arange(0, 2 * angles, 2, dtype=torch.float32) / 128))
-        self.inv = torch.cat((inv, torch.zeros(64 - angles))).to(device)
-
-    def __call__(self, pos, *xs):
-        fr = pos.to(torch.float32)[:, None] * self.inv[None]
-        emb = torch.cat((fr, fr), -1)
-        c = emb.cos().to(torch.bfloat16).float()[:, None]
-        s = emb.sin().to(torch.bfloat16).float()[:, None]
-        return tuple((x.float() * c + _rotate_half(x.float()) * s).to(x.dtype) for x in xs)
+def model_rope_tables(theta, angles, n, device):
+    """(cos, sin) (n, 64) bf16 of the model's neox RoPE (vllm_model.py:106-151): frequency f < angles is
+    theta^(-2f/128), the rest 0 (cos 1, sin 0); angles in fp32, then bf16, as the reference's cos / sin caches."""
+    inv = 1.0 / (theta ** (torch.arange(0, 2 * angles, 2, dtype=torch.float32) / 128))
+    inv = torch.cat((inv, torch.zeros(64 - angles)))
+    fr = torch.arange(n, dtype=torch.float32)[:, None] * inv[None]
+    return fr.cos().to(torch.bfloat16).to(device), fr.sin().to(torch.bfloat16).to(device)
 
 
 def kernel_tables(n, device):
@@ -86,9 +71,12 @@ def kernel_tables(n, device):
 
 class Lfm3Decoder:
     """Random-init LFM3-shaped model for batched decode: step(tokens) appends one token to every row and returns the
-    logits. conv_state: per conv layer (R, hidden, conv_len - 1) bf16."""
+    logits. The dense products are torch GEMMs; everything between them is one fused HIP kernel (model_ops): the
+    sandwich norms with the residual add, the q / k norms with RoPE, the short-conv step, the gated activation and
+    the attention output gate. conv_state: per conv layer (R, hidden, conv_len - 1) bf16. max_pos bounds the
+    positions of the model's RoPE tables."""
 
-    def __init__(self, cfg: Lfm3Config, attention, rows, device, seed=0):
+    def __init__(self, cfg: Lfm3Config, attention, rows, device, seed=0, max_pos=65536):
         self.cfg, self.attn, self.R, self.dev = cfg, attention, rows, device
         g = torch.Generator(device=device).manual_seed(seed)
         H, D, G = cfg.hidden, cfg.head_dim, cfg.heads
@@ -99,6 +87,8 @@ class Lfm3Decoder:
         ones = lambda n: torch.ones(n, dtype=torch.bfloat16, device=device)
         self.embed = w(cfg.vocab, H)
         self.final_norm = ones(H)
+        self.tables = {FULL: model_rope_tables(1e6, 32, max_pos, device),
+                       SLIDE: model_rope_tables(1e4, 64, max_pos, device)}
         self.layers = []
         for l in range(cfg.layers):
             t = cfg.layer_type(l)
@@ -108,8 +98,9 @@ class Lfm3Decoder:
                 L.update(in_proj=w(3 * H, H), conv=w(H, cfg.conv_len), out_proj=w(H, H),
                          state=torch.zeros(rows, H, cfg.conv_len - 1, dtype=torch.bfloat16, device=device))
             else:
-                L.update(qkv=w((G + 2 * cfg.kv_heads) * D, H), q_norm=ones(D), k_norm=ones(D), gate=w(G, H),
-                         o_proj=w(H, G * D), rope=Rope(1e6, 32, device) if t == FULL else Rope(1e4, 64, device))
+                # q, k, v and the 16 output-gate logits from one product: rows [q | k | v | gate]
+                L.update(qkvg=torch.cat((w((G + 2 * cfg.kv_heads) * D, H), w(G, H))), q_norm=ones(D), k_norm=ones(D),
+                         o_proj=w(H, G * D))
             self.layers.append(L)
 
     def randomize_conv_states(self, seed):
@@ -118,37 +109,31 @@ class Lfm3Decoder:
             if L["type"] == CONV:
                 L["state"].copy_(torch.randn(L["state"].shape, generator=g, device=self.dev) * 0.1)
 
-    def _conv(self, L, h):
-        B_, C_, x = F.linear(h, L["in_proj"]).chunk(3, -1)
-        win = torch.cat((L["state"], (B_ * x).unsqueeze(-1)), -1)                 # (R, hidden, conv_len)
-        y = (win * L["conv"]).sum(-1)
-        L["state"].copy_(win[..., 1:])
-        return F.linear(C_ * y, L["out_proj"])
+    def _conv(self, L, n):
+        return F.linear(mo.conv_step(F.linear(n, L["in_proj"]), L["conv"], L["state"]), L["out_proj"])
 
-    def _attention(self, l, L, h, pos):
+    def _attention(self, l, L, n, pos):
         cfg = self.cfg
-        R, G, KV, D = h.shape[0], cfg.heads, cfg.kv_heads, cfg.head_dim
-        q, k, v = F.linear(h, L["qkv"]).split([G * D, KV * D, KV * D], -1)
-        q = rms_norm(q.reshape(R, G, D), L["q_norm"], cfg.eps)
-        k = rms_norm(k.reshape(R, KV, D), L["k_norm"], cfg.eps)
-        qr, kr = L["rope"](pos, q, k)
-        o = self.attn.attend(l, qr.contiguous(), k.contiguous(), kr.contiguous(), v.reshape(R, KV, D).contiguous())
-        o = o * torch.sigmoid(F.linear(h, L["gate"]).float()).to(o.dtype).unsqueeze(-1)
-        return F.linear(o.reshape(R, G * D), L["o_proj"])
+        qkvg = F.linear(n, L["qkvg"])                                                   # (R, 3088)
+        cos, sin = self.tables[L["type"]]
+        q, k_pre, k_rot, v = mo.qkv_post(qkvg, L["q_norm"], L["k_norm"], cos, sin, pos, cfg.eps)
+        o = self.attn.attend(l, q, k_pre, k_rot, v)
+        o = mo.gate_mul(o, qkvg[:, (cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim:])
+        return F.linear(o.reshape(o.shape[0], -1), L["o_proj"])
 
     def step(self, tokens, pos):
         """tokens (R,) int64, pos (R,) int64 the new tokens' positions (device); the attention object's begin_step
         has been called with the rows' lengths including this token. Returns (R, vocab) fp32 logits."""
         cfg = self.cfg
         x = self.embed[tokens]
+        _, n = mo.add_rmsnorm(None, x, None, self.layers[0]["norm"], cfg.eps)
         for l, L in enumerate(self.layers):
-            h = rms_norm(x, L["norm"], cfg.eps)
-            h = self._conv(L, h) if L["type"] == CONV else self._attention(l, L, h, pos)
-            x = x + rms_norm(h, L["post_norm"], cfg.eps)
-            h = F.linear(rms_norm(x, L["ffn_norm"], cfg.eps), L["w13"])
-            gte, up = h.chunk(2, -1)
-            x = x + rms_norm(F.linear(F.silu(gte) * up, L["w2"]), L["post_ffn_norm"], cfg.eps)
-        return F.linear(rms_norm(x, self.final_norm, cfg.eps), self.embed).float()
+            h = self._conv(L, n) if L["type"] == CONV else self._attention(l, L, n, pos)
+            x, n = mo.add_rmsnorm(h, x, L["post_norm"], L["ffn_norm"], cfg.eps)
+            h = F.linear(mo.silu_mul(F.linear(n, L["w13"])), L["w2"])
+            nxt = self.layers[l + 1]["norm"] if l + 1 < len(self.layers) else self.final_norm
+            x, n = mo.add_rmsnorm(h, x, L["post_ffn_norm"], nxt, cfg.eps)
+        return F.linear(n, self.embed).float()
 
 
 class PagedAttention800:

@@ -59,3 +59,17 @@ def test_plan(lib):
     assert ns.value * spb.value >= 19 and (ns.value - 1) * spb.value < 19
     assert lib.kv800_hip_plan(4, 0, ctypes.byref(ns), ctypes.byref(spb)) == 0 and ns.value == 0
     assert lib.kv800_hip_decode_workspace(64, 8, 0) >= 64 * 9 * 16 * 4 * 2 + 64 * 9 * 16 * 128 * 4
+
+
+def test_model_header_symbols_exported_and_bound(lib):
+    """include/lfm3_model.h (the engine loop's fused kernels): every declared entry point is exported by the same
+    library and bound by lfm3_kv800_amd.model_ops."""
+    import lfm3_kv800_amd.model_ops as mo
+    src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "lfm3_model.h")).read(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(lfm3_hip_\w+)\s*\(", src)))
+    assert len(names) == 5
+    out = subprocess.run(["nm", "-D", "--defined-only", kh.LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (lfm3_hip_\w+)", out))
+    assert not [n for n in names if n not in exported]
+    assert sorted(mo.SIGNATURES) == names
+    assert lib.lfm3_hip_silu_mul(None, 1, 7, None, None) == -1          # F not a multiple of 8: rejected on the host

@@ -149,3 +149,60 @@ def test_slide_layer_decode(hip, oracle):
     d = np.abs(got - want)
     say(f"slide layer: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
     assert np.isfinite(got).all() and d.max() < 2e-2 and d.mean() < 1e-3
+
+
+def test_fused_model_ops_match_torch(hip):
+    """The engine loop's fused kernels (model_ops) against the torch statements of the same ops on bf16 tensors, within
+    2 bf16 ulps per element (the kernels sum means and the 7-tap conv in their own fp32 order and use the hardware
+    exp)."""
+    import torch.nn.functional as F
+    from lfm3_kv800_amd import model as M
+    from lfm3_kv800_amd import model_ops as mo
+    g = torch.Generator(device=DEV).manual_seed(12)
+    R, H, FF, eps = 37, 2048, 8192, 1e-5
+    bf = lambda *s, scale=1.0: (torch.randn(*s, generator=g, device=DEV) * scale).to(torch.bfloat16)
+
+    def rms(x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(torch.bfloat16)
+
+    def close(a, b, what):
+        a, b = a.float(), b.float()
+        d = (a - b).abs()
+        bad = d > b.abs() * 2 ** -7 + 1e-30
+        say(f"{what}: max-abs {float(d.max()):.3e}, equal {float((d == 0).float().mean()):.4f}, over 2 ulp {int(bad.sum())}")
+        assert not bool(bad.any()), what
+
+    x, h, wp, wn = bf(R, H), bf(R, H), bf(H, scale=0.5) + 1, bf(H, scale=0.5) + 1
+    xo, no = mo.add_rmsnorm(h, x, wp, wn, eps)
+    x_ref = x + rms(h, wp)
+    close(xo, x_ref, "add_rmsnorm x"); close(no, rms(x_ref, wn), "add_rmsnorm n")
+    _, n0 = mo.add_rmsnorm(None, x, None, wn, eps)
+    close(n0, rms(x, wn), "rmsnorm")
+    gu = bf(R, 2 * FF, scale=3.0)
+    close(mo.silu_mul(gu), F.silu(gu[:, :FF]) * gu[:, FF:], "silu_mul")
+    qkvg = bf(R, 3088, scale=2.0)
+    qw, kw = bf(128, scale=0.3) + 1, bf(128, scale=0.3) + 1
+    pos = torch.randint(0, 40000, (R,), generator=g, device=DEV)
+    for theta, angles in ((1e6, 32), (1e4, 64)):
+        cos, sin = M.model_rope_tables(theta, angles, 40000, DEV)
+        q, kp, kr, v = mo.qkv_post(qkvg, qw, kw, cos, sin, pos, eps)
+        qn = rms(qkvg[:, :2048].reshape(R, 16, 128), qw)
+        kn = rms(qkvg[:, 2048:2560].reshape(R, 4, 128), kw)
+        c, s = cos[pos].float()[:, None], sin[pos].float()[:, None]
+        rot = lambda t: (t.float() * torch.cat((c, c), -1) +
+                         torch.cat((-t.float()[..., 64:], t.float()[..., :64]), -1) * torch.cat((s, s), -1)).to(torch.bfloat16)
+        close(q, rot(qn), f"qkv_post q theta {theta:g}"); close(kp, kn, "qkv_post k_pre")
+        close(kr, rot(kn), f"qkv_post k_rot theta {theta:g}")
+        assert torch.equal(v, qkvg[:, 2560:3072].reshape(R, 4, 128))
+    bcx, cw = bf(R, 3 * H), bf(H, 7, scale=0.3)
+    st = bf(R, H, 6)
+    st_ref = st.clone()
+    out = mo.conv_step(bcx, cw, st)
+    Bx = bcx[:, :H] * bcx[:, 2 * H:]
+    win = torch.cat((st_ref, Bx.unsqueeze(-1)), -1)
+    close(out, bcx[:, H:2 * H] * (win * cw).sum(-1), "conv_step out")
+    assert torch.equal(st, win[..., 1:])
+    o = bf(R, 16, 128)
+    close(mo.gate_mul(o, qkvg[:, 3072:]), o * torch.sigmoid(qkvg[:, 3072:].float()).to(torch.bfloat16).unsqueeze(-1),
+          "gate_mul")
