@@ -208,14 +208,16 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
 E2E_R, E2E_MIN, E2E_MAX = 256, 1024, 32768
 
 
-def bench_e2e(torch, dev, steps, lens=None, seed=51):
+def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
     """greedy decode of a random-init LFM3-1.7B-shaped model (lfm3-kv800_amd/model.py: 24 layers,
     13 short-conv, 6 full-attention on the 800h caches, 5 sliding-window; weights N(0, 0.02) bf16) over 256 sequences
     with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps; `lens` replaces the prompt lengths (the reference's
     published throughput point is 398 sequences of 32,768 tokens, RESULTS_RELEASE.md:90-96). tok/s = c (steps - 1) /
     time, time from the end of the first step to the end of the last (the reference's decode tok/s,
     RESULTS_RELEASE.md:83-85). The prompts' K / V histories are synthetic N(0, 1), written into the caches (quantized by
-    the HIP quantizer) before the first step: prompt processing is not part of the measurement."""
+    the HIP quantizer) before the first step: prompt processing is not part of the measurement. Each step is launched
+    kernel by kernel from the host (the loop is GPU-bound at these batch sizes: replaying one recorded HIP graph of the
+    step, graph=True / model.DecodeGraph, measured the same step time)."""
     import numpy as np
     from lfm3_kv800_amd import model as M
     cfg = M.Lfm3Config()
@@ -237,11 +239,17 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51):
     tokens = torch.randint(0, cfg.vocab, (R,), generator=g, device=dev)
     torch.cuda.synchronize()
     log(f"e2e: caches of {R} prompts ({int(L0.sum())} tokens) and weights ready in {time.perf_counter() - t:.1f} s")
-    tokens = model.step(tokens, attn.begin_step()).argmax(-1)        # first step: outside the measured window
+    # first step (and the recording of the graph): outside the measured window
+    if graph:
+        dg = M.DecodeGraph(model, attn, tokens, steps - 1)
+        advance = dg.step
+    else:
+        tokens = model.greedy(tokens, attn.begin_step())
+        advance = lambda: model.greedy(tokens, attn.begin_step())
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps - 1):
-        tokens = model.step(tokens, attn.begin_step()).argmax(-1)
+        tokens = advance()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     assert bool(((tokens >= 0) & (tokens < cfg.vocab)).all())
@@ -252,7 +260,8 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51):
                        f"{R} seqs, prompts {prompts}, {steps} steps",
            "data": "synthetic N(0,1) K/V prompt histories, random token ids",
            "tok_s": round(R * (steps - 1) / dt, 1), "ms_per_step": round(dt * 1e3 / (steps - 1), 3),
-           "steps": steps, "seqs": R, "context_tokens_end": int(ctx.sum())}
+           "steps": steps, "seqs": R, "context_tokens_end": int(ctx.sum()),
+           "launch": "one HIP graph per step" if graph else "eager"}
     del attn, model
     torch.cuda.empty_cache()
     return out

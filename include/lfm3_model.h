@@ -43,6 +43,11 @@ int lfm3_hip_conv_step(const uint16_t* bcx, int64_t stride, const uint16_t* conv
 /* Attention output gate: out (R, 16, 128) = o bf16(sigmoid(g)) per head; row r's 16 gate logits at g + r gstride. */
 int lfm3_hip_gate_mul(const uint16_t* o, const uint16_t* g, int64_t gstride, int64_t R, uint16_t* out, void* stream);
 
+/* Greedy token: out[r] (int64) = index of the largest of the V bf16 values of row r (row stride `stride` elements):
+ * among equal values the first, and a NaN ranks above every number (the first NaN wins), as torch.argmax over the
+ * same values. V and stride multiples of 8, x 16-byte aligned. */
+int lfm3_hip_argmax(const uint16_t* x, int64_t R, int64_t V, int64_t stride, int64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

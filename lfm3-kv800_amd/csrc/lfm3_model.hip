@@ -11,6 +11,7 @@
 //   conv_step     y = sum_k bf16(win_k w_k) over the 7-wide window [state | B x], state shifted, out = bf16(C y)
 //                 (the short-conv decode step, vllm_model.py:327-431)
 //   gate_mul      o bf16(sigmoid(g)) per head (the attention output gate)
+//   argmax        index of the largest bf16 logit of a row (the greedy token; torch.argmax's choice among equals)
 // rms(x) = x rsqrt(mean(x^2) + eps) in fp32. Sums run in a fixed tree order, so results equal torch's up to the
 // order of fp32 additions inside a mean or a 7-term sum.
 #include "kv800_common.h"
@@ -179,6 +180,46 @@ gate_mul_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ g, 
   store8(out + i, v);
 }
 
+// ---------------------------------------------------------------- greedy token (one workgroup of 256 threads per row)
+// (a, ia) ranks before (b, ib): the larger value, the smaller index among equals; NaN ranks above every number, the
+// first NaN first (torch.argmax)
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+// thread t scans the 8-element pieces t, t + 256, ... of the row in order; the workgroup then reduces the 256 bests
+__global__ void __launch_bounds__(256)
+argmax_kernel(const uint16_t* __restrict__ x, int64_t V, int64_t stride, int64_t* __restrict__ out) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const uint16_t* row = x + (int64_t)blockIdx.x * stride;
+  float bv = -INFINITY;
+  int bi = (int)V;   // ranks after every element
+  for (int64_t p = threadIdx.x; p * 8 < V; p += 256) {
+    float f[8];
+    load8(row + 8 * p, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (ranks_before(f[e], (int)(8 * p) + e, bv, bi)) { bv = f[e]; bi = (int)(8 * p) + e; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    if (ranks_before(v2, i2, bv, bi)) { bv = v2; bi = i2; }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { rv[w] = bv; ri[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 1; k < 4; ++k)
+      if (ranks_before(rv[k], ri[k], bv, bi)) { bv = rv[k]; bi = ri[k]; }
+    out[blockIdx.x] = bi;
+  }
+}
+
 }  // namespace
 }  // namespace lfm3
 
@@ -238,6 +279,15 @@ int lfm3_hip_gate_mul(const uint16_t* o, const uint16_t* g, int64_t gstride, int
   hipLaunchKernelGGL(gate_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, o, g,
                      gstride, R, out);
   return kv800::check_launch("gate_mul");
+}
+
+int lfm3_hip_argmax(const uint16_t* x, int64_t R, int64_t V, int64_t stride, int64_t* out, void* stream) {
+  KV800_REQUIRE(R >= 0 && V > 0 && V % 8 == 0 && V < (1LL << 31) && stride >= V && stride % 8 == 0,
+                "argmax: needs 0 < V < 2^31, V and the row stride multiples of 8");
+  if (R == 0) return KV800_OK;
+  KV800_REQUIRE(x && out && ((uintptr_t)x % 16) == 0, "argmax: null or misaligned pointer");
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)R), dim3(256), 0, (hipStream_t)stream, x, V, stride, out);
+  return kv800::check_launch("argmax");
 }
 
 }  // extern "C"

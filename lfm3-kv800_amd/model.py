@@ -16,7 +16,8 @@ The vocabulary and feed-forward sizes are not in the reference (its weights are 
 Attention goes through an object with begin_step() -> the new tokens' positions and attend(layer, q, k_pre, k_post, v)
 -> (R, 16, 128): PagedAttention800 (below) keeps vLLM's page geometry and runs every layer on libkv800_hip.so; tests
 substitute an oracle implementation to check the logits. Between the GEMMs, the model's elementwise work runs on the
-fused kernels of model_ops (include/lfm3_model.h)."""
+fused kernels of model_ops (include/lfm3_model.h). DecodeGraph captures one whole decode step (metadata, 24 layers,
+greedy token) as a HIP graph and replays it per step."""
 from dataclasses import dataclass
 
 import torch
@@ -121,9 +122,10 @@ class Lfm3Decoder:
         o = mo.gate_mul(o, qkvg[:, (cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim:])
         return F.linear(o.reshape(o.shape[0], -1), L["o_proj"])
 
-    def step(self, tokens, pos):
+    def step(self, tokens, pos, fp32=True):
         """tokens (R,) int64, pos (R,) int64 the new tokens' positions (device); the attention object's begin_step
-        has been called with the rows' lengths including this token. Returns (R, vocab) fp32 logits."""
+        has been called with the rows' lengths including this token. Returns (R, vocab) logits, fp32 (the bf16 LM-head
+        output widened) or, with fp32=False, bf16."""
         cfg = self.cfg
         x = self.embed[tokens]
         _, n = mo.add_rmsnorm(None, x, None, self.layers[0]["norm"], cfg.eps)
@@ -133,7 +135,13 @@ class Lfm3Decoder:
             h = F.linear(mo.silu_mul(F.linear(n, L["w13"])), L["w2"])
             nxt = self.layers[l + 1]["norm"] if l + 1 < len(self.layers) else self.final_norm
             x, n = mo.add_rmsnorm(h, x, L["post_ffn_norm"], nxt, cfg.eps)
-        return F.linear(n, self.embed).float()
+        logits = F.linear(n, self.embed)
+        return logits.float() if fp32 else logits
+
+    def greedy(self, tokens, pos):
+        """One step's greedy tokens (R,) int64: the first index of each row's largest logit (one HIP launch on the
+        bf16 logits, the same choice as argmax over their fp32 widening)."""
+        return mo.argmax(self.step(tokens, pos, fp32=False))
 
 
 class PagedAttention800:
@@ -185,6 +193,7 @@ class PagedAttention800:
             ev = torch.zeros(npages[self.group_of[l]], 4, ebs, 256, dtype=torch.bfloat16, device=device)
             self.layers[l] = vc.KV800SlideLayer(l, ev)
         self.metas = None
+        self.lens_dev = self.lens_bound = None   # set by freeze()
 
     # ---- prompt history
     def fill(self, history):
@@ -222,12 +231,25 @@ class PagedAttention800:
                         aux[:src.numel()] = src.reshape(-1)
 
     # ---- decode steps
+    def freeze(self, steps):
+        """Make the next `steps` decode steps replayable from one recorded step: the rows' lengths then advance on the
+        device (an add inside the step instead of a copy from the host), and the host values of the step metadata are
+        taken at the lengths after the last of those steps. Those values are bounds that hold for every step in
+        between: the largest flushed sub-block count (the width of the decode tables and the clamp of each row's own
+        count, which the kernels read on the device) and the rows of the sliding layers' identity tables."""
+        self.lens_dev = self.lens.to(self.dev)
+        self.lens_bound = self.lens + steps
+
     def begin_step(self):
         """Metadata of the next decode step (every row appends one token) and the start of its flushes."""
         self.lens += 1
-        dl = vc.step_lens(self.lens, self.dev)
-        me = {g: vc.step_meta(self.bt[g], self.lens, self.ebs, self.dev, dl) for g in self.bt}
-        mq = vc.step_meta(self.qbt, self.lens, vc.QBLOCK, self.dev, dl)
+        if self.lens_dev is None:
+            host, dl = self.lens, vc.step_lens(self.lens, self.dev)
+        else:
+            self.lens_dev += 1
+            host, dl = self.lens_bound, self.lens_dev
+        me = {g: vc.step_meta(self.bt[g], host, self.ebs, self.dev, dl) for g in self.bt}
+        mq = vc.step_meta(self.qbt, host, vc.QBLOCK, self.dev, dl)
         self.metas = (me, mq)
         full = [self.layers[l] for l in (2, 6, 10, 14, 18, 22)]
         vc.launch_flushes(full, {l.l: me[self.group_of[l.l]] for l in full}, mq)
@@ -241,12 +263,53 @@ class PagedAttention800:
         return layer.forward(q, k_pre, v, me[self.group_of[l]], mq, hosts=self.layers, cos_t=self.cos, sin_t=self.sin)
 
 
-def decode_loop(model, attention, tokens, steps, sync_every=0):
-    """Greedy decode: `steps` steps from `tokens` (R,) int64; returns the (steps, R) generated tokens."""
+class DecodeGraph:
+    """Greedy decode with one HIP graph per step. Construction runs the first step eagerly on the graph's own stream
+    (it builds the cached tables, library handles and the flush stream that the recorded step reuses; its tokens are
+    `tokens` afterwards, its bf16 logits `first_logits`), then freezes the attention for `steps` further steps and records
+    one step, whose input is the token buffer and whose greedy tokens are copied back into it. Each step() replays it:
+    one graph launch instead of ~250 kernel launches from the host. `tokens` and `logits` (the last replay's bf16
+    logits) are buffers that the next step overwrites. The attention must be a PagedAttention800."""
+
+    def __init__(self, model, attention, tokens, steps):
+        self.attn, self.left = attention, int(steps)
+        self.stream = torch.cuda.Stream(device=tokens.device)
+        self.stream.wait_stream(torch.cuda.current_stream(tokens.device))
+        with torch.cuda.stream(self.stream):
+            self.first_logits = model.step(tokens, attention.begin_step(), fp32=False)
+            self.tokens = mo.argmax(self.first_logits)
+        self.stream.synchronize()
+        attention.freeze(self.left)
+        lens = attention.lens.clone()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            logits = model.step(self.tokens, attention.begin_step(), fp32=False)
+            self.tokens.copy_(mo.argmax(logits))
+        attention.lens = lens          # recording ran no step
+        self.logits = logits
+        torch.cuda.current_stream(tokens.device).wait_stream(self.stream)
+
+    def step(self):
+        """One decode step: returns the (R,) greedy tokens."""
+        if self.left <= 0:
+            raise RuntimeError("DecodeGraph: the steps it was recorded for are used up")
+        self.left -= 1
+        self.attn.lens += 1
+        self.graph.replay()
+        return self.tokens
+
+
+def decode_loop(model, attention, tokens, steps, graph=False):
+    """Greedy decode: `steps` steps from `tokens` (R,) int64; returns the (steps, R) generated tokens. graph=True runs
+    the steps after the first as replays of one recorded step (DecodeGraph; PagedAttention800 only)."""
+    if graph and steps > 0:
+        dg = DecodeGraph(model, attention, tokens, steps - 1)
+        out = [dg.tokens.clone()]
+        for _ in range(steps - 1):
+            out.append(dg.step().clone())
+        return torch.stack(out)
     out = []
     for _ in range(steps):
-        pos = attention.begin_step()
-        logits = model.step(tokens, pos)
-        tokens = logits.argmax(-1)
+        tokens = model.greedy(tokens, attention.begin_step())
         out.append(tokens)
     return torch.stack(out)

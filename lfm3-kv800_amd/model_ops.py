@@ -15,6 +15,7 @@ SIGNATURES = {
     "lfm3_hip_qkv_post": (_I32, [_VP, _I64, _VP, _VP, _VP, _VP, _I64, _VP, _F32, _I64, _VP, _VP, _VP, _VP, _VP]),
     "lfm3_hip_conv_step": (_I32, [_VP, _I64, _VP, _VP, _I64, _I64, _VP, _VP]),
     "lfm3_hip_gate_mul": (_I32, [_VP, _VP, _I64, _I64, _VP, _VP]),
+    "lfm3_hip_argmax": (_I32, [_VP, _I64, _I64, _I64, _VP, _VP]),
 }
 _BOUND = {}
 
@@ -103,4 +104,14 @@ def gate_mul(o, g):
     o = _bf16(o, "o")
     out = torch.empty_like(o)
     kv800_hip._check(L.lfm3_hip_gate_mul(_ptr(o), _ptr(g), g.stride(0), o.shape[0], _ptr(out), _stream(o)))
+    return out
+
+
+def argmax(x):
+    """(R, V) bf16 -> (R,) int64 index of each row's largest value (torch.argmax(-1) of the same values)."""
+    L = _lib()
+    x = _bf16(x, "x")
+    R, V = x.shape
+    out = torch.empty(R, dtype=torch.int64, device=x.device)
+    kv800_hip._check(L.lfm3_hip_argmax(_ptr(x), R, V, x.stride(0), _ptr(out), _stream(x)))
     return out

@@ -7,7 +7,8 @@ bf16 rounding; the bar on the logits is rel-L2 2e-2 per step with the same greed
 with the top within the two models' largest logit difference).
 
 Also the native sliding layer alone (vllm_cache.KV800SlideLayer: window 256, no sinks, post-RoPE keys, identity RoPE
-tables) against the oracle, at the north-star bar."""
+tables) against the oracle, at the north-star bar; the decode steps replayed from one recorded HIP graph
+(model.DecodeGraph) against the same steps launched from the host; and the fused kernels against torch."""
 import numpy as np
 import pytest
 import torch
@@ -206,3 +207,78 @@ def test_fused_model_ops_match_torch(hip):
     o = bf(R, 16, 128)
     close(mo.gate_mul(o, qkvg[:, 3072:]), o * torch.sigmoid(qkvg[:, 3072:].float()).to(torch.bfloat16).unsqueeze(-1),
           "gate_mul")
+
+
+def _decode_setup(lens0, steps):
+    """A model and its paged attention with seeded weights, conv states and K / V histories (the same every call)."""
+    from lfm3_kv800_amd import model as M
+    cfg = M.Lfm3Config()
+    g = torch.Generator(device=DEV).manual_seed(21)
+
+    def history(l, r, p0, p1):
+        return (torch.randn((p1 - p0, 4, 128), generator=g, device=DEV).to(torch.bfloat16),
+                torch.randn((p1 - p0, 4, 128), generator=g, device=DEV).to(torch.bfloat16))
+
+    attn = M.PagedAttention800(lens0, steps, DEV, seed=3)
+    attn.fill(history)
+    model = M.Lfm3Decoder(cfg, attn, len(lens0), DEV, seed=5)
+    model.randomize_conv_states(6)
+    return model, attn
+
+
+def test_decode_graph_replays_match_eager(hip):
+    """DecodeGraph (the first step eager, the others replays of one recorded step, lengths advanced on the device and
+    the step metadata's host values taken at the last step's lengths) against the same steps launched one kernel at a
+    time from the host, on identical models and caches: every step's greedy tokens and bf16 logits equal bit for bit.
+    Eager GPU work and synchronisations run between the replays. Row 0 flushes a sub-block at the third step
+    (n = 1408 = 256 * 4 + 384) and row 3 crosses an exact page boundary."""
+    from lfm3_kv800_amd import model as M
+    from lfm3_kv800_amd import model_ops as mo
+    lens0, steps = [1405, 700, 2000, 127], 6
+    tok0 = torch.tensor([11, 22, 33, 44], dtype=torch.int64, device=DEV)
+    say("eager run", lens0, steps)
+    model, attn = _decode_setup(lens0, steps)
+    want, tok = [], tok0
+    for s in range(steps):
+        logits = model.step(tok, attn.begin_step(), fp32=False)
+        tok = mo.argmax(logits)
+        assert torch.equal(tok, logits.float().argmax(-1))
+        want.append((tok.clone(), logits.clone()))
+    torch.cuda.synchronize()
+    del model, attn
+    say("graph run")
+    model, attn = _decode_setup(lens0, steps)
+    dg = M.DecodeGraph(model, attn, tok0, steps - 1)
+    got = [(dg.tokens.clone(), dg.first_logits.clone())]
+    junk = torch.randn(512, 512, device=DEV)
+    for s in range(1, steps):
+        dg.step()
+        got.append((dg.tokens.clone(), dg.logits.clone()))
+        junk = (junk @ junk.t()).tanh()     # eager work between the replays
+        torch.cuda.synchronize()
+    assert int(attn.lens.sum()) == sum(lens0) + len(lens0) * steps
+    for s, ((tw, lw), (tg, lg)) in enumerate(zip(want, got)):
+        d = float((lw.float() - lg.float()).abs().max())
+        say(f"step {s}: tokens {tg.tolist()} (eager {tw.tolist()}), logits max-abs difference {d:.3e}")
+        assert torch.equal(tw, tg) and torch.equal(lw, lg), s
+    with pytest.raises(RuntimeError):
+        dg.step()
+
+
+def test_argmax_matches_torch(hip):
+    """The greedy-token kernel against torch.argmax over the same bf16 values: random rows, rows whose maximum is
+    repeated (the first index wins), rows with NaN (the first NaN wins), -inf / +inf rows and a strided view."""
+    from lfm3_kv800_amd import model_ops as mo
+    g = torch.Generator(device=DEV).manual_seed(3)
+    R, V = 9, 65536
+    x = torch.randn(R, V, generator=g, device=DEV).to(torch.bfloat16)
+    x[1, 100] = x[1, 40000] = x[1, 65535] = 50.0          # ties: first index
+    x[2].fill_(1.0)                                       # all equal: index 0
+    x[3, 7] = x[3, 9000] = float("nan")                   # NaN ranks first
+    x[4].fill_(float("-inf"))
+    x[5, 60000] = float("inf")
+    x[6, 65535] = 100.0                                   # the last element
+    for t in (x, torch.cat((x, x), 1)[:, 8:V + 8]):
+        got, want = mo.argmax(t), t.float().argmax(-1)
+        say("argmax", got.tolist(), want.tolist())
+        assert torch.equal(got, want)
