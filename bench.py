@@ -6,6 +6,9 @@ tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--e2e-only] [--e2e-steps S] [--calib]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
+Warm-up: the GPU reaches its sustained-load clocks only after tens of milliseconds of work (the first 50 C3 kernel
+launches after setup average 178 us, the following ones 152 us), so every timed section follows ~50-100 ms of its own
+untimed work: W = 500 layer steps and as many kernel launches for C3, 200 flushes for C2, 20 steps for C4.
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
 JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
 duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
@@ -327,7 +330,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
@@ -441,9 +444,9 @@ def main():
     extra_steps = max(5, min(a.steps, 20))
     flush_c2 = c4 = e2e = e2e_398 = None
     if not a.c3_only:
-        flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 2)
+        flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 200)
         cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
-        c4 = bench_c4(torch, kh, dev, extra_steps, 3, cos4, sin4)
+        c4 = bench_c4(torch, kh, dev, extra_steps, 20, cos4, sin4)
         del cos4, sin4
         torch.cuda.empty_cache()
         e2e = bench_e2e(torch, dev, a.e2e_steps)
