@@ -207,6 +207,17 @@ def test_fused_model_ops_match_torch(hip):
     o = bf(R, 16, 128)
     close(mo.gate_mul(o, qkvg[:, 3072:]), o * torch.sigmoid(qkvg[:, 3072:].float()).to(torch.bfloat16).unsqueeze(-1),
           "gate_mul")
+    # inputs of the wrong type or shape are rejected on the host, before any launch
+    with pytest.raises(TypeError):
+        mo.qkv_post(qkvg, qw, kw, cos, sin, pos.to(torch.int32), eps)
+    with pytest.raises(TypeError):
+        mo.conv_step(bcx, cw, st.float())
+    with pytest.raises(ValueError):
+        mo.conv_step(bcx[:, :3 * H - 8], cw, st)
+    with pytest.raises(ValueError):
+        mo.gate_mul(o, qkvg[:, 3072:3080])
+    with pytest.raises(ValueError):
+        mo.add_rmsnorm(h, x, wp[:1024], wn, eps)
 
 
 def _decode_setup(lens0, steps):
