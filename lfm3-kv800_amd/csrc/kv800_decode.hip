@@ -475,7 +475,7 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 // The table lookups of one instruction touch 4 tables (one per lane group) whose entries sit in disjoint LDS banks.
 constexpr int QWAVES = 4;
 constexpr float QLAZY = 7.f;   // p <= 2^7 and vsc <= 448 keep the fp16 weights p vsc below 65,504
-constexpr int64_t BAL_CHUNK = 16, BAL_GROUPS = 1536;   // balanced schedule: sub-blocks per workgroup, most workgroups
+constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 3;   // balanced schedule: sub-blocks per workgroup, most rounds
 constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
 constexpr int QROW = 132;
 constexpr int VBH = 34;        // staged vb rows per head: 32 + 2 of padding put head h + 2 16 banks away from head h
@@ -833,16 +833,27 @@ struct ExactArgs {
   int nexact, nsink;
 };
 
-// Balanced schedule (groups > 0): the B rows' sub-blocks laid end to end, q_b sub-blocks in row b, T = sum q_b. With
-// C = ceil(T / groups), row b is cut into n_b = ceil(q_b / C) slices of at most C sub-blocks, and the slices of all rows
-// are laid end to end: row b's at workgroup indices [pre[b], pre[b + 1]). Workgroup g takes one slice and writes its
-// partial to slot g; sum n_b <= T / C + B <= groups + B, so the grid has groups + B workgroups and the ones past the
-// last slice return at once. The exact partial of row b is slot groups + B + b. groups = 0: the fixed (row, split)
-// grid, split s of row b in slot b (ns + 1) + s, the exact partial in slot b (ns + 1) + ns (the reference's partial
-// layout).
+// Balanced schedule (groups > 0): the B rows' sub-blocks laid end to end, q_b sub-blocks in row b (clamped to
+// [0, cap]), T = sum q_b, C = ceil(T / groups). Two cuts of that list into pieces of at most C sub-blocks, the one
+// needing fewer rounds of resident workgroups taken (ties: row-wise):
+//   row-wise: row b is cut into ceil(q_b / C) slices, the slices of all rows laid end to end; workgroup g takes
+//     slice g (one row) and writes its partial to slot g. sum ceil(q_b / C) <= T / C + B <= groups + B, so the grid
+//     has groups + B workgroups and the ones past the last slice return at once.
+//   list-wise: workgroup g takes the list's sub-blocks [g C, (g + 1) C), which may end in a later row than they
+//     start; it attends each row segment in turn and writes one partial per segment, the first to slot g, each later
+//     one (which starts a row b) to slot groups + b, since no other workgroup enters row b from an earlier row. Every
+//     workgroup but the last has exactly C sub-blocks, however ragged the rows are.
+// Uniform rows whose count divides into whole rounds (64 x 127 sub-blocks: 8 slices of 16 a row, 512 workgroups,
+// one round) keep one segment per workgroup; otherwise the list-wise cut avoids a nearly empty last round (398 x 127:
+// 1592 slices of 33 is 4 rounds of 512, the list-wise cut 1532 pieces of 33, 3 rounds). The exact partial of row b is
+// slot groups + B + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact
+// partial in slot b (ns + 1) + ns (the reference's partial layout).
 struct Sched {
-  int32_t* pre;         // pre[0 .. B]: written by workgroup 0 of the decode grid, read by the merge
+  int32_t* pre;         // pre[0 .. B + 1], written by workgroup 0 of the decode grid for the merge: the row-wise cut's
+                        // slices before each row and pre[B + 1] = -C, or the list's sub-blocks before each row and
+                        // pre[B + 1] = C
   int groups, B, cap;   // cap: sub-blocks per row are clamped to [0, cap]
+  int res;              // workgroups of the grid resident at once (one round)
 };
 
 // The decode grid's workgroups each scan NQ themselves: thread t owns rows [t k, t k + k), k = ceil(B / 256), reads
@@ -851,7 +862,8 @@ struct Sched {
 constexpr int RREG = 4;
 struct RowTab {
   int wsum[4];
-  int b, pb, nsb;       // the row of this workgroup's slice, its first slice index, its clamped sub-block count
+  int b, pb, nsb, s1;   // the row of the current segment, its first sub-block in the list, its clamped sub-block
+                        // count; the end of the workgroup's sub-blocks in the list
 };
 struct RowCache {       // this thread's rows [r0, r1) and their clamped sub-block counts
   int r0, r1;
@@ -871,8 +883,8 @@ __device__ __forceinline__ int nsb_of(const int32_t* __restrict__ nq, const Sche
     if (k == i) x = C.v[k];
   return i < RREG ? x : min(max(nq[C.r0 + i], 0), S.cap);
 }
-__device__ __forceinline__ int slices_of(int nsb, int C) { return (nsb + C - 1) / C; }
 // Exclusive prefix of v over the workgroup's threads (in thread order); *total = the sum over all threads.
+__device__ __forceinline__ int slices_of(int nsb, int C) { return (nsb + C - 1) / C; }
 __device__ __forceinline__ int block_scan(int v, RowTab& R, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int x = v;
@@ -908,55 +920,91 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
     return;
   }
   const int blk = (int)blockIdx.x - X.nexact;
-  // fixed grid: (row b, split s); balanced: slice blk (one row's sub-blocks [j0, j1))
   int b, j0, j1;
   int64_t prow;
-  if (S.groups == 0) {
+  bool rowwise = true;   // one span per workgroup (the fixed grid, the row-wise cut)
+  __shared__ RowTab R;
+  if (S.groups == 0) {   // fixed grid: (row b, split s)
     b = blk / ns;
     const int s = blk % ns;
     j0 = s * spb;
     j1 = min(min((s + 1) * spb, nq[b]), (int)min(bstride, (int64_t)INT32_MAX));
     prow = ((int64_t)b * (ns + 1) + s) * 16;
-  } else {
-    __shared__ RowTab R;
+  } else {   // balanced: the row-wise or the list-wise cut of the rows' sub-blocks laid end to end
     RowCache RC;
     load_rows(nq, S, RC);
     int qsum = 0;
     for (int i = 0; i < RC.r1 - RC.r0; ++i) qsum += nsb_of(nq, S, RC, i);
     int T;
-    block_scan(qsum, R, &T);
-    if (T <= 0) {   // no quantized work in any row
-      if (blk == 0)
-        for (int r = threadIdx.x; r <= S.B; r += 256) S.pre[r] = 0;
-      return;
-    }
-    const int C = (T + S.groups - 1) / S.groups;
+    const int p = block_scan(qsum, R, &T);   // sub-blocks of the rows before this thread's rows
+    const int C = T > 0 ? (T + S.groups - 1) / S.groups : 1;
     int nsl = 0;
     for (int i = 0; i < RC.r1 - RC.r0; ++i) nsl += slices_of(nsb_of(nq, S, RC, i), C);
-    int G2;
-    int p = block_scan(nsl, R, &G2);
-    if (blk == 0) {   // pre[0 .. B] for the merge
-      if (threadIdx.x == 0) S.pre[0] = 0;
-      int pp = p;
+    int G1;
+    const int ps = block_scan(nsl, R, &G1);  // row-wise slices of the rows before this thread's rows
+    const int G2 = (T + C - 1) / C, res = max(S.res, 1);
+    rowwise = (G1 + res - 1) / res <= (G2 + res - 1) / res;
+    if (blk == 0) {   // pre[0 .. B + 1] for the merge
+      if (threadIdx.x == 0) { S.pre[0] = 0; S.pre[S.B + 1] = rowwise ? -C : C; }
+      int pp = rowwise ? ps : p;
       for (int i = 0; i < RC.r1 - RC.r0; ++i) {
-        pp += slices_of(nsb_of(nq, S, RC, i), C);
+        const int nb = nsb_of(nq, S, RC, i);
+        pp += rowwise ? slices_of(nb, C) : nb;
         S.pre[RC.r0 + i + 1] = pp;
       }
     }
-    if (blk >= G2) return;   // past the last slice (uniform over the workgroup)
-    for (int i = 0; i < RC.r1 - RC.r0; ++i) {   // exactly one thread owns the row of slice blk
-      const int nb = nsb_of(nq, S, RC, i), n = slices_of(nb, C);
-      if (p <= blk && blk < p + n) { R.b = RC.r0 + i; R.pb = p; R.nsb = nb; }
-      p += n;
+    if (rowwise) {   // slice blk: one row's sub-blocks [j0, j1)
+      if (blk >= G1) return;   // past the last slice (uniform over the workgroup)
+      int pp = ps;
+      for (int i = 0; i < RC.r1 - RC.r0; ++i) {   // exactly one thread owns the row of slice blk
+        const int nb = nsb_of(nq, S, RC, i), n = slices_of(nb, C);
+        if (pp <= blk && blk < pp + n) { R.b = RC.r0 + i; R.pb = pp; R.nsb = nb; }
+        pp += n;
+      }
+      __syncthreads();
+      b = __builtin_amdgcn_readfirstlane(R.b);
+      const int k = blk - __builtin_amdgcn_readfirstlane(R.pb);
+      j0 = C * k;
+      j1 = min(C * (k + 1), __builtin_amdgcn_readfirstlane(R.nsb));
+    } else {   // sub-blocks [blk C, (blk + 1) C) of the list
+      const int s0 = blk * C;
+      if (s0 >= T) return;   // past the last sub-block (uniform over the workgroup)
+      int pp = p;
+      for (int i = 0; i < RC.r1 - RC.r0; ++i) {   // exactly one thread owns the row holding sub-block s0
+        const int nb = nsb_of(nq, S, RC, i);
+        if (pp <= s0 && s0 < pp + nb) { R.b = RC.r0 + i; R.pb = pp; R.nsb = nb; }
+        pp += nb;
+      }
+      if (threadIdx.x == 0) R.s1 = min(T, s0 + C);
+      __syncthreads();
+      b = __builtin_amdgcn_readfirstlane(R.b);
+      const int st = __builtin_amdgcn_readfirstlane(R.pb);
+      j0 = s0 - st;
+      j1 = min(__builtin_amdgcn_readfirstlane(R.nsb), __builtin_amdgcn_readfirstlane(R.s1) - st);
     }
-    __syncthreads();
-    b = __builtin_amdgcn_readfirstlane(R.b);
-    const int k = blk - __builtin_amdgcn_readfirstlane(R.pb), nb = __builtin_amdgcn_readfirstlane(R.nsb);
-    j0 = C * k;
-    j1 = min(C * (k + 1), nb);
     prow = (int64_t)blk * 16;
   }
-  quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs2, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
+  // one span per row segment; between spans the segment state lives in R, so that only the span's own arguments stay
+  // in registers across it
+  for (;;) {
+    quant_span(lds_raw, q, qpool, qpool_bytes, boff, bstride, cs2, rope_rows, mo, lo_out, ao, scale, b, j0, j1, prow);
+    if (rowwise) return;
+    asm volatile("" ::: "memory");
+    const int st = __builtin_amdgcn_readfirstlane(R.pb), nb = __builtin_amdgcn_readfirstlane(R.nsb);
+    const int s1 = __builtin_amdgcn_readfirstlane(R.s1);
+    if (st + nb >= s1) return;   // the segment reached the end of the workgroup's sub-blocks
+    b = __builtin_amdgcn_readfirstlane(R.b);
+    int nb2;
+    do {   // the next row with sub-blocks (one exists: st + nb < s1 <= T)
+      ++b;
+      nb2 = min(max(nq[b], 0), S.cap);
+    } while (nb2 == 0);
+    __syncthreads();   // every wave has read R and is done with the span's end-of-span LDS
+    if (threadIdx.x == 0) { R.b = b; R.pb = st + nb; R.nsb = nb2; }
+    j0 = 0;
+    j1 = min(nb2, s1 - (st + nb));
+    prow = ((int64_t)S.groups + b) * 16;
+  }
 }
 
 
@@ -965,11 +1013,19 @@ __global__ void __launch_bounds__(256)
 decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
                     Sched S, uint16_t* __restrict__ out) {
   const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
-  // row b's quantized partials: slots first .. first + ns - 1; its exact partial: slot xs
-  int64_t first = (int64_t)b * (ns + 1), xs = first + ns;
-  if (S.groups > 0) {   // row b's slices are workgroups [pre[b], pre[b + 1]), one partial each
-    first = S.pre[b];
-    ns = S.pre[b + 1] - S.pre[b];
+  // row b's quantized partials: slots first .. first + ns - 1 (and slot extra); its exact partial: slot xs
+  int64_t first = (int64_t)b * (ns + 1), xs = first + ns, extra = -1;
+  if (S.groups > 0) {
+    const int cut = S.pre[S.B + 1];
+    if (cut < 0) {   // row-wise: row b's slices are workgroups [pre[b], pre[b + 1]), one partial each
+      first = S.pre[b];
+      ns = S.pre[b + 1] - S.pre[b];
+    } else {         // list-wise: row b holds sub-blocks [st, st + nb) of the list, workgroup g took [g C, (g + 1) C)
+      const int st = S.pre[b], nb = S.pre[b + 1] - st, C = cut;
+      first = (st + C - 1) / C;                                     // the workgroups that start inside the row
+      ns = nb > 0 ? (st + nb - 1) / C - (int)first + 1 : 0;
+      if (nb > 0 && st % C != 0) extra = (int64_t)S.groups + b;     // the one that entered it from an earlier row
+    }
     xs = (int64_t)S.groups + S.B + b;
   }
   const int64_t r0 = first * 16 + r;   // row of the first quantized partial; the next adds 16
@@ -982,6 +1038,19 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
   const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
   const float Mx = M;
   float Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, xe[8];
+  const bool anyq = ns > 0 || extra >= 0;
+  if (extra >= 0) {   // the entering workgroup's partial, folded first
+    const int64_t row = extra * 16 + r;
+    const float me = mo[row], le = lo[row];
+    const float4 e0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
+    const float4 e1 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
+    M = fmaxf(M, me);
+    const float wgt = exp2f(me - M);
+    const float a[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    Ls = wgt * le;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xq[e] = wgt * a[e];
+  }
   for (int s0 = 0; s0 < ns; s0 += 4) {   // quantized splits
     float mv[4], lv[4];
     float4 a0[4], a1[4];
@@ -1016,7 +1085,7 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
   }
-  if (ns > 0) {   // y = H x, d = 8 l16 + e: three in-lane stages, four across the 16-lane group
+  if (anyq) {   // y = H x, d = 8 l16 + e: three in-lane stages, four across the 16-lane group
 #pragma unroll
     for (int k = 0; k < 3; ++k)
 #pragma unroll
@@ -1039,8 +1108,8 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
   uint32_t o[4];
 #pragma unroll
   for (int e = 0; e < 8; e += 2) {
-    float y0 = (ns > 0 ? xq[e] * hn : 0.f) + xe[e];
-    float y1 = (ns > 0 ? xq[e + 1] * hn : 0.f) + xe[e + 1];
+    float y0 = (anyq ? xq[e] * hn : 0.f) + xe[e];
+    float y1 = (anyq ? xq[e + 1] * hn : 0.f) + xe[e + 1];
     y0 = Ls > 0.f ? y0 / Ls : 0.f;
     y1 = Ls > 0.f ? y1 / Ls : 0.f;
     o[e >> 1] = f2bf(y0) | (f2bf(y1) << 16);
@@ -1184,17 +1253,44 @@ int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows) {
   return align256(B * S * 16 * 4) * 2 + align256(B * S * 16 * 128 * 4) + align256(rope_rows * 32 * 4);
 }
 
+// Workgroups of decode_quant_kernel resident at once on the current device (its CUs x the kernel's workgroups per
+// CU), cached per device; 512 (MI355X: 256 CUs x 2) when the device cannot be queried.
+static int64_t resident_groups() {
+  static std::mutex mu;
+  static int64_t cache[64] = {0};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 512;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cu = 0, per = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(decode_quant_kernel), 256, 0) !=
+            hipSuccess ||
+        cu <= 0 || per <= 0) {
+      (void)hipGetLastError();
+      cache[dev] = 512;
+    } else {
+      cache[dev] = (int64_t)cu * per;
+    }
+  }
+  return cache[dev];
+}
+
 int64_t kv800_hip_decode_workspace_balanced(int64_t B, int64_t groups, int64_t rope_rows) {
   const int64_t S = 2 * B + groups;
-  return align256(S * 16 * 4) * 2 + align256(S * 16 * 128 * 4) + align256((B + 1) * 4) + align256(rope_rows * 32 * 4);
+  return align256(S * 16 * 4) * 2 + align256(S * 16 * 128 * 4) + align256((B + 2) * 4) + align256(rope_rows * 32 * 4);
 }
 
 int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
   KV800_REQUIRE(B >= 0 && nqmax >= 0 && groups, "plan_balanced: bad arguments");
-  // about BAL_CHUNK sub-blocks per workgroup (at most BAL_GROUPS workgroups) at the batch's largest size B * nqmax;
-  // ragged batches hold fewer sub-blocks, and each workgroup then takes proportionally fewer
-  const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK;
-  *groups = want < 1 ? 1 : want > BAL_GROUPS ? BAL_GROUPS : want;
+  // about BAL_CHUNK sub-blocks per workgroup at the batch's largest size B * nqmax (ragged batches hold fewer
+  // sub-blocks, and each workgroup then takes proportionally fewer); beyond one round of resident workgroups, whole
+  // rounds, at most BAL_ROUNDS
+  const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK, res = resident_groups();
+  *groups = want < 1 ? 1 : want <= res ? want : min((want + res - 1) / res, BAL_ROUNDS) * res;
   return KV800_OK;
 }
 
@@ -1238,6 +1334,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
     if (!G && (rc = kv800_hip_plan_balanced(B, nqmax, &G)) != KV800_OK) return rc;
     KV800_REQUIRE(B * nqmax < 0x7FFFFFFF - G && B < 0x7FFFFFFF / 2 - G, "decode: batch too large for the balanced schedule");
     S.groups = (int)G;
+    S.res = (int)resident_groups();
     ns = 1;
     sp = nqmax;
     slots = 2 * B + G;
@@ -1252,7 +1349,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   char* tail = ws + 2 * align256(slots * 16 * 4) + align256(slots * 16 * 128 * 4);
   if (S.groups) {
     S.pre = (int32_t*)tail;
-    tail += align256((B + 1) * 4);
+    tail += align256((B + 2) * 4);
   }
   uint32_t* cst = (uint32_t*)tail;
   if (!cs2) {
