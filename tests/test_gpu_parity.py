@@ -267,8 +267,8 @@ def test_decode_shuffled_ragged(hip, oracle, win):
 
 
 def test_decode_many_rows_few_groups(hip, oracle):
-    """Balanced schedule with workgroups spanning more rows than their 64-row offset table holds (the table is refilled
-    in rounds), rows without quantized sub-blocks between them, and row ranges that start and end inside rows."""
+    """Balanced schedule with few workgroups over 150 ragged rows: a single workgroup (one slice per row), slices that
+    start and end inside rows, rows without quantized sub-blocks between them."""
     rng = np.random.RandomState(57)
     lens = [int(x) for x in rng.randint(1, 1400, size=150)]
     lens[10:20] = [1, 2, 127, 128, 129, 383, 384, 385, 639, 640]
@@ -283,6 +283,27 @@ def test_decode_many_rows_few_groups(hip, oracle):
     for groups in (1, 2, 7, None):
         out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), groups=groups)
         close(bits_of(out), want, f"150 rows groups={groups}")
+
+
+def test_decode_list_wise_cut(hip, oracle):
+    """The balanced schedule's list-wise cut: 700 rows of 0-3 sub-blocks with group counts whose row-wise cut needs
+    two rounds of the 512 resident workgroups and the list-wise cut one, so the list-wise cut runs: workgroups whose
+    sub-blocks span 2 (groups 400) or ~7 rows (groups 97), each row segment its own partial, rows entered from an
+    earlier workgroup and rows without sub-blocks on the way."""
+    rng = np.random.RandomState(83)
+    lens = [int(x) for x in rng.randint(380, 1100, size=700)]
+    lens[::37] = [int(x) for x in rng.randint(1, 384, size=len(lens[::37]))]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (len(lens), 16, 128))
+    cos, sin = oracle.rope_tables(1200)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, ebs=128, shuffle_seed=83)
+    say("decode 700 rows list-wise, sub-blocks", int(case.NQ.sum()))
+    P = upload(case)
+    want = oracle.decode(case, q, cos, sin)
+    for groups in (400, 97):
+        out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), groups=groups)
+        close(bits_of(out), want, f"700 rows groups={groups}")
 
 
 def test_decode_batch_over_1024_rows(hip, oracle):
