@@ -467,14 +467,15 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 //   (lane group g: channels 8 g .. 8 g + 7, their rope pairs (dim j, dim j + 64) in two k-steps and nope pairs
 //   (j + 32, j + 96) in two more), B = q (column n = query row n, the same K order), so products are exact and sums
 //   fp32. Column n is meaningful for head h = n / 4 only; lane (g, n) keeps head n / 4's scores of tokens 4 g .. 4 g + 3.
-// - softmax: fp32, log2 units, lazy running max (rescale only when a chunk max exceeds it by more than QLAZY).
+// - softmax: fp32, log2 units, exact running max (the state is rescaled when a chunk max exceeds it): the largest
+//   score's p is exactly 1, so its P.V weight is its vsc, exactly.
 // - PV on MFMA f32_16x16x32_f16 in the Hadamard domain (kv800.py:157-168): A = 16 dims of one bit plane x the lane
 //   group's 8 tokens, read by one ds_read_b64_tr_b8 per head from the wave's LDS copy of the chunk's vb bytes; a bit
 //   becomes the fp16 subnormal 2^(i - 24) by one AND per two tokens; B = the weights fp16(p vsc) in head h's columns.
 //   Plane i is scaled back by 2^(24 - i) at the end; sum p vlo is kept per row.
 // The table lookups of one instruction touch 4 tables (one per lane group) whose entries sit in disjoint LDS banks.
 constexpr int QWAVES = 4;
-constexpr float QLAZY = 7.f;   // p <= 2^7 and vsc <= 448 keep the fp16 weights p vsc below 65,504
+constexpr float QLAZY = 0.f;   // rescale threshold (log2 units): p <= 2^QLAZY, and p vsc <= 448 stays far below 65,504
 constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 3;   // balanced schedule: sub-blocks per workgroup, most rounds
 constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
 constexpr int QROW = 132;
@@ -484,7 +485,7 @@ struct QWaveLds {
   float vs[2][64], vl[2][64];  // decoded vsc / vlo of the wave's 64 tokens, per head group
 };
 struct QLds {
-  uint32_t lut[2][LUT_WORDS];  // code tables of the current and the next sub-block
+  uint32_t lut[QWAVES][LUT_WORDS];  // each wave's code tables of the sub-block it is in
   QWaveLds wv[QWAVES];
 };
 struct QFinLds {               // end-of-span merge of the 4 waves (reuses the LDS)
@@ -533,36 +534,45 @@ __device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
 }
 __device__ __forceinline__ b8 pack8b(const uint32_t (&x)[4]) { return as_b8(u4v{x[0], x[1], x[2], x[3]}); }
 
-// The K scale bytes table t needs: klo / ksc of its two dims (kind 0: dims j, j + 64; kind 1: j + 32, j + 96), head h,
-// as four separate loads (combined only when the table is built, a sub-block after they are issued).
-struct TabBytes { uint32_t la, lb, sa, sb; };
-__device__ __forceinline__ TabBytes table_bytes(const uint8_t* __restrict__ sb, int t) {
-  const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31;
-  const uint8_t* p = sb + KLO_O + 128 * h + 32 * kind + j;
-  return TabBytes{p[0], p[64], p[KSC_O - KLO_O], p[KSC_O - KLO_O + 64]};
+// The K scale bytes of the 4 tables lane l builds, t = 4 l + e (kind t >> 7 = l >> 5, head (t >> 5) & 3, channel
+// t & 31 = 4 (l & 7) + e): klo / ksc of the tables' two dims (kind 0: dims j, j + 64; kind 1: j + 32, j + 96) for 4
+// consecutive channels, one aligned dword each, byte e for table e (combined only when the tables are built, a
+// pair of chunks after they are issued).
+struct TabWords { uint32_t la, lb, sa, sb; };
+__device__ __forceinline__ TabWords table_words(const uint8_t* __restrict__ sb, int lane) {
+  const uint8_t* p = sb + KLO_O + 128 * ((lane >> 3) & 3) + 32 * (lane >> 5) + 4 * (lane & 7);
+  return TabWords{*reinterpret_cast<const uint32_t*>(p), *reinterpret_cast<const uint32_t*>(p + 64),
+                  *reinterpret_cast<const uint32_t*>(p + KSC_O - KLO_O),
+                  *reinterpret_cast<const uint32_t*>(p + KSC_O - KLO_O + 64)};
 }
-// Table t of one LUT buffer: entry (ca, cb) = bf16(ca ksc_a + klo_a) | bf16(cb ksc_b + klo_b) << 16 (kv800.py:84-86:
+// Table t of a wave's LUT: entry (ca, cb) = bf16(ca ksc_a + klo_a) | bf16(cb ksc_b + klo_b) << 16 (kv800.py:84-86:
 // the product is exact in fp32, so the fused multiply-add rounds where torch's add does). The tables of channels
 // 8 g + 4 d + e, e < 4, fill the 256-byte block ((kind 4 + h) 2 + d) 4 + g, table e in its 64-byte slot e ^ (g & 1),
 // entry (ca, cb) at dword ca + 4 cb of the slot: the 32 lanes of a half-wave read two lane groups' tables, whose 16
 // entries each occupy one half of the 32 LDS banks.
-__device__ __forceinline__ void lut_build(uint32_t* lut, int t, const TabBytes& tb) {
-  float v[4];
-  f8x4(tb.la | (tb.lb << 8) | (tb.sa << 16) | (tb.sb << 24), v);   // klo_a, klo_b, ksc_a, ksc_b
-  const int kind = t >> 7, h = (t >> 5) & 3, j = t & 31, g = j >> 3, d = (j >> 2) & 1, e = j & 3;
-  uint32_t pa[4];
+__device__ __forceinline__ void lut_build4(uint32_t* lut, int lane, const TabWords& tw) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
-  uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 16 * (e ^ (g & 1));
-  // row cb of the table at dword 4 cb; write k stores row (k + r) & 3 with r = (j >> 1) & 3, so that the 8 lanes of
-  // one 128-byte write cycle (same g, e and d varying) cover the 32 banks once: bank 16 (slot & 1) + 4 row + 0..3
-  const int r = (j >> 1) & 3;
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t sel = 0x0C0C0000u | ((uint32_t)(4 + e) << 8) | (uint32_t)e;
+    const uint32_t x = __builtin_amdgcn_perm(tw.lb, tw.la, sel) | (__builtin_amdgcn_perm(tw.sb, tw.sa, sel) << 16);
+    float v[4];
+    f8x4(x, v);   // klo_a, klo_b, ksc_a, ksc_b
+    const int t = 4 * lane + e, kind = t >> 7, h = (t >> 5) & 3, j = t & 31, g = j >> 3, d = (j >> 2) & 1;
+    uint32_t pa[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int cb = (k + r) & 3;
-    const uint32_t hi = (cb & 2 ? (cb & 1 ? pa[3] : pa[2]) : (cb & 1 ? pa[1] : pa[0])) & 0xFFFF0000u;
-    *reinterpret_cast<u4v*>(tab + 4 * cb) =
-        u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
+    for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
+    uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 16 * (e ^ (g & 1));
+    // row cb of the table at dword 4 cb; write k stores row (k + r) & 3 with r = d | (j >> 3 & 2): the 8 lanes of one
+    // 128-byte write cycle (lanes 8 m .. 8 m + 7: same kind, head and e) then cover the 32 banks once, bank group
+    // 4 (slot & 1) + row
+    const int r = d | ((j >> 3) & 2);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int cb = (k + r) & 3;
+      const uint32_t hi = (cb & 2 ? (cb & 1 ? pa[3] : pa[2]) : (cb & 1 ? pa[1] : pa[0])) & 0xFFFF0000u;
+      *reinterpret_cast<u4v*>(tab + 4 * cb) =
+          u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
+    }
   }
 }
 // vlo / vsc bytes of token t (both head groups)
@@ -704,11 +714,11 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       }
     }
     __builtin_amdgcn_s_setprio(2);
-    // ---- online softmax over the chunk's 32 tokens (lazy max); row = column n, tokens 4 g + i of each tile
+    // ---- online softmax over the chunk's 32 tokens; row = column n, tokens 4 g + i of each tile
     float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                        fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
     tmax = max4rows(tmax) * scale;
-    if (__any(tmax > m + QLAZY)) {   // lazy running max: rescale only when a chunk max exceeds m by more than QLAZY
+    if (__any(tmax > m + QLAZY)) {   // a chunk max above the running max: rescale (a wave-uniform branch)
       const float mn = fmaxf(m, tmax);
       const float al = __builtin_amdgcn_exp2f(m - mn);   // v_exp_f32; tiny results flush to 0
       m = mn; lsum *= al; lvs *= al;
@@ -750,38 +760,47 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   };
 
   if (j0 < j1) {
+    // The span's 4 (j1 - j0) pairs of 32-token chunks: wave w takes pairs [len w, len (w + 1)), pair P being tokens
+    // 64 (P % 4) .. + 63 of sub-block j0 + P / 4. The wave builds its own code tables for each sub-block it enters,
+    // so the waves never wait for each other until the span's end.
     const int64_t* brow = boff + (int64_t)b * bstride;
     auto sanitize = [&](int64_t raw, int jb) -> int64_t {
       return (raw < 0 || raw > qpool_bytes - SUB || (int64_t)(jb + 1) * BLK > rope_rows) ? -1 : raw;
     };
-    int64_t base = sanitize(brow[j0], j0);
-    int64_t nraw = brow[min(j0 + 1, j1 - 1)];   // the next sub-block's offset, loaded one sub-block ahead of its use
+    const int len = j1 - j0, P0 = len * w, P1 = P0 + len;
+    int jb = j0 + P0 / 4, pin = P0 % 4;
+    int64_t base = sanitize(brow[jb], jb);
+    int64_t nraw = brow[min(jb + 1, j1 - 1)];   // the next sub-block's offset, loaded a sub-block ahead of its use
     const uint8_t* sb = qpool + (base < 0 ? 0 : base);
+    uint32_t* lut = L.lut[w];
+    const uint32_t gw = (((uint32_t)w << 6) | (uint32_t)g) << 8;   // byte 1: the wave's LUT and the lane group
     QChunk C0, C1;
-    qload(C0, sb, cs2 + (int64_t)(base < 0 ? 0 : j0) * BLK * 32, 64 * w, lane);
-    lut_build(L.lut[0], tid, table_bytes(sb, tid));
-    stage_scales(scale_bytes(sb, 64 * w + lane));
-    __syncthreads();
-    uint32_t buf = 0;
-    for (int jb = j0; jb < j1; ++jb) {
-      const bool more = jb + 1 < j1;
-      const int64_t nbase = more ? sanitize(nraw, jb + 1) : -1;
-      nraw = brow[min(jb + 2, j1 - 1)];
-      const uint8_t* nsb = qpool + (nbase < 0 ? 0 : nbase);
-      // the next sub-block's scale bytes (read unconditionally; used after this sub-block's chunks)
-      const TabBytes ntb = table_bytes(nsb, tid);
-      const uint32_t nsc = scale_bytes(nsb, 64 * w + lane);
-      const uint32_t gw = ((buf << 6) | (uint32_t)g) << 8;   // byte 1: LUT buffer and lane group (256-byte blocks)
-      qload(C1, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * w + 32, lane);
+    qload(C0, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * pin, lane);
+    lut_build4(lut, lane, table_words(sb, lane));
+    stage_scales(scale_bytes(sb, 64 * pin + lane));
+    for (int P = P0; P < P1; ++P) {
+      const bool more = P + 1 < P1, cross = more && pin == 3;   // the next pair is in the next sub-block
+      const int njb = cross ? jb + 1 : jb, npin = cross ? 0 : (pin + 1) & 3;
+      int64_t nbase = base;
+      const uint8_t* nsb = sb;
+      if (cross) {
+        nbase = sanitize(nraw, njb);
+        nsb = qpool + (nbase < 0 ? 0 : nbase);
+        nraw = brow[min(njb + 1, j1 - 1)];
+      }
+      // the next sub-block's table words (used after this pair's chunks) and the next pair's scale bytes
+      const TabWords ntw = table_words(nsb, lane);
+      const uint32_t nsc = scale_bytes(nsb, 64 * npin + lane);
+      qload(C1, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * pin + 32, lane);
       if (base >= 0) chunk(C0, 0, gw);
-      qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : jb + 1) * BLK * 32, 64 * w, lane);
+      qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : njb) * BLK * 32, 64 * npin, lane);
       if (base >= 0) chunk(C1, 1, gw);
-      if (more) {
-        lut_build(L.lut[buf ^ 1u], tid, ntb);
+      if (more) {   // the wave's own LDS: its lookups and scale reads of this pair were issued before these writes
+        if (cross) lut_build4(lut, lane, ntw);
         stage_scales(nsc);
       }
-      __syncthreads();
-      buf ^= 1u;
+      jb = njb;
+      pin = npin;
       base = nbase;
       sb = nsb;
     }

@@ -6,8 +6,9 @@ the same bytes.
     path converts scale bytes with the hardware fp8 conversion, the oracle with integer arithmetic
     (kv800.py:83-91 decodes them through torch's float8_e4m3fn);
   * the fp16 P.V weights p * vsc at their largest: vsc = 448 on every token and a score that climbs by just under, and
-    by just over, the lazy-rescale threshold (7 log2 units) from one sub-block to the next, so the unrescaled
-    probabilities reach 2^6.98 and 448 * 2^6.98 = 56,500 sits just below the fp16 maximum 65,504.
+    by just over, 7 log2 units from one sub-block to the next (the kernel's running max rescales on every new maximum,
+    so p <= 1 and the weights stay <= 448; the climb also exercises the rescale of a state built from probabilities
+    2^-7 below the new maximum).
 
 Bar: finite outputs and rel-L2 < 1e-2 per row against the oracle (the reference's own decode bar,
 tests/test_parity.py:104); the outputs reach magnitudes of hundreds here, where an absolute 2e-2 is below one bf16
