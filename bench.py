@@ -428,15 +428,15 @@ def main():
 
     achieved = QBYTES / (ms_quant * 1e-3) / 1e9
     layer_gbps = ALG_BYTES / (ms_step * 1e-3) / 1e9
-    cpu = None
-    if not a.no_cpu:
-        rows = max(1, min(B, a.cpu_rows))
-        (dt, cores), (dt_c, cores_c) = cpu_baseline(torch, layers[0], q, cos, sin, rows)
-        cpu = {"value": round(dt * 1e3 * B / rows, 1), "unit": "ms/layer (64x32K, scaled from the sample)",
-               "cores": cores, "cpu_model": cpu_model(), "kind": "port",
-               "sample": f"pure-torch restatement of torch_decode.decode (oracle/torch_port.py) on rows 0..{rows - 1} "
-                         f"of the 64 x 32768 layer, {cores} torch threads: {dt:.2f} s, scaled by 64/{rows}",
-               "c_oracle_ms_per_layer": round(dt_c * 1e3 * B / rows, 1), "c_oracle_threads": cores_c}
+    # the CPU baseline runs last, on a host copy of the layer: its 16 busy threads would otherwise share the host with
+    # the launches of the GPU sections below (a C4 step issues ~60 launches)
+    from types import SimpleNamespace
+    P0 = layers[0]
+    C = lambda t: t.detach().cpu() if t is not None else None
+    host_layer = SimpleNamespace(qpool=C(P0.qpool), boff=C(P0.boff), epool=C(P0.epool), eoff=C(P0.eoff), ebs=P0.ebs,
+                                 e_hs=P0.e_hs, e_ts=P0.e_ts, e_v=P0.e_v, sk=None, sv=None, skoff=None, svoff=None,
+                                 N=C(P0.N), NQ=C(P0.NQ), nqmax=P0.nqmax, win=P0.win) if not a.no_cpu else None
+    host_q, host_cos, host_sin = C(q), C(cos), C(sin)
 
     # ---- the other BASELINE configs with a GPU workload: C2 (flush alone) and C4 (6-layer decode step)
     del layers, structs
@@ -452,6 +452,15 @@ def main():
         e2e = bench_e2e(torch, dev, a.e2e_steps)
         e2e["workload"] = "C5: " + e2e["workload"]
         e2e_398 = bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)
+    cpu = None
+    if not a.no_cpu:
+        rows = max(1, min(B, a.cpu_rows))
+        (dt, cores), (dt_c, cores_c) = cpu_baseline(torch, host_layer, host_q, host_cos, host_sin, rows)
+        cpu = {"value": round(dt * 1e3 * B / rows, 1), "unit": "ms/layer (64x32K, scaled from the sample)",
+               "cores": cores, "cpu_model": cpu_model(), "kind": "port",
+               "sample": f"pure-torch restatement of torch_decode.decode (oracle/torch_port.py) on rows 0..{rows - 1} "
+                         f"of the 64 x 32768 layer, {cores} torch threads: {dt:.2f} s, scaled by 64/{rows}",
+               "c_oracle_ms_per_layer": round(dt_c * 1e3 * B / rows, 1), "c_oracle_threads": cores_c}
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
