@@ -47,6 +47,7 @@ struct DenseSrc {   // (M, 256, 4, 128) contiguous K and V
   const uint16_t* k;
   const uint16_t* v;
   int64_t m;
+  __device__ void prepare(int64_t*) {}
   __device__ const uint16_t* krow(int t, int h) const { return k + ((m * BLK + t) * 4 + h) * 128; }
   __device__ const uint16_t* vrow(int t, int h) const { return v + ((m * BLK + t) * 4 + h) * 128; }
 };
@@ -55,10 +56,17 @@ struct PagedSrc {   // exact pages: K of (position p, head h) at eoff[r, p / ebs
   const uint16_t* ep;
   const int64_t* et;   // this row's page table
   int64_t ebs, e_hs, e_ts, e_v, p0;
-  __device__ const uint16_t* krow(int t, int h) const {
-    const int64_t p = p0 + t;
-    return ep + et[p / ebs] + h * e_hs + (p % ebs) * e_ts;
+  const int64_t* rowoff = nullptr;   // LDS: element offset of token t's head-0 K row, t < 256
+  // One page-table lookup and division per token for the whole workgroup (every thread must call it).
+  __device__ void prepare(int64_t* tab) {
+    for (int t = threadIdx.x; t < BLK; t += blockDim.x) {
+      const int64_t p = p0 + t;
+      tab[t] = et[p / ebs] + (p % ebs) * e_ts;
+    }
+    __syncthreads();
+    rowoff = tab;
   }
+  __device__ const uint16_t* krow(int t, int h) const { return ep + rowoff[t] + h * e_hs; }
   __device__ const uint16_t* vrow(int t, int h) const { return krow(t, h) + e_v; }
 };
 
@@ -139,12 +147,6 @@ __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
   return x;
-}
-
-// bits jj, jj + 16, jj + 32, jj + 48 of m gathered into bits 0..3
-__device__ __forceinline__ uint32_t gather4(uint64_t m, int jj) {
-  const uint64_t x = (m >> jj) & 0x0001000100010001ull;
-  return (uint32_t)((x | (x >> 15) | (x >> 30) | (x >> 45)) & 0xFull);
 }
 
 struct QuantLds {                  // K path: per-wave min / max partials, then per-column lo and divisor
@@ -237,66 +239,126 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
   }
 }
 
-// V bits and scales of tokens [t0, t0 + VTOK) of one sub-block: wave w takes VTPW consecutive tokens, per token its
-// 4 head rows with lane = dims lane, lane + 64. Each lane loads 16 bytes of a token's rows (head rh, dims rc .. +7),
-// two tokens ahead; the wave writes them as floats into its own 2 KB of LDS, and the rows' Hadamard chains run from
-// there two at a time (hadamard_chain2).
+// ---------------------------------------------------------------- V path
+// One lane owns 8 dims of one head row: lane = 16 hh + jj computes head hh's dims jj + 16 i (i = 0..7), which are
+// exactly the 8 bits of the row's code byte jj. For k = 16 m + kl (m, i < 8, kl < 16),
+// H[k][jj + 16 i] = H[kl][jj] (-1)^popcount(m & i), so the lane keeps the 16 values H[kl][jj] and every other sign is
+// a compile-time negation.
+__device__ __forceinline__ void hadamard_low(float (&hl)[16], int jj) {
+  const float c = __uint_as_float(0x3DB504F3u);   // fp32(1 / sqrt(128))
+#pragma unroll
+  for (int kl = 0; kl < 16; ++kl) hl[kl] = (__builtin_popcount(kl & jj) & 1) ? -c : c;
+}
+
+__device__ __forceinline__ constexpr bool hneg(int m, int i) { return __builtin_popcount(m & i) & 1; }
+
+// y[i] = sum_k x[k] H[k][jj + 16 i], each output by torch-CPU's sequential fma chain over k = 0..127. Outputs whose
+// signs agree on a prefix of k share its partial sums: one chain for k < 16, two for k < 32 (by i & 1), four for
+// k < 64 (by i & 3), eight after (688 fmas for the 8 outputs instead of 1024). x (the lane's staged row) is read one
+// float4 at a time, two reads ahead of their use.
+__device__ __forceinline__ void hadamard_row8(const float* x, const float (&hl)[16], float (&y)[8]) {
+  float4 buf[3];
+  buf[0] = *reinterpret_cast<const float4*>(x);
+  buf[1] = *reinterpret_cast<const float4*>(x + 4);
+  float ch[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 32; ++g) {   // k = 4 g .. 4 g + 3
+    if (g + 2 < 32) buf[(g + 2) % 3] = *reinterpret_cast<const float4*>(x + 4 * (g + 2));
+    const float4 v = buf[g % 3];
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    const int m = g >> 2;   // k >> 4
+    if (g == 4) ch[1] = ch[0];
+    if (g == 8) { ch[2] = ch[0]; ch[3] = ch[1]; }
+    if (g == 16) { ch[4] = ch[0]; ch[5] = ch[1]; ch[6] = ch[2]; ch[7] = ch[3]; }
+    const int nch = m == 0 ? 1 : m == 1 ? 2 : m < 4 ? 4 : 8;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h = hl[(4 * g + e) & 15];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < nch) ch[i] = __builtin_fmaf(xv[e], hneg(m, i) ? -h : h, ch[i]);
+    }
+    // the group's fmas stay before this point and the next group's reads after it: two reads ahead, no further
+    asm volatile("" : "+v"(ch[0]), "+v"(ch[1]), "+v"(ch[2]), "+v"(ch[3]), "+v"(ch[4]), "+v"(ch[5]), "+v"(ch[6]),
+                 "+v"(ch[7])::"memory");
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = ch[i];
+}
+
+// min over each 16-lane row, the result in every lane of the row (quad swaps, then half-row and row mirrors)
+__device__ __forceinline__ float row_min16(float x) {
+  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0xB1, 0xF, 0xF, false)));
+  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x4E, 0xF, 0xF, false)));
+  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x141, 0xF, 0xF, false)));
+  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x140, 0xF, 0xF, false)));
+  return x;
+}
+
+// V bits and scales of tokens [t0, t0 + VT * QW) of one sub-block: wave w takes VT consecutive tokens, one token (its
+// 4 head rows) per step. Each lane loads 16 bytes of the token's rows (head hh, dims 8 jj .. 8 jj + 7), two tokens
+// ahead; the wave writes them as floats into its own LDS rows, and each lane runs its row's 8-output chain from there.
+// Per (token, 2-head group) -- lanes 32 g .. 32 g + 31 -- the min / max of the 256 outputs go through a 16-row swap and
+// DPP row reductions; the token's four scale bytes (lo and scale of each group) are encoded by lanes 0..3 at once.
+// bit = rne(fl(d / den)) >= 1 with d = fl(y - lo) is evaluated without the division as fl(d - den / 2) > den 2^-25: the
+// quotient rounds above 1/2 exactly when d / den > 1/2 + 2^-25, and near that point d - den / 2 is exact (Sterbenz) and a
+// small multiple of half an ulp of den / 2, so the comparison is exact; far from it rounding keeps the sign of the
+// margin (den >= 1e-8 is normal, and a NaN den or d gives 0 both ways).
 constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
-constexpr int VLDS_BYTES = QW * 4 * 128 * 4;   // per wave: the current token's 4 rows as floats
+constexpr int VROW = 132;   // floats per staged row: the 4 rows of a token start on different LDS banks
+constexpr int VLDS_BYTES = QW * 4 * VROW * 4;
 
 template <int VT, typename Src>
 __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int tw = t0 + VT * w;                        // this wave's first token; VT tokens per wave
-  const int rh = lane >> 4, rc = 8 * (lane & 15);    // the 16 bytes this lane loads: head rh, dims rc .. rc + 7
-  float (*xs)[128] = reinterpret_cast<float (*)[128]>(lds) + 4 * w;
-  auto fetch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, rh) + rc); };
+  const int tw = t0 + VT * w;                    // this wave's first token
+  const int hh = lane >> 4, jj = lane & 15;      // head row and code byte of this lane
+  float* xrow = reinterpret_cast<float*>(lds) + (w * 4 + hh) * VROW;
+  auto fetch = [&](int t) { return *reinterpret_cast<const uint4*>(src.vrow(t, hh) + 8 * jj); };
   uint4 pf0 = fetch(tw), pf1 = VT > 1 ? fetch(tw + 1) : pf0;
-  float hcol[64];
-  hadamard_column(hcol, lane);
+  float hl[16];
+  hadamard_low(hl, jj);
+  const int q = lane & 3, g = lane >> 5;
 #pragma unroll 1
   for (int tt = 0; tt < VT; ++tt) {
     const int t = tw + tt;
-    // token t's rows -> xs (a wave's LDS instructions execute in order: these stores follow the previous token's
+    // token t's rows -> LDS (a wave's LDS instructions execute in order: these stores follow the previous token's
     // reads and precede this token's)
-    *reinterpret_cast<float4*>(xs[rh] + rc) = make_float4(bf2f_lo(pf0.x), bf2f_hi(pf0.x), bf2f_lo(pf0.y), bf2f_hi(pf0.y));
-    *reinterpret_cast<float4*>(xs[rh] + rc + 4) = make_float4(bf2f_lo(pf0.z), bf2f_hi(pf0.z), bf2f_lo(pf0.w), bf2f_hi(pf0.w));
+    float4* dst = reinterpret_cast<float4*>(xrow + 8 * jj);
+    dst[0] = make_float4(bf2f_lo(pf0.x), bf2f_hi(pf0.x), bf2f_lo(pf0.y), bf2f_hi(pf0.y));
+    dst[1] = make_float4(bf2f_lo(pf0.z), bf2f_hi(pf0.z), bf2f_lo(pf0.w), bf2f_hi(pf0.w));
     pf0 = pf1;
     if (tt + 2 < VT) pf1 = fetch(t + 2);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    float ya[4], yb[4];
-#pragma unroll 1
-    for (int r = 0; r < 4; r += 2) {   // a runtime loop: two rows' reads at a time keep the registers bounded
-      float a2[2], b2[2];
-      hadamard_chain2(xs[r], xs[r + 1], hcol, a2, b2);
-      ya[r] = a2[0]; ya[r + 1] = a2[1];
-      yb[r] = b2[0]; yb[r + 1] = b2[1];
-    }
-    uint64_t ma[4], mb[4];
+    float y[8];
+    hadamard_row8(xrow, hl, y);
+
+    // min and -max of the lane's 8 outputs; after the swap rows 0 / 1 hold group 0's min / -max partials (lanes
+    // l, l + 16 combined), rows 2 / 3 group 1's
+    const float mn = fminf(fminf(fminf(y[0], y[1]), fminf(y[2], y[3])), fminf(fminf(y[4], y[5]), fminf(y[6], y[7])));
+    const float mx = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])), fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(-mx), false, false);
+    const float red = row_min16(fminf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+    const float lo0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 0));
+    const float hi0 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 16));
+    const float lo1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 32));
+    const float hi1 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 48));
+    // lane q encodes lo (q even) or the scale (q odd) of group q >> 1
+    const float glo = (q & 2) ? lo1 : lo0, ghi = (q & 2) ? hi1 : hi0;
+    const uint32_t b8 = f8e((q & 1) ? clamp_min_1e8(__fsub_rn(ghi, glo)) : glo);
+    const float dec = (q & 1) ? clamp_min_1e8(f8d(b8)) : f8d(b8);
+    if (lane < 4) out[((q & 1) ? VSC_O : VLO_O) + t * 2 + (q >> 1)] = (uint8_t)b8;
+    const float lof = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 0));
+    const float den = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 1));
+    const float lof1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 2));
+    const float den1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 3));
+    const float l = g ? lof1 : lof, dn = g ? den1 : den;
+    const float half = dn * 0.5f, eps = dn * 0x1p-25f;
+    uint32_t byte = 0;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float lo = wave_min(fminf(fminf(ya[2 * g], yb[2 * g]), fminf(ya[2 * g + 1], yb[2 * g + 1])));
-      const float hi = wave_max(fmaxf(fmaxf(ya[2 * g], yb[2 * g]), fmaxf(ya[2 * g + 1], yb[2 * g + 1])));
-      const uint32_t lo8 = f8e(lo);
-      const uint32_t sc8 = f8e(clamp_min_1e8(__fsub_rn(hi, lo)));
-      const float lof = f8d(lo8), den = clamp_min_1e8(f8d(sc8));
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int r = 2 * g + u;
-        const float ba = __builtin_rintf(__fdiv_rn(__fsub_rn(ya[r], lof), den));
-        const float bb = __builtin_rintf(__fdiv_rn(__fsub_rn(yb[r], lof), den));
-        ma[r] = __ballot(ba >= 1.f);
-        mb[r] = __ballot(bb >= 1.f);
-      }
-      if (lane == 0) { out[VLO_O + t * 2 + g] = (uint8_t)lo8; out[VSC_O + t * 2 + g] = (uint8_t)sc8; }
-    }
-    {
-      const int hh = lane >> 4, jj = lane & 15;
-      const uint64_t a = hh == 0 ? ma[0] : hh == 1 ? ma[1] : hh == 2 ? ma[2] : ma[3];
-      const uint64_t b = hh == 0 ? mb[0] : hh == 1 ? mb[1] : hh == 2 ? mb[2] : mb[3];
-      out[VB_O + t * 64 + lane] = (uint8_t)(gather4(a, jj) | (gather4(b, jj) << 4));
-    }
+    for (int i = 0; i < 8; ++i) byte |= (__fsub_rn(__fsub_rn(y[i], l), half) > eps) ? (1u << i) : 0u;
+    out[VB_O + t * 64 + lane] = (uint8_t)byte;
   }
 }
 
@@ -329,6 +391,7 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
                                                          const int32_t* __restrict__ nq_prev,
                                                          const int32_t* __restrict__ nq_new, int64_t R, int max_new) {
   __shared__ __align__(16) char lds[QLDS_BYTES];
+  __shared__ int64_t rowtab[BLK];
   const int64_t units = R * max_new, i = blockIdx.x;
   const bool kpass = i < units;
   const int64_t unit = kpass ? i : (i - units) / VSPLIT;
@@ -337,8 +400,9 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
   if (j >= nq_new[r]) return;   // uniform over the workgroup
   const int64_t tok0 = (int64_t)j * BLK;
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
-  quantize_part(PagedSrc{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0}, dst, lds, kpass,
-                kpass ? 0 : (int)((i - units) % VSPLIT));
+  PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
+  src.prepare(rowtab);
+  quantize_part(src, dst, lds, kpass, kpass ? 0 : (int)((i - units) % VSPLIT));
 }
 
 // ---------------------------------------------------------------- latency-oriented flush (decode steps)
@@ -355,6 +419,7 @@ __global__ void __launch_bounds__(QTHREADS) flush_lat_kernel(const uint16_t* __r
                                                              const int32_t* __restrict__ nq_prev,
                                                              const int32_t* __restrict__ nq_new, int64_t R, int max_new) {
   __shared__ __align__(16) char lds[QLDS_BYTES];
+  __shared__ int64_t rowtab[BLK];
   const int64_t units = R * max_new, i = blockIdx.x;
   const bool kpass = i < units;
   const int64_t unit = kpass ? i : (i - units) / LSPLIT;
@@ -363,7 +428,8 @@ __global__ void __launch_bounds__(QTHREADS) flush_lat_kernel(const uint16_t* __r
   if (j >= nq_new[r]) return;   // uniform over the workgroup
   const int64_t tok0 = (int64_t)j * BLK;
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
-  const PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
+  PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
+  src.prepare(rowtab);
   if (kpass) quantize_k<PagedSrc, 16>(src, dst, lds);
   else quantize_v<1>(src, dst, (int)((i - units) % LSPLIT) * QW, lds);
 }
