@@ -149,6 +149,25 @@ __device__ __forceinline__ float wave_max(float x) {
   return x;
 }
 
+// K code clamp(rne(fl(d / den)), 0, 3) without the division. fl(q) > 1/2 <=> d > den / 2 (a float above den / 2 is
+// at least an ulp of den / 2 above it); fl(q) >= 3/2 <=> q >= 3/2 - 2^-24 and fl(q) > 5/2 <=> q > 5/2 + 2^-23 (the
+// midpoints round to the even 3/2 and 5/2). Those two are decided on r = fl(d - t den) (one fma): near the threshold
+// d - t den is a small multiple of 2^-24 times den's power of two, hence exact, and a second fma adds the margin
+// den 2^-24 (den 2^-23) with the sign of the exact sum; far from it |r| dwarfs the margin. den >= 1e-8 is normal; a
+// NaN d or den gives code 0, as the clamp of a NaN quotient does.
+__device__ __forceinline__ uint32_t kcode(float d, float den) {
+  const bool c1 = d > den * 0.5f;
+  const bool c2 = __builtin_fmaf(den, 0x1p-24f, __builtin_fmaf(-den, 1.5f, d)) >= 0.f;
+  const bool c3 = __builtin_fmaf(-den, 0x1p-23f, __builtin_fmaf(-den, 2.5f, d)) > 0.f;
+  return (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
+}
+
+// x of the lane `n` places further round its 16-lane row (DPP row_ror)
+__device__ __forceinline__ uint32_t row_ror(uint32_t x, int n) {
+  return n == 4 ? (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x124, 0xF, 0xF, false)
+                : (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x128, 0xF, 0xF, false);
+}
+
 struct QuantLds {                  // K path: per-wave min / max partials, then per-column lo and divisor
   float red_min[QW][512];
   float red_max[QW][512];
@@ -217,19 +236,18 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
       for (int tt = 0; tt < KG; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + t0 + tt, h) + c0);
 #pragma unroll
       for (int tt = 0; tt < KG; ++tt) {
-        __builtin_amdgcn_sched_barrier(0);   // one token row at a time: keeps the division temporaries bounded
+        __builtin_amdgcn_sched_barrier(0);   // one token row at a time
         const uint32_t wd[4] = {kx[tt].x, kx[tt].y, kx[tt].z, kx[tt].w};
         uint32_t d0 = 0, d1 = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
-          float c = __builtin_rintf(__fdiv_rn(__fsub_rn(x, lof[e]), den[e]));
-          c = fminf(fmaxf(c, 0.f), 3.f);
-          const uint32_t code = (uint32_t)c << (2 * p);
+          const uint32_t code = kcode(__fsub_rn(x, lof[e]), den[e]) << (2 * p);
           if (e < 4) d0 |= code << (8 * e); else d1 |= code << (8 * (e - 4));
         }
-        d0 |= __shfl_xor(d0, 4); d1 |= __shfl_xor(d1, 4);
-        d0 |= __shfl_xor(d0, 8); d1 |= __shfl_xor(d1, 8);
+        // the 4 planes of these bytes sit in the lanes 4, 8, 12 apart within the 16-lane row
+        d0 |= row_ror(d0, 4); d1 |= row_ror(d1, 4);
+        d0 |= row_ror(d0, 8); d1 |= row_ror(d1, 8);
         if (p == 0) {
           const int t = TPW * w + t0 + tt;
           *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + h) * 32 + 8 * q) = make_uint2(d0, d1);
@@ -300,10 +318,9 @@ __device__ __forceinline__ float row_min16(float x) {
 // ahead; the wave writes them as floats into its own LDS rows, and each lane runs its row's 8-output chain from there.
 // Per (token, 2-head group) -- lanes 32 g .. 32 g + 31 -- the min / max of the 256 outputs go through a 16-row swap and
 // DPP row reductions; the token's four scale bytes (lo and scale of each group) are encoded by lanes 0..3 at once.
-// bit = rne(fl(d / den)) >= 1 with d = fl(y - lo) is evaluated without the division as fl(d - den / 2) > den 2^-25: the
-// quotient rounds above 1/2 exactly when d / den > 1/2 + 2^-25, and near that point d - den / 2 is exact (Sterbenz) and a
-// small multiple of half an ulp of den / 2, so the comparison is exact; far from it rounding keeps the sign of the
-// margin (den >= 1e-8 is normal, and a NaN den or d gives 0 both ways).
+// bit = rne(fl(d / den)) >= 1 with d = fl(y - lo) is evaluated without the division as d > den / 2: a float d above
+// den / 2 exceeds it by at least an ulp of den / 2, so d / den > 1/2 + 2^-25 and the quotient rounds above 1/2; at
+// d = den / 2 it is 1/2, which rounds to 0 (den >= 1e-8 is normal; a NaN den or d gives 0 both ways).
 constexpr int VSPLIT = 4, VTOK = BLK / VSPLIT, VTPW = VTOK / QW;
 constexpr int VROW = 132;   // floats per staged row: the 4 rows of a token start on different LDS banks
 constexpr int VLDS_BYTES = QW * 4 * VROW * 4;
@@ -354,10 +371,10 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
     const float lof1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 2));
     const float den1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 3));
     const float l = g ? lof1 : lof, dn = g ? den1 : den;
-    const float half = dn * 0.5f, eps = dn * 0x1p-25f;
+    const float half = dn * 0.5f;
     uint32_t byte = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) byte |= (__fsub_rn(__fsub_rn(y[i], l), half) > eps) ? (1u << i) : 0u;
+    for (int i = 0; i < 8; ++i) byte |= (__fsub_rn(y[i], l) > half) ? (1u << i) : 0u;
     out[VB_O + t * 64 + lane] = (uint8_t)byte;
   }
 }
