@@ -176,7 +176,7 @@ struct QuantLds {                  // K path: per-wave min / max partials, then 
 };
 
 // K codes and scales of one sub-block: per (head, channel) min / max over its 256 tokens (8 waves x 32 tokens).
-template <typename Src, int KG = 8>
+template <typename Src, int KG = 4>
 __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   QuantLds& S = *reinterpret_cast<QuantLds*>(lds);
@@ -186,8 +186,8 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
   float* col_den = S.col_den;
 
   // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16). The
-  // rows are read in groups of KG tokens, twice (min / max, then codes; the second pass hits L2), which keeps the
-  // pass within the register budget of the V pass it shares a grid with.
+  // rows are read in groups of KG tokens, twice (min / max, then codes; the second pass hits L2). KG = 4 keeps the
+  // pass within the 64 VGPRs of the V pass it shares a grid with (8 waves per SIMD).
   const int h = lane >> 4, c0 = 8 * (lane & 15);
   float mn[8], mx[8];
 #pragma unroll
@@ -380,8 +380,8 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
 }
 
 // A quantize grid holds, per sub-block, one K workgroup (all 256 tokens per (head, channel)) followed in the grid by
-// VSPLIT V workgroups (V is independent per token). Both passes fit one register budget, so 4 waves per SIMD run and
-// the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup i < units is the K pass of unit i;
+// VSPLIT V workgroups (V is independent per token). Both passes fit 64 VGPRs and 39 KB of LDS, so 8 waves per SIMD run
+// and the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup i < units is the K pass of unit i;
 // i >= units is the V pass of unit (i - units) / VSPLIT, token range (i - units) % VSPLIT.
 constexpr int QLDS_BYTES = (int)sizeof(QuantLds) > VLDS_BYTES ? (int)sizeof(QuantLds) : VLDS_BYTES;
 
