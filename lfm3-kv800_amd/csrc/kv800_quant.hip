@@ -278,7 +278,8 @@ __device__ __forceinline__ void hadamard_row8(const float* x, const float (&hl)[
   float4 buf[3];
   buf[0] = *reinterpret_cast<const float4*>(x);
   buf[1] = *reinterpret_cast<const float4*>(x + 4);
-  float ch[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float ch[8];
+  ch[0] = 0.f;
 #pragma unroll
   for (int g = 0; g < 32; ++g) {   // k = 4 g .. 4 g + 3
     if (g + 2 < 32) buf[(g + 2) % 3] = *reinterpret_cast<const float4*>(x + 4 * (g + 2));
@@ -296,20 +297,40 @@ __device__ __forceinline__ void hadamard_row8(const float* x, const float (&hl)[
       for (int i = 0; i < 8; ++i)
         if (i < nch) ch[i] = __builtin_fmaf(xv[e], hneg(m, i) ? -h : h, ch[i]);
     }
-    // the group's fmas stay before this point and the next group's reads after it: two reads ahead, no further
-    asm volatile("" : "+v"(ch[0]), "+v"(ch[1]), "+v"(ch[2]), "+v"(ch[3]), "+v"(ch[4]), "+v"(ch[5]), "+v"(ch[6]),
-                 "+v"(ch[7])::"memory");
+    // the group's fmas stay before this point and the next group's reads after it: two reads ahead, no further (the
+    // live chains only; the last group's results stay plain fma results)
+    if (nch == 1) asm volatile("" : "+v"(ch[0])::"memory");
+    else if (nch == 2) asm volatile("" : "+v"(ch[0]), "+v"(ch[1])::"memory");
+    else if (nch == 4) asm volatile("" : "+v"(ch[0]), "+v"(ch[1]), "+v"(ch[2]), "+v"(ch[3])::"memory");
+    else if (g < 31)
+      asm volatile("" : "+v"(ch[0]), "+v"(ch[1]), "+v"(ch[2]), "+v"(ch[3]), "+v"(ch[4]), "+v"(ch[5]), "+v"(ch[6]),
+                   "+v"(ch[7])::"memory");
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = ch[i];
 }
 
+// v_min_f32 as the instruction: the compiler would first quiet possible signalling NaNs of operands it cannot see
+// the origin of (a DPP or permlane result); these are all fma results or copies of them, never signalling.
+__device__ __forceinline__ float vmin(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// min(x, x of a DPP partner lane); s_nop 1 gives the two wait states a DPP read of a just-written VGPR needs
+#define KV800_MIN_DPP(x, ctrl)                                                                                \
+  ({                                                                                                          \
+    float r_;                                                                                                 \
+    asm("s_nop 1\n\tv_min_f32_dpp %0, %1, %1 " ctrl " row_mask:0xf bank_mask:0xf" : "=v"(r_) : "v"(x));     \
+    r_;                                                                                                       \
+  })
+
 // min over each 16-lane row, the result in every lane of the row (quad swaps, then half-row and row mirrors)
 __device__ __forceinline__ float row_min16(float x) {
-  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0xB1, 0xF, 0xF, false)));
-  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x4E, 0xF, 0xF, false)));
-  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x141, 0xF, 0xF, false)));
-  x = fminf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x140, 0xF, 0xF, false)));
+  x = KV800_MIN_DPP(x, "quad_perm:[1,0,3,2]");
+  x = KV800_MIN_DPP(x, "quad_perm:[2,3,0,1]");
+  x = KV800_MIN_DPP(x, "row_half_mirror");
+  x = KV800_MIN_DPP(x, "row_mirror");
   return x;
 }
 
@@ -356,7 +377,7 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
     const float mn = fminf(fminf(fminf(y[0], y[1]), fminf(y[2], y[3])), fminf(fminf(y[4], y[5]), fminf(y[6], y[7])));
     const float mx = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])), fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
     const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(-mx), false, false);
-    const float red = row_min16(fminf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+    const float red = row_min16(vmin(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
     const float lo0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 0));
     const float hi0 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 16));
     const float lo1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 32));
