@@ -54,6 +54,27 @@ __device__ __forceinline__ uint32_t f8e(float f) {
 
 __device__ __forceinline__ float clamp_min_1e8(float a) { return a < 1e-8f ? 1e-8f : a; }
 
+// v_min_f32 / v_max_f32 / v_max3_f32 as the bare instructions. fminf and fmaxf first quiet signalling NaNs of operands
+// whose origin the compiler cannot see (cross-lane moves, selects, inline assembly); arithmetic never produces a
+// signalling NaN, so for arithmetic results and copies of them the quieting is dead work. The operands must be written
+// by ordinary VALU or memory instructions, not straight by an MFMA (no hazard wait states are inserted for inline
+// assembly reading an MFMA result).
+__device__ __forceinline__ float vmin(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 }  // namespace kv800
 
 // ---------------------------------------------------------------- host error plumbing

@@ -68,8 +68,8 @@ __device__ __forceinline__ float sum4rows(float x) {   // sum over lanes l, l ^ 
 }
 __device__ __forceinline__ float max4rows(float x) {
   float2 p = rows16(x);
-  p = halves32(fmaxf(p.x, p.y));
-  return fmaxf(p.x, p.y);
+  p = halves32(vmax(p.x, p.y));
+  return vmax(p.x, p.y);
 }
 
 // Four fp8 e4m3fn bytes of w -> floats (byte i -> o[i]) with the hardware conversion: gfx950 converts the OCP e4m3
@@ -715,8 +715,8 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     }
     __builtin_amdgcn_s_setprio(2);
     // ---- online softmax over the chunk's 32 tokens; row = column n, tokens 4 g + i of each tile
-    float tmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+    float tmax = vmax3(vmax3(sv[0][0], sv[0][1], sv[0][2]), vmax3(sv[0][3], sv[1][0], sv[1][1]),
+                       vmax(sv[1][2], sv[1][3]));
     tmax = max4rows(tmax) * scale;
     if (__any(tmax > m + QLAZY)) {   // a chunk max above the running max: rescale (a wave-uniform branch)
       const float mn = fmaxf(m, tmax);

@@ -310,13 +310,6 @@ __device__ __forceinline__ void hadamard_row8(const float* x, const float (&hl)[
   for (int i = 0; i < 8; ++i) y[i] = ch[i];
 }
 
-// v_min_f32 as the instruction: the compiler would first quiet possible signalling NaNs of operands it cannot see
-// the origin of (a DPP or permlane result); these are all fma results or copies of them, never signalling.
-__device__ __forceinline__ float vmin(float a, float b) {
-  float r;
-  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
 // min(x, x of a DPP partner lane); s_nop 1 gives the two wait states a DPP read of a just-written VGPR needs
 #define KV800_MIN_DPP(x, ctrl)                                                                                \
   ({                                                                                                          \
