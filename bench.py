@@ -82,7 +82,8 @@ C2_B, C2_N, C2_EBS = 64, 2048, 128
 C2_NQ = (C2_N - 128) // 256                         # 7 flushed sub-blocks per sequence (kv800.py:433 flush rule)
 C2_READ = C2_B * C2_NQ * 256 * 4 * 128 * 2 * 2      # bf16 K + V gathered from the exact pages
 C2_WRITE = C2_B * C2_NQ * 51200
-C2_FMA = C2_B * C2_NQ * 256 * 4 * 64 * 192          # fp32 fma of the bit-exact V Hadamard chains (96 per output)
+C2_FMA = C2_B * C2_NQ * 256 * 4 * 16 * 688          # fp32 fma of the bit-exact V Hadamard chains: 688 per lane's 8
+                                                    # outputs (16 lanes per head row), 86 per output
 FMA_PEAK = 256 * 64 * 2.4e9                         # non-packed fp32 fma/s: 256 CUs x 64 lanes x 2.4 GHz
 
 
@@ -336,6 +337,7 @@ def main():
     ap.add_argument("--calib", action="store_true", help="plain copy of known size (rocprof FETCH/WRITE calibration)")
     ap.add_argument("--c3-only", action="store_true", help="skip the C2 / C4 / C5 workloads (counter passes of the C3 kernel)")
     ap.add_argument("--e2e-only", action="store_true", help="only the C5 decode loop; prints its record")
+    ap.add_argument("--c2-only", action="store_true", help="only the C2 flush (counter passes of the flush kernel)")
     ap.add_argument("--e2e-steps", type=int, default=128)
     a = ap.parse_args()
     if a.gpus != 1:
@@ -351,6 +353,10 @@ def main():
     if a.e2e_only:
         print(json.dumps({"e2e": bench_e2e(torch, dev, a.e2e_steps),
                           "e2e_398x32k": bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)}), flush=True)
+        return
+
+    if a.c2_only:
+        print(json.dumps({"flush_c2": bench_flush_c2(torch, kh, dev, a.steps, a.warmup)}), flush=True)
         return
 
     if a.calib:
