@@ -2,7 +2,7 @@
  * in the same library as the 800h path (lfm3-kv800_amd/_lib/libkv800_hip.so).
  *
  * No counterpart in the reference's own code: its model (vllm_model.py:195-471) runs these steps through vLLM's fused
- * RMSNorm / rotary / activation ops. Conventions as include/kv800_hip.h: device pointers to bf16 (uint16_t) data,
+ * RMSNorm / rotary / activation ops and its linear layers. Conventions as include/kv800_hip.h: device pointers to bf16 (uint16_t) data,
  * `stream` a hipStream_t as void*, asynchronous launches, 0 on success or a negative status with
  * kv800_hip_last_error(). Every result is rounded to bf16 where the corresponding torch op on bf16 tensors rounds;
  * rms(x) = x rsqrt(mean(x^2) + eps) in fp32.
@@ -47,6 +47,20 @@ int lfm3_hip_gate_mul(const uint16_t* o, const uint16_t* g, int64_t gstride, int
  * among equal values the first, and a NaN ranks above every number (the first NaN wins), as torch.argmax over the
  * same values. V and stride multiples of 8, x 16-byte aligned. */
 int lfm3_hip_argmax(const uint16_t* x, int64_t R, int64_t V, int64_t stride, int64_t* out, void* stream);
+
+/* Dense products y = x W^T of the decode batch (lfm3-kv800_amd/csrc/lfm3_gemm.hip). W (N, K) bf16 is stored once in
+ * the B-operand order of the 32 x 32 x 16 bf16 MFMA: wsh holds Npad / 32 x K / 16 blocks of 512 bf16, block
+ * (nt, ks) lane l = W[32 nt + l % 32][16 ks + 8 (l / 32) .. + 8], rows n >= N zero. K a multiple of 64, Npad of 128. */
+int lfm3_hip_shuffle_weight(const uint16_t* w, int64_t N, int64_t K, int64_t Npad, uint16_t* wsh, void* stream);
+
+/* y (R, Npad; row stride ldy) = bf16(x (R, K; row stride ldx) . W^T) with fp32 accumulation, W as shuffled above;
+ * ldx and ldy multiples of 8, x and y 16-byte aligned.
+ * split > 1 cuts K into `split` equal parts (multiples of 64) whose fp32 partials go to work (split x R x Npad floats)
+ * and are summed in part order before the rounding (split 1: work unused). glu = 1 (split 1): W's rows come in 128-row
+ * groups [64 gate rows | the matching 64 up rows] and y (R, Npad / 2) = bf16(bf16(silu(g)) u) of the bf16 products,
+ * the gated activation of lfm3_hip_silu_mul on a [g | u] product. */
+int lfm3_hip_linear(const uint16_t* x, int64_t ldx, const uint16_t* wsh, int64_t R, int64_t Npad, int64_t K,
+                    uint16_t* y, int64_t ldy, int split, float* work, int glu, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ LIBDIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIBDIR, "libkv800_hip.so")
 ARCH = "gfx950"
 SOURCES = {"kv800_quant.hip": ["-ffp-contract=off"], "kv800_decode.hip": ["-fno-strict-aliasing", "-mllvm", "-amdgpu-mfma-vgpr-form"],
-           "kv800_cache.hip": [], "kv800_prefill.hip": [], "lfm3_model.hip": []}
+           "kv800_cache.hip": [], "kv800_prefill.hip": [], "lfm3_model.hip": [], "lfm3_gemm.hip": []}
 COMMON = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", INCLUDE, "-I", CSRC]
 

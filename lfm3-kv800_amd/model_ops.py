@@ -16,6 +16,8 @@ SIGNATURES = {
     "lfm3_hip_conv_step": (_I32, [_VP, _I64, _VP, _VP, _I64, _I64, _VP, _VP]),
     "lfm3_hip_gate_mul": (_I32, [_VP, _VP, _I64, _I64, _VP, _VP]),
     "lfm3_hip_argmax": (_I32, [_VP, _I64, _I64, _I64, _VP, _VP]),
+    "lfm3_hip_shuffle_weight": (_I32, [_VP, _I64, _I64, _I64, _VP, _VP]),
+    "lfm3_hip_linear": (_I32, [_VP, _I64, _VP, _I64, _I64, _I64, _VP, _I64, _I32, _VP, _I32, _VP]),
 }
 _BOUND = {}
 
@@ -155,4 +157,53 @@ def argmax(x):
     R, V = x.shape
     out = torch.empty(R, dtype=torch.int64, device=x.device)
     kv800_hip._check(L.lfm3_hip_argmax(_ptr(x), R, V, x.stride(0), _ptr(out), _stream(x)))
+    return out
+
+
+class PackedWeight:
+    """A (N, K) bf16 weight in the MFMA operand order of lfm3_hip_linear, padded to Npad = ceil(N / 128) 128 columns
+    (zeros); n, k the logical shape. glu: w is a [g | u] (2F, K) gate / up pair (F a multiple of 64) whose rows are
+    regrouped as [64 g rows | the matching 64 u rows] so that linear() returns bf16(bf16(silu(g)) u), (R, F)."""
+
+    def __init__(self, w, glu=False):
+        L = _lib()
+        w = _bf16(w, "w")
+        if w.dim() != 2 or w.shape[1] % 64:
+            raise ValueError(f"w must be (N, K) with K a multiple of 64, got {tuple(w.shape)}")
+        self.n, self.k = w.shape
+        self.glu = bool(glu)
+        if self.glu:
+            if self.n % 128:
+                raise ValueError(f"a [g | u] weight needs 2F a multiple of 128, got {self.n}")
+            w = w.view(2, self.n // 128, 64, self.k).transpose(0, 1).contiguous().view(self.n, self.k)
+        self.npad = (self.n + 127) // 128 * 128
+        self.data = torch.empty(self.npad * self.k, dtype=torch.bfloat16, device=w.device)
+        kv800_hip._check(L.lfm3_hip_shuffle_weight(_ptr(w), self.n, self.k, self.npad, _ptr(self.data), _stream(w)))
+
+
+def linear(x, pw, split=1, out=None, work=None):
+    """(R, K) bf16 . W^T -> (R, Npad) bf16 (columns >= pw.n are zero), or (R, n / 2) silu(g) u for a glu weight;
+    out / work optional preallocated buffers."""
+    L = _lib()
+    if x.dtype != torch.bfloat16 or x.device.type != "cuda" or x.dim() != 2 or x.shape[1] != pw.k \
+            or x.stride(-1) != 1 or x.stride(0) % 8:
+        raise ValueError(f"x must be bf16 (R, {pw.k}) with contiguous rows, got {x.dtype} {tuple(x.shape)}")
+    if x.device != pw.data.device:
+        raise ValueError("x and the weight must be on one device")
+    if pw.glu and split != 1:
+        raise ValueError("a glu product takes no K split")
+    R = x.shape[0]
+    width = pw.npad // 2 if pw.glu else pw.npad
+    if out is None:
+        out = torch.empty(R, width, dtype=torch.bfloat16, device=x.device)
+    elif out.dtype != torch.bfloat16 or out.device != x.device or out.dim() != 2 or out.shape[0] != R \
+            or out.shape[1] < width or out.stride(-1) != 1 or out.stride(0) % 8:
+        raise ValueError(f"out must be bf16 ({R}, >= {width}) with contiguous rows")
+    if split > 1:
+        need = split * R * pw.npad
+        if work is None or work.dtype != torch.float32 or work.device != x.device or work.numel() < need:
+            work = torch.empty(need, dtype=torch.float32, device=x.device)
+    kv800_hip._check(L.lfm3_hip_linear(_ptr(x), x.stride(0), _ptr(pw.data), R, pw.npad, pw.k, _ptr(out),
+                                       out.stride(0), int(split), _ptr(work if split > 1 else None), int(pw.glu),
+                                       _stream(x)))
     return out

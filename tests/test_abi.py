@@ -67,14 +67,20 @@ def test_model_header_symbols_exported_and_bound(lib):
     import lfm3_kv800_amd.model_ops as mo
     src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "lfm3_model.h")).read(), flags=re.S)
     names = sorted(set(re.findall(r"\b(lfm3_hip_\w+)\s*\(", src)))
-    assert len(names) == 6
+    assert len(names) == 8
     out = subprocess.run(["nm", "-D", "--defined-only", kh.LIB], capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\bT (lfm3_hip_\w+)", out))
     assert not [n for n in names if n not in exported]
     assert sorted(mo.SIGNATURES) == names
-    for name in ("lfm3_hip_silu_mul", "lfm3_hip_argmax"):
+    for name in ("lfm3_hip_silu_mul", "lfm3_hip_argmax", "lfm3_hip_shuffle_weight", "lfm3_hip_linear"):
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = mo.SIGNATURES[name]
     assert lib.lfm3_hip_silu_mul(None, 1, 7, None, None) == -1          # F not a multiple of 8: rejected on the host
     assert lib.lfm3_hip_argmax(None, 1, 12, 12, None, None) == -1       # V not a multiple of 8
     assert lib.lfm3_hip_argmax(None, 1, 16, 8, None, None) == -1        # row stride below V
+    assert lib.lfm3_hip_shuffle_weight(None, 100, 96, 128, None, None) == -1           # K not a multiple of 64
+    assert lib.lfm3_hip_shuffle_weight(None, 200, 128, 128, None, None) == -1          # Npad below N
+    assert lib.lfm3_hip_linear(None, 128, None, 4, 100, 128, None, 104, 1, None, 0, None) == -1   # Npad % 128
+    assert lib.lfm3_hip_linear(None, 128, None, 4, 128, 128, None, 128, 3, None, 0, None) == -1   # split of K
+    assert lib.lfm3_hip_linear(None, 128, None, 4, 128, 128, None, 128, 2, None, 0, None) == -1   # no workspace
+    assert lib.lfm3_hip_linear(None, 128, None, 4, 128, 128, None, 64, 2, None, 1, None) == -1    # glu with split

@@ -293,3 +293,44 @@ def test_argmax_matches_torch(hip):
         got, want = mo.argmax(t), t.float().argmax(-1)
         say("argmax", got.tolist(), want.tolist())
         assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("R,N,K,split", [(256, 2048, 2048, 1), (256, 16384, 2048, 1), (398, 3088, 2048, 1),
+                                         (37, 640, 8192, 4), (398, 2048, 8192, 8), (1, 128, 64, 1), (130, 256, 320, 1),
+                                         (256, 2048, 2048, 8)])
+def test_linear_matches_fp32(hip, R, N, K, split):
+    """The engine loop's GEMM (lfm3_hip_linear over a shuffled weight) against an fp32 product of the same bf16
+    operands, rounded to bf16: within one bf16 rounding of the fp32 result plus fp32 summation-order noise
+    (|d| <= 2^-8 |ref| + 1e-3 max |ref|); the padded columns are zero; split-K sums its parts in a fixed order, so
+    two runs give identical bits. Shapes cover partial 128-row tiles (398, 130, 37 rows), a padded width (3088),
+    K = 8192 with 4- and 8-way splits, slab counts below and off the weight ring's depth (1, 5, 4 per part)."""
+    from lfm3_kv800_amd import model_ops as mo
+    g = torch.Generator(device=DEV).manual_seed(R + N + K)
+    x = torch.randn(R, K, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    pw = mo.PackedWeight(w)
+    y = mo.linear(x, pw, split=split)
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().t()
+    d = (y[:, :N].float() - ref).abs()
+    bar = ref.abs() * 2.0 ** -8 + 1e-3 * ref.abs().max()
+    say("linear", R, N, K, split, "max |d|", float(d.max()), "max |ref|", float(ref.abs().max()))
+    assert bool((d <= bar).all())
+    assert not bool(y[:, N:].any())
+    y2 = mo.linear(x, pw, split=split)
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("R,F,K", [(256, 8192, 2048), (398, 256, 2048), (5, 64, 64)])
+def test_linear_glu_matches_unfused(hip, R, F, K):
+    """The gated-activation epilogue (a [g | u] weight regrouped in 64-row pairs) against the plain product of the same
+    kernel followed by the silu_mul kernel: the same k order per output, so identical bits."""
+    from lfm3_kv800_amd import model_ops as mo
+    g = torch.Generator(device=DEV).manual_seed(R + F)
+    x = torch.randn(R, K, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(2 * F, K, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    fused = mo.linear(x, mo.PackedWeight(w, glu=True))
+    plain = mo.silu_mul(mo.linear(x, mo.PackedWeight(w))[:, :2 * F].contiguous())
+    torch.cuda.synchronize()
+    say("glu", R, F, K, "equal", bool(torch.equal(fused, plain)))
+    assert fused.shape == (R, F) and torch.equal(fused, plain)
