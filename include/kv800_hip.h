@@ -192,6 +192,14 @@ int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, i
                           int64_t R, int64_t nqmax, int64_t nnew, int64_t* boff, int32_t* NQ, int32_t* NP,
                           int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add, void* stream);
 
+/* One decode step's metadata of a KV group (every row appends one token): for r < R with lens[r] = n (int64, the
+ * length including the new token), pos[r] = n - 1, slot[r] = bt[r, pos / ebs] * ebs + pos % ebs (int64; -1 for n = 0
+ * or a page index >= npages, a padding token) and lens32[r] = n. bt: (R, bt_stride) int32 block table. The
+ * reference's vLLM scheduler hands these to the backend (slot_mapping, seq_lens, vllm_attn.py:255-270); here one
+ * launch replaces the per-step torch ops that derive them. */
+int kv800_hip_step_meta(const int32_t* bt, int64_t bt_stride, int64_t npages, const int64_t* lens, int64_t R,
+                        int64_t ebs, int64_t* slot, int64_t* pos, int32_t* lens32, void* stream);
+
 /* off[r, p] = bt[r, p] * scale + add for p < npages (off row stride npages): an exact group's (R, bt_stride) int32
  * block table as element offsets of its pages, the eoff table the decode and flush read (the reference forms it with
  * torch ops per step, vllm_attn.py:320-323). */

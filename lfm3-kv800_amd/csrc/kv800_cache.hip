@@ -8,6 +8,7 @@
 //                        (256 j % bsq) / 256 * 51200 (vllm_attn.py:332-340); optionally the sub-blocks flushed before
 //                        the step's nnew tokens (the flush range's start, vllm_attn.py:297-317), the block table as
 //                        int64 and the offsets of the sink aux areas (vllm_attn.py:276-291).
+//   step_meta_kernel     per row of a decode step: the new token's slot, its position and the int32 length
 //   page_offsets_kernel  off[r, p] = bt[r, p] * scale + add: an exact group's block table as element offsets of its
 //                        pages (the eoff table of the decode and flush kernels).
 // All are plain data movement: one thread per 16-byte piece or per table entry, coalesced along the row.
@@ -68,6 +69,21 @@ page_offsets_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int64_t R
   if (i >= R * npages) return;
   const int64_t r = i / npages, p = i % npages;
   out[i] = (int64_t)bt[r * bt_stride + p] * scale + add;
+}
+
+// One decode step's slot, position and int32 length of row r (every row appends one token at position len - 1): the
+// slot is the token's page bt[r, pos / ebs] times ebs plus pos % ebs; a row of length 0 gets slot and position -1
+// (a padding token, which write_exact skips); a position past the row's npages pages gets slot -1 as well.
+__global__ void __launch_bounds__(256)
+step_meta_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int64_t npages, const int64_t* __restrict__ lens,
+                 int64_t R, int64_t ebs, int64_t* __restrict__ slot, int64_t* __restrict__ pos,
+                 int32_t* __restrict__ lens32) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const int64_t n = lens[r], p = n - 1, pg = p >= 0 ? p / ebs : -1;
+  slot[r] = (pg >= 0 && pg < npages) ? (int64_t)bt[r * bt_stride + pg] * ebs + p % ebs : -1;
+  pos[r] = p >= 0 ? p : -1;
+  lens32[r] = (int32_t)n;
 }
 
 }  // namespace
@@ -131,6 +147,17 @@ int kv800_hip_page_offsets(const int32_t* bt, int64_t bt_stride, int64_t R, int6
   hipLaunchKernelGGL(page_offsets_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, bt,
                      bt_stride, R, npages, scale, add, out);
   return check_launch("page_offsets");
+}
+
+int kv800_hip_step_meta(const int32_t* bt, int64_t bt_stride, int64_t npages, const int64_t* lens, int64_t R,
+                        int64_t ebs, int64_t* slot, int64_t* pos, int32_t* lens32, void* stream) {
+  KV800_REQUIRE(R >= 0 && ebs > 0 && npages >= 0 && bt_stride >= npages, "step_meta: need R >= 0, ebs > 0, "
+                "bt_stride >= npages >= 0");
+  if (R == 0) return KV800_OK;
+  KV800_REQUIRE((bt || npages == 0) && lens && slot && pos && lens32, "step_meta: null pointer");
+  hipLaunchKernelGGL(step_meta_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, (hipStream_t)stream, bt,
+                     bt_stride, npages, lens, R, ebs, slot, pos, lens32);
+  return check_launch("step_meta");
 }
 
 }  // extern "C"

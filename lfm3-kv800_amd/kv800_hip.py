@@ -64,6 +64,7 @@ SIGNATURES = {
     "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
                                      _VP]),
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
+    "kv800_hip_step_meta": (_I32, [_VP, _I64, _I64, _VP, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_rope_rows": (_I32, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _VP]),
     "kv800_hip_prefill": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _VP]),
@@ -242,6 +243,24 @@ def step_tables(qbt, bsq, qs0, N, nqmax, nnew=1, aux_scale=None, aux_add=0):
                                    int(nnew), _ptr(boff), _ptr(NQ), _ptr(NP), _ptr(qbt64), _ptr(aux),
                                    int(aux_scale or 0), int(aux_add), _stream(dev)))
     return boff, NQ, NP, qbt64, aux
+
+
+def step_meta(bt, lens, ebs):
+    """(slot int64, pos int64, lens int32) of a decode step from the (R, pages) int32 block table and the (R,) int64
+    device lengths including the new token (kv800_hip_step_meta)."""
+    L = ops()
+    dev = bt.device
+    _need(bt, "bt", torch.int32, dev)
+    _need(lens, "lens", torch.int64, dev)
+    if bt.dim() != 2 or bt.stride(-1) != 1 or lens.dim() != 1 or lens.shape[0] != bt.shape[0]:
+        raise ValueError("bt must be (R, pages) with contiguous rows and lens (R,)")
+    R = bt.shape[0]
+    slot = torch.empty(R, dtype=torch.int64, device=dev)
+    pos = torch.empty(R, dtype=torch.int64, device=dev)
+    l32 = torch.empty(R, dtype=torch.int32, device=dev)
+    _check(L.kv800_hip_step_meta(_ptr(bt), bt.stride(0), bt.shape[1], _ptr(lens.contiguous()), R, int(ebs), _ptr(slot),
+                                 _ptr(pos), _ptr(l32), _stream(dev)))
+    return slot, pos, l32
 
 
 def page_offsets(bt, scale, add=0):

@@ -55,8 +55,11 @@ def step_meta(block_table, seq_lens_cpu, ebs, device, seq_lens_dev=None):
     lengths already on the device (step_lens), shared by the KV groups of a step."""
     sl = seq_lens_cpu.to(torch.int64)
     dsl = step_lens(sl, device) if seq_lens_dev is None else seq_lens_dev
-    pos = dsl - 1
     bt = block_table.to(device=device, dtype=torch.int32)
+    if bt.device.type == "cuda":   # one launch (kv800_hip_step_meta)
+        slot, pos, dsl32 = kv800_hip.step_meta(bt.contiguous(), dsl, ebs)
+        return StepMeta(bt, slot, dsl32, sl, pos)
+    pos = dsl - 1
     page = bt.gather(1, (pos // ebs)[:, None].long())[:, 0].long()
     slot = page * ebs + pos % ebs
     return StepMeta(bt, slot, dsl.to(torch.int32), sl, pos)
@@ -149,7 +152,7 @@ class KV800SlideLayer:
     def identity_tables(self, rows):
         """(cos, sin) (rows, 32) bf16 of ones / zeros: the kernel's RoPE then leaves the stored keys as they are."""
         if self._ident is None or self._ident[0].shape[0] < rows:
-            n = max(rows, 64)
+            n = max(2 * rows, 4096)   # grown ahead: a decode step asks for one more row each time
             self._ident = (torch.ones(n, 32, dtype=torch.bfloat16, device=self.ev.device),
                            torch.zeros(n, 32, dtype=torch.bfloat16, device=self.ev.device))
         return self._ident

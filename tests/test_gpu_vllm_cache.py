@@ -165,3 +165,23 @@ def test_step_tables(hip):
     assert torch.equal(aux.cpu(), qbt[:, 0].long() * (qs0 // 2) + AUX // 2)
     eoff = hip.page_offsets(qbt.to(DEV), 131072, 5)
     assert torch.equal(eoff.cpu(), qbt.long() * 131072 + 5)
+
+
+def test_step_meta_matches_torch(hip):
+    """The per-step metadata launch (kv800_hip_step_meta) against the torch statement it replaces (slot = page of
+    pos // ebs times ebs plus pos % ebs, pos = len - 1): random block tables with a padded row stride, lengths on page
+    boundaries, 1, and a full table; a row of length 0 and one past its table get slot -1."""
+    from lfm3_kv800_amd import kv800_hip
+    g = torch.Generator(device=DEV).manual_seed(5)
+    R, pages, stride, ebs = 37, 9, 12, 16
+    bt_full = torch.randint(0, 1000, (R, stride), generator=g, device=DEV, dtype=torch.int32)
+    bt = bt_full[:, :pages]
+    lens = torch.randint(1, pages * ebs + 1, (R,), generator=g, device=DEV, dtype=torch.int64)
+    lens[0], lens[1], lens[2], lens[3] = 1, ebs, ebs + 1, pages * ebs
+    slot, pos, l32 = kv800_hip.step_meta(bt, lens, ebs)
+    p = lens - 1
+    want = bt.gather(1, (p // ebs)[:, None].long())[:, 0].long() * ebs + p % ebs
+    assert torch.equal(slot, want) and torch.equal(pos, p) and torch.equal(l32, lens.to(torch.int32))
+    lens[4], lens[5] = 0, pages * ebs + 1
+    slot, pos, _ = kv800_hip.step_meta(bt, lens, ebs)
+    assert int(slot[4]) == -1 and int(pos[4]) == -1 and int(slot[5]) == -1 and int(pos[5]) == pages * ebs
