@@ -188,21 +188,39 @@ __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
   if (na || nb) return na && (!nb || ia < ib);
   return a > b || (a == b && ia < ib);
 }
-// thread t scans the 8-element pieces t, t + 256, ... of the row in order; the workgroup then reduces the 256 bests
+// thread t scans the 8-element pieces t, t + 256, ... of the row, eight loads at a time; the workgroup then reduces
+// the 256 bests (the order of the compares does not matter: ranks_before breaks ties by index)
 __global__ void __launch_bounds__(256)
 argmax_kernel(const uint16_t* __restrict__ x, int64_t V, int64_t stride, int64_t* __restrict__ out) {
   __shared__ float rv[4];
   __shared__ int ri[4];
   const uint16_t* row = x + (int64_t)blockIdx.x * stride;
-  float bv = -INFINITY;
-  int bi = (int)V;   // ranks after every element
-  for (int64_t p = threadIdx.x; p * 8 < V; p += 256) {
-    float f[8];
-    load8(row + 8 * p, f);
+  float cv[8];
+  int ci[8];   // eight independent running bests, one per in-flight piece
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (ranks_before(f[e], (int)(8 * p) + e, bv, bi)) { bv = f[e]; bi = (int)(8 * p) + e; }
+  for (int u = 0; u < 8; ++u) { cv[u] = -INFINITY; ci[u] = (int)V; }   // index V ranks after every element
+  for (int64_t p0 = threadIdx.x; p0 * 8 < V; p0 += 256 * 8) {   // 8 pieces' loads in flight, then their compares
+    float f[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t p = p0 + 256 * u;
+      if (p * 8 < V) load8(row + 8 * p, f[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t p = p0 + 256 * u;
+      if (p * 8 < V) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (ranks_before(f[u][e], (int)(8 * p) + e, cv[u], ci[u])) { cv[u] = f[u][e]; ci[u] = (int)(8 * p) + e; }
+      }
+    }
   }
+  float bv = cv[0];
+  int bi = ci[0];
+#pragma unroll
+  for (int u = 1; u < 8; ++u)
+    if (ranks_before(cv[u], ci[u], bv, bi)) { bv = cv[u]; bi = ci[u]; }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(bv, o, 64);
