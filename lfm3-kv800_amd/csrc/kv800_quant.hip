@@ -70,85 +70,6 @@ struct PagedSrc {   // exact pages: K of (position p, head h) at eoff[r, p / ebs
   __device__ const uint16_t* vrow(int t, int h) const { return krow(t, h) + e_v; }
 };
 
-// Per-lane column of the normalized Sylvester Hadamard for k < 64: H[k][lane] (H[k][lane + 64] is the same for
-// k < 64 and its negation for k >= 64; H[k][d] = H[k - 64][d] for d < 64).
-__device__ __forceinline__ void hadamard_column(float (&hc)[64], int lane) {
-  const float c = __uint_as_float(0x3DB504F3u);   // fp32(1 / sqrt(128)), the entries of kv800.hadamard
-#pragma unroll
-  for (int k = 0; k < 64; ++k) hc[k] = (__builtin_popcount(k & lane) & 1) ? -c : c;
-}
-
-// y[d] = sum_k x[k] H[k][d], the sequential fma chain of torch-CPU, for d = lane (ya) and d = lane + 64 (yb).
-// x is read from LDS (uniform across the wave). The first 64 steps are shared by both outputs.
-__device__ __forceinline__ void hadamard_chain(const float* x, const float (&hc)[64], float& ya, float& yb) {
-  float a = 0.f;
-#pragma unroll
-  for (int k = 0; k < 64; k += 4) {
-    __builtin_amdgcn_sched_barrier(0);   // one float4 of the row in flight: the chain is serial anyway
-    asm volatile("" ::: "memory");     // and no later read is moved up to here
-    const float4 v4 = *reinterpret_cast<const float4*>(x + k);
-    a = __builtin_fmaf(v4.x, hc[k], a);
-    a = __builtin_fmaf(v4.y, hc[k + 1], a);
-    a = __builtin_fmaf(v4.z, hc[k + 2], a);
-    a = __builtin_fmaf(v4.w, hc[k + 3], a);
-  }
-  float b = a;
-#pragma unroll
-  for (int k = 64; k < 128; k += 4) {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    const float4 v4 = *reinterpret_cast<const float4*>(x + k);
-    a = __builtin_fmaf(v4.x, hc[k - 64], a);     b = __builtin_fmaf(v4.x, -hc[k - 64], b);
-    a = __builtin_fmaf(v4.y, hc[k - 63], a);     b = __builtin_fmaf(v4.y, -hc[k - 63], b);
-    a = __builtin_fmaf(v4.z, hc[k - 62], a);     b = __builtin_fmaf(v4.z, -hc[k - 62], b);
-    a = __builtin_fmaf(v4.w, hc[k - 61], a);     b = __builtin_fmaf(v4.w, -hc[k - 61], b);
-  }
-  ya = a;
-  yb = b;
-}
-
-// The chains of two rows x0, x1 interleaved (each in hadamard_chain's order): two float4 reads in flight, and each
-// row's dependent fmas alternate with the other's.
-__device__ __forceinline__ void hadamard_chain2(const float* x0, const float* x1, const float (&hc)[64], float (&ya)[2],
-                                                float (&yb)[2]) {
-  float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-  for (int k = 0; k < 64; k += 4) {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    const float4 u = *reinterpret_cast<const float4*>(x0 + k), v = *reinterpret_cast<const float4*>(x1 + k);
-    a0 = __builtin_fmaf(u.x, hc[k], a0);     a1 = __builtin_fmaf(v.x, hc[k], a1);
-    a0 = __builtin_fmaf(u.y, hc[k + 1], a0); a1 = __builtin_fmaf(v.y, hc[k + 1], a1);
-    a0 = __builtin_fmaf(u.z, hc[k + 2], a0); a1 = __builtin_fmaf(v.z, hc[k + 2], a1);
-    a0 = __builtin_fmaf(u.w, hc[k + 3], a0); a1 = __builtin_fmaf(v.w, hc[k + 3], a1);
-  }
-  float b0 = a0, b1 = a1;
-#pragma unroll
-  for (int k = 64; k < 128; k += 4) {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    const float4 u = *reinterpret_cast<const float4*>(x0 + k), v = *reinterpret_cast<const float4*>(x1 + k);
-    const float h0 = hc[k - 64], h1 = hc[k - 63], h2 = hc[k - 62], h3 = hc[k - 61];
-    a0 = __builtin_fmaf(u.x, h0, a0); b0 = __builtin_fmaf(u.x, -h0, b0); a1 = __builtin_fmaf(v.x, h0, a1); b1 = __builtin_fmaf(v.x, -h0, b1);
-    a0 = __builtin_fmaf(u.y, h1, a0); b0 = __builtin_fmaf(u.y, -h1, b0); a1 = __builtin_fmaf(v.y, h1, a1); b1 = __builtin_fmaf(v.y, -h1, b1);
-    a0 = __builtin_fmaf(u.z, h2, a0); b0 = __builtin_fmaf(u.z, -h2, b0); a1 = __builtin_fmaf(v.z, h2, a1); b1 = __builtin_fmaf(v.z, -h2, b1);
-    a0 = __builtin_fmaf(u.w, h3, a0); b0 = __builtin_fmaf(u.w, -h3, b0); a1 = __builtin_fmaf(v.w, h3, a1); b1 = __builtin_fmaf(v.w, -h3, b1);
-  }
-  ya[0] = a0; ya[1] = a1;
-  yb[0] = b0; yb[1] = b1;
-}
-
-__device__ __forceinline__ float wave_min(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-
 // K code clamp(rne(fl(d / den)), 0, 3) without the division. fl(q) > 1/2 <=> d > den / 2 (a float above den / 2 is
 // at least an ulp of den / 2 above it); fl(q) >= 3/2 <=> q >= 3/2 - 2^-24 and fl(q) > 5/2 <=> q > 5/2 + 2^-23 (the
 // midpoints round to the even 3/2 and 5/2). Those two are decided on r = fl(d - t den) (one fma): near the threshold
@@ -327,6 +248,33 @@ __device__ __forceinline__ float row_min16(float x) {
   return x;
 }
 
+// Scales of one token's V rows from the 8 chain outputs y each lane holds (lane 16 hh + jj: row hh): per 2-head group g
+// (lanes 32 g .. 32 g + 31, 256 outputs) the min and max through a 16-row swap -- afterwards rows 0 / 1 hold group
+// 0's min / -max partials (lanes l, l + 16 combined), rows 2 / 3 group 1's -- and DPP row reductions; lanes q = 0..3
+// then encode lo (q even) or max(hi - lo, 1e-8) (q odd) of group q >> 1 in one pass. b8 is that byte (lanes 0..3);
+// lof, scf are the lane's group's decoded lo and scale, den = max(scf, 1e-8) the quantizer's divisor.
+struct VScales { uint32_t b8; float lof, scf, den; };
+__device__ __forceinline__ VScales v_scales(const float (&y)[8], int lane) {
+  const int q = lane & 3, g = lane >> 5;
+  const float mn = fminf(fminf(fminf(y[0], y[1]), fminf(y[2], y[3])), fminf(fminf(y[4], y[5]), fminf(y[6], y[7])));
+  const float mx = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])), fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
+  const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(-mx), false, false);
+  const float red = row_min16(vmin(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+  const float lo0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 0));
+  const float hi0 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 16));
+  const float lo1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 32));
+  const float hi1 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 48));
+  const float glo = (q & 2) ? lo1 : lo0, ghi = (q & 2) ? hi1 : hi0;
+  const uint32_t b8 = f8e((q & 1) ? clamp_min_1e8(__fsub_rn(ghi, glo)) : glo);
+  const float dec = f8d(b8);
+  const float lof0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 0));
+  const float scf0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 1));
+  const float lof1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 2));
+  const float scf1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 3));
+  const float scf = g ? scf1 : scf0;
+  return VScales{b8, g ? lof1 : lof0, scf, clamp_min_1e8(scf)};
+}
+
 // V bits and scales of tokens [t0, t0 + VT * QW) of one sub-block: wave w takes VT consecutive tokens, one token (its
 // 4 head rows) per step. Each lane loads 16 bytes of the token's rows (head hh, dims 8 jj .. 8 jj + 7), two tokens
 // ahead; the wave writes them as floats into its own LDS rows, and each lane runs its row's 8-output chain from there.
@@ -349,7 +297,7 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
   uint4 pf0 = fetch(tw), pf1 = VT > 1 ? fetch(tw + 1) : pf0;
   float hl[16];
   hadamard_low(hl, jj);
-  const int q = lane & 3, g = lane >> 5;
+  const int q = lane & 3;
 #pragma unroll 1
   for (int tt = 0; tt < VT; ++tt) {
     const int t = tw + tt;
@@ -365,30 +313,12 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
     float y[8];
     hadamard_row8(xrow, hl, y);
 
-    // min and -max of the lane's 8 outputs; after the swap rows 0 / 1 hold group 0's min / -max partials (lanes
-    // l, l + 16 combined), rows 2 / 3 group 1's
-    const float mn = fminf(fminf(fminf(y[0], y[1]), fminf(y[2], y[3])), fminf(fminf(y[4], y[5]), fminf(y[6], y[7])));
-    const float mx = fmaxf(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])), fmaxf(fmaxf(y[4], y[5]), fmaxf(y[6], y[7])));
-    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(mn), __float_as_uint(-mx), false, false);
-    const float red = row_min16(vmin(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
-    const float lo0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 0));
-    const float hi0 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 16));
-    const float lo1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 32));
-    const float hi1 = -__int_as_float(__builtin_amdgcn_readlane(__float_as_int(red), 48));
-    // lane q encodes lo (q even) or the scale (q odd) of group q >> 1
-    const float glo = (q & 2) ? lo1 : lo0, ghi = (q & 2) ? hi1 : hi0;
-    const uint32_t b8 = f8e((q & 1) ? clamp_min_1e8(__fsub_rn(ghi, glo)) : glo);
-    const float dec = (q & 1) ? clamp_min_1e8(f8d(b8)) : f8d(b8);
-    if (lane < 4) out[((q & 1) ? VSC_O : VLO_O) + t * 2 + (q >> 1)] = (uint8_t)b8;
-    const float lof = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 0));
-    const float den = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 1));
-    const float lof1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 2));
-    const float den1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dec), 3));
-    const float l = g ? lof1 : lof, dn = g ? den1 : den;
-    const float half = dn * 0.5f;
+    const VScales sc = v_scales(y, lane);
+    if (lane < 4) out[((q & 1) ? VSC_O : VLO_O) + t * 2 + (q >> 1)] = (uint8_t)sc.b8;
+    const float half = sc.den * 0.5f;
     uint32_t byte = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) byte |= (__fsub_rn(y[i], l) > half) ? (1u << i) : 0u;
+    for (int i = 0; i < 8; ++i) byte |= (__fsub_rn(y[i], sc.lof) > half) ? (1u << i) : 0u;
     out[VB_O + t * 64 + lane] = (uint8_t)byte;
   }
 }
@@ -468,7 +398,7 @@ __global__ void __launch_bounds__(QTHREADS) flush_lat_kernel(const uint16_t* __r
 // ---------------------------------------------------------------- dequantize (kv800.py:79-92)
 __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ sb, uint16_t* __restrict__ kout,
                                                       float* __restrict__ vout) {
-  __shared__ __align__(16) float xbuf[4][2][512];
+  __shared__ __align__(16) float xbuf[4][4 * VROW];   // per wave: one token's 4 V rows
   const int64_t m = blockIdx.x;
   const uint8_t* s = sb + m * SUB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -490,32 +420,31 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
     }
     *reinterpret_cast<uint4*>(kout + (m * BLK + t) * 512 + hc0) = make_uint4(o[0], o[1], o[2], o[3]);
   }
-  // V: (bit * vsc + vlo) @ H, wave w = tokens 64w .. 64w + 63, per token its 4 head rows
-  float hcol[64];
-  hadamard_column(hcol, lane);
-  const int rr = lane >> 4, e0 = 8 * (lane & 15);
+  // V: (bit * vsc + vlo) @ H, wave w = tokens 64w .. 64w + 63, per token its 4 head rows staged in the wave's LDS
+  // rows; lane 16 hh + jj builds dims 8 jj .. 8 jj + 7 of row hh and gets dims jj + 16 i back from the chain
+  float hl[16];
+  const int hh = lane >> 4, jj = lane & 15;
+  hadamard_low(hl, jj);
+  float* xrow = &xbuf[w][hh * VROW];
   for (int tt = 0; tt < 64; ++tt) {
     const int t = 64 * w + tt;
-    float* xb = xbuf[w][tt & 1];
     {
-      const float vsc = f8d(s[VSC_O + t * 2 + (rr >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (rr >> 1)]);
-      const uint8_t* vb = s + VB_O + (t * 4 + rr) * 16;
+      const float vsc = f8d(s[VSC_O + t * 2 + (hh >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (hh >> 1)]);
+      const uint8_t* vb = s + VB_O + (t * 4 + hh) * 16;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = e0 + e;
+        const int d = 8 * jj + e;
         const float bit = (float)((vb[d & 15] >> (d >> 4)) & 1u);
-        xb[rr * 128 + d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
+        xrow[d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();   // a wave's LDS instructions run in order: this token's rows, then its reads
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float y[8];
+    hadamard_row8(xrow, hl, y);
+    float* vo = vout + ((m * BLK + t) * 4 + hh) * 128 + jj;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float ya, yb;
-      hadamard_chain(xb + r * 128, hcol, ya, yb);
-      float* vo = vout + ((m * BLK + t) * 4 + r) * 128;
-      vo[lane] = ya;
-      vo[lane + 64] = yb;
-    }
+    for (int i = 0; i < 8; ++i) vo[16 * i] = y[i];
   }
 }
 
@@ -550,63 +479,45 @@ __global__ void __launch_bounds__(256) fake_quant_k_kernel(const float* __restri
 
 // fake_quant_v: v (N, 4, 128) fp32 -> per token y = v H (the quantizer's sequential fma chain), one bit per dim with
 // fp8 lo / scale per pair of heads, then (bit * sc8 + lo8) H with the dequantizer's chain: the V value of a
-// quantize -> dequantize round trip. One wave per token at a time, the token's rows staged in LDS.
+// quantize -> dequantize round trip. One wave per token at a time, the token's rows staged in LDS; lane 16 hh + jj
+// holds dims jj + 16 i of row hh in both chains (the quantizer's scales and bit test as in quantize_v).
 constexpr int FQV_TPW = 8;   // tokens per wave
 __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restrict__ v, int64_t N,
                                                            float* __restrict__ out) {
-  __shared__ __align__(16) float xb[4][4][128];   // per wave: the token's 4 rows (v, then the dequantized y)
+  __shared__ __align__(16) float xb[4][4 * VROW];   // per wave: the token's 4 rows (v, then the dequantized values)
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float hcol[64];
-  hadamard_column(hcol, lane);
-  float* X = &xb[w][0][0];
+  const int hh = lane >> 4, jj = lane & 15;
+  float hl[16];
+  hadamard_low(hl, jj);
+  float* xrow = &xb[w][hh * VROW];
   const int64_t t0 = ((int64_t)blockIdx.x * 4 + w) * FQV_TPW;
 #pragma unroll 1
   for (int tt = 0; tt < FQV_TPW; ++tt) {
     const int64_t t = t0 + tt;
     if (t >= N) break;   // uniform over the wave
-    const float4* src = reinterpret_cast<const float4*>(v + t * 512);
-    const float4 a = src[lane], b = src[64 + lane];
-    reinterpret_cast<float4*>(X)[lane] = a;
-    reinterpret_cast<float4*>(X)[64 + lane] = b;
-    __builtin_amdgcn_wave_barrier();
-    float ya[4], yb[4];
-#pragma unroll 1
-    for (int r = 0; r < 4; r += 2) {   // a runtime loop: two rows' reads at a time keep the registers bounded
-      float a2[2], b2[2];
-      hadamard_chain2(X + r * 128, X + (r + 1) * 128, hcol, a2, b2);
-      ya[r] = a2[0]; ya[r + 1] = a2[1];
-      yb[r] = b2[0]; yb[r + 1] = b2[1];
-    }
-    float za[4], zb[4];
+    const float4* src = reinterpret_cast<const float4*>(v + (t * 4 + hh) * 128 + 8 * jj);
+    const float4 a = src[0], b = src[1];
+    *reinterpret_cast<float4*>(xrow + 8 * jj) = a;
+    *reinterpret_cast<float4*>(xrow + 8 * jj + 4) = b;
+    __builtin_amdgcn_wave_barrier();   // a wave's LDS instructions run in order
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float y[8];
+    hadamard_row8(xrow, hl, y);
+    const VScales sc = v_scales(y, lane);
+    const float half = sc.den * 0.5f;
+    float z[8];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float lo = wave_min(fminf(fminf(ya[2 * g], yb[2 * g]), fminf(ya[2 * g + 1], yb[2 * g + 1])));
-      const float hi = wave_max(fmaxf(fmaxf(ya[2 * g], yb[2 * g]), fmaxf(ya[2 * g + 1], yb[2 * g + 1])));
-      const float lof = f8d(f8e(lo)), scf = f8d(f8e(clamp_min_1e8(__fsub_rn(hi, lo))));
-      const float den = clamp_min_1e8(scf);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int r = 2 * g + u;
-        const float ba = fminf(fmaxf(__builtin_rintf(__fdiv_rn(__fsub_rn(ya[r], lof), den)), 0.f), 1.f);
-        const float bb = fminf(fmaxf(__builtin_rintf(__fdiv_rn(__fsub_rn(yb[r], lof), den)), 0.f), 1.f);
-        za[r] = __fadd_rn(__fmul_rn(ba, scf), lof);
-        zb[r] = __fadd_rn(__fmul_rn(bb, scf), lof);
-      }
-    }
+    for (int i = 0; i < 8; ++i)
+      z[i] = __fadd_rn(__fmul_rn((__fsub_rn(y[i], sc.lof) > half) ? 1.f : 0.f, sc.scf), sc.lof);
     __builtin_amdgcn_wave_barrier();   // every lane has read the v rows
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { X[r * 128 + lane] = za[r]; X[r * 128 + 64 + lane] = zb[r]; }
+    for (int i = 0; i < 8; ++i) xrow[jj + 16 * i] = z[i];
     __builtin_amdgcn_wave_barrier();
-#pragma unroll 1
-    for (int r = 0; r < 4; r += 2) {
-      float oa[2], ob[2];
-      hadamard_chain2(X + r * 128, X + (r + 1) * 128, hcol, oa, ob);
-      out[t * 512 + r * 128 + lane] = oa[0];
-      out[t * 512 + r * 128 + 64 + lane] = ob[0];
-      out[t * 512 + (r + 1) * 128 + lane] = oa[1];
-      out[t * 512 + (r + 1) * 128 + 64 + lane] = ob[1];
-    }
-    __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite X
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    hadamard_row8(xrow, hl, y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[(t * 4 + hh) * 128 + jj + 16 * i] = y[i];
+    __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite the staged rows
   }
 }
 
@@ -639,7 +550,7 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
                                                       int64_t qpool_bytes, int64_t epool_elems,
                                                       const int64_t* __restrict__ out_off, uint16_t* __restrict__ kout,
                                                       uint16_t* __restrict__ vout) {
-  __shared__ __align__(16) float xbuf[4][512];   // per wave: one token's 4 dequantized V rows
+  __shared__ __align__(16) float xbuf[4][4 * VROW];   // per wave: one token's 4 dequantized V rows
   __shared__ float klo_s[512], ksc_s[512];
   const int r = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int n = P.N[r], p0 = blockIdx.x * BLK;
@@ -681,12 +592,12 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
       *reinterpret_cast<uint4*>(ko) = pack_bf16x8(a);
       *reinterpret_cast<uint4*>(ko + 64) = pack_bf16x8(b);
     }
-    // V: wave w takes tokens w, w + 4, ...; lane (head lane / 16, dims 8 (lane % 16) ..) builds bit vsc + vlo, then the
-    // four Hadamard chains (lane = dims lane, lane + 64)
-    float hcol[64];
-    hadamard_column(hcol, lane);
-    float* xb = xbuf[w];
-    const int rr = lane >> 4, e0 = 8 * (lane & 15);
+    // V: wave w takes tokens w, w + 4, ...; lane 16 hh + jj builds dims 8 jj .. 8 jj + 7 of bit vsc + vlo for row hh,
+    // then gets dims jj + 16 i of that row from the chain
+    float hl[16];
+    const int hh = lane >> 4, jj = lane & 15;
+    hadamard_low(hl, jj);
+    float* xrow = &xbuf[w][hh * VROW];
     for (int t = w; t < cnt; t += 4) {
       uint16_t* vo = vout + (ob + t) * 512;
       if (!ok) {
@@ -694,25 +605,21 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
         continue;
       }
       {
-        const float vsc = f8d(s[VSC_O + t * 2 + (rr >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (rr >> 1)]);
-        const uint8_t* vb = s + VB_O + (t * 4 + rr) * 16;
+        const float vsc = f8d(s[VSC_O + t * 2 + (hh >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (hh >> 1)]);
+        const uint8_t* vb = s + VB_O + (t * 4 + hh) * 16;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int d = e0 + e;
+          const int d = 8 * jj + e;
           const float bit = (float)((vb[d & 15] >> (d >> 4)) & 1u);
-          xb[rr * 128 + d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
+          xrow[d] = __fadd_rn(__fmul_rn(bit, vsc), vlo);
         }
       }
       __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      float y[8];
+      hadamard_row8(xrow, hl, y);
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        float ya, yb;
-        __builtin_amdgcn_sched_barrier(0);
-        hadamard_chain(xb + h * 128, hcol, ya, yb);
-        vo[h * 128 + lane] = (uint16_t)f2bf(ya);
-        vo[h * 128 + 64 + lane] = (uint16_t)f2bf(yb);
-      }
-      __builtin_amdgcn_wave_barrier();   // the next token's rows overwrite xb
+      for (int i = 0; i < 8; ++i) vo[hh * 128 + jj + 16 * i] = (uint16_t)f2bf(y[i]);
     }
     return;
   }
