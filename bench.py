@@ -3,7 +3,8 @@ over 64 sequences x 32,768 tokens (127 quantized 256-token sub-blocks + 256 exac
 tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape; same bytes and flops per token as
 32 / 8 / 64).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--e2e-only] [--e2e-steps S] [--calib]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--calib]
+                    [--c2-only | --c4-only | --e2e-only [--e2e-which both|256|398] [--e2e-steps S]]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Warm-up: the GPU reaches its sustained-load clocks only after tens of milliseconds of work (the first 50 C3 kernel
@@ -16,8 +17,11 @@ cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on
 oracle's time beside it). Extra
 fields: flush_c2 (the flush kernel alone), c4 (config 4, one decode step of all 6 attention
 layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
-sequences) and e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens). --calib runs a plain copy of known size instead (rocprof FETCH/WRITE calibration)."""
+sequences) and e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens). Every
+timed loop runs with the interpreter's garbage collector frozen (frozen_heap). --calib runs a plain copy of known size
+instead (rocprof FETCH/WRITE calibration)."""
 import argparse
+import gc
 import json
 import os
 import sys
@@ -50,6 +54,25 @@ def measured_traffic():
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class frozen_heap:
+    """Runs a timed loop with the interpreter's collector off: collects once, moves every live object to the permanent
+    generation (gc.freeze) and disables collection until the block ends. A full collection of this process's heap takes
+    ~40 ms (torch's import alone leaves ~10^6 objects); one landing inside a timed loop stalls the launches that long
+    (measured: one 40 ms idle gap on the GPU in an otherwise unchanged C4 loop, 2.2 -> 3.5 ms per step). A serving
+    engine freezes its heap after start-up for the same reason."""
+
+    def __enter__(self):
+        gc.collect()
+        gc.freeze()
+        gc.disable()
+        return self
+
+    def __exit__(self, *exc):
+        gc.enable()
+        gc.unfreeze()
+        return False
 
 
 def build_layer(torch, kh, seed, dev):
@@ -109,16 +132,17 @@ def bench_flush_c2(torch, kh, dev, steps, warmup):
     def flush():
         kh.flush(epool, eoff, C2_EBS, C2_EBS * 256, 256, 128, qpool, qbt, 1280, 262144, nq0, nq1, C2_NQ)
 
-    for _ in range(warmup):
-        flush()
-    torch.cuda.synchronize()
     s = torch.cuda.current_stream(dev)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for e0, e1 in ev:
-        e0.record(s)
-        flush()
-        e1.record(s)
-    ev[-1][1].synchronize()
+    with frozen_heap():
+        for _ in range(warmup):
+            flush()
+        torch.cuda.synchronize()
+        for e0, e1 in ev:
+            e0.record(s)
+            flush()
+            e1.record(s)
+        ev[-1][1].synchronize()
     ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
     gbps = (C2_READ + C2_WRITE) / (ms * 1e-3) / 1e9
     return {"workload": "C2: flush of 64 seqs x 2048-token chunk = 448 sub-blocks, vLLM page geometry, shuffled "
@@ -184,14 +208,15 @@ def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
             q, k, v = qkv[l]
             layers[l].forward(q, k, v, me[C4_GROUP[l]], mq, hosts=layers, cos_t=cos, sin_t=sin)
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(warmup, warmup + steps):
-        step(i)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    with frozen_heap():
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            step(i)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
     # one more step (past the timed ones) whose layer outputs are checked
     me, mq = metas[-1]
     outs = [layers[l].forward(*qkv[l], me[C4_GROUP[l]], mq, hosts=layers, cos_t=cos, sin_t=sin)
@@ -251,11 +276,12 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
         tokens = model.greedy(tokens, attn.begin_step())
         advance = lambda: model.greedy(tokens, attn.begin_step())
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps - 1):
-        tokens = advance()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    with frozen_heap():
+        t0 = time.perf_counter()
+        for _ in range(steps - 1):
+            tokens = advance()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
     assert bool(((tokens >= 0) & (tokens < cfg.vocab)).all())
     ctx = L0 + steps
     prompts = "U[1K, 32K]" if lens is None else f"{int(L0.min())}..{int(L0.max())} tokens"
@@ -338,7 +364,10 @@ def main():
     ap.add_argument("--c3-only", action="store_true", help="skip the C2 / C4 / C5 workloads (counter passes of the C3 kernel)")
     ap.add_argument("--e2e-only", action="store_true", help="only the C5 decode loop; prints its record")
     ap.add_argument("--c2-only", action="store_true", help="only the C2 flush (counter passes of the flush kernel)")
+    ap.add_argument("--c4-only", action="store_true", help="only the C4 step; prints its record")
     ap.add_argument("--e2e-steps", type=int, default=128)
+    ap.add_argument("--e2e-which", choices=("both", "256", "398"), default="both",
+                    help="with --e2e-only: the 256-sequence loop, the 398 x 32K one, or both")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the 800h path shards by "
@@ -351,12 +380,22 @@ def main():
     torch.cuda.set_device(dev)
 
     if a.e2e_only:
-        print(json.dumps({"e2e": bench_e2e(torch, dev, a.e2e_steps),
-                          "e2e_398x32k": bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)}), flush=True)
+        rec = {}
+        if a.e2e_which in ("both", "256"):
+            rec["e2e"] = bench_e2e(torch, dev, a.e2e_steps)
+            torch.cuda.empty_cache()
+        if a.e2e_which in ("both", "398"):
+            rec["e2e_398x32k"] = bench_e2e(torch, dev, 32, lens=[C4_MAX] * C4_R)
+        print(json.dumps(rec), flush=True)
         return
 
     if a.c2_only:
         print(json.dumps({"flush_c2": bench_flush_c2(torch, kh, dev, a.steps, a.warmup)}), flush=True)
+        return
+
+    if a.c4_only:
+        cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
+        print(json.dumps({"c4": bench_c4(torch, kh, dev, max(5, min(a.steps, 20)), 20, cos4, sin4)}), flush=True)
         return
 
     if a.calib:
@@ -385,14 +424,15 @@ def main():
     log(f"built 2 cache copies in {time.perf_counter() - t_build:.1f} s")
 
     # ---- whole-layer timing: W warmup + K timed steps, synchronized on both sides
-    for i in range(a.warmup):
-        kh.decode(layers[i & 1], q, cos, sin)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(a.steps):
-        kh.decode(layers[i & 1], q, cos, sin)
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / a.steps
+    with frozen_heap():
+        for i in range(a.warmup):
+            kh.decode(layers[i & 1], q, cos, sin)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(a.steps):
+            kh.decode(layers[i & 1], q, cos, sin)
+        torch.cuda.synchronize()
+        ms_step = (time.perf_counter() - t0) * 1e3 / a.steps
 
     # ---- dominant kernel alone (decode_quant), HIP events on the stream it runs on
     import ctypes
@@ -416,15 +456,15 @@ def main():
         assert rc == 0, L.kv800_hip_last_error()
 
     # one event pair around each launch, so the average is the kernel's own duration (no dispatch gaps)
-    with torch.cuda.stream(s):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
+    with torch.cuda.stream(s), frozen_heap():
         for i in range(a.warmup):
             quant(i)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
         for i in range(a.steps):
             ev[i][0].record(s)
             quant(i)
             ev[i][1].record(s)
-    ev[-1][1].synchronize()
+        ev[-1][1].synchronize()
     ms_quant = sum(e0.elapsed_time(e1) for e0, e1 in ev) / a.steps
     torch.cuda.synchronize()
 
@@ -444,13 +484,14 @@ def main():
                                  N=C(P0.N), NQ=C(P0.NQ), nqmax=P0.nqmax, win=P0.win) if not a.no_cpu else None
     host_q, host_cos, host_sin = C(q), C(cos), C(sin)
 
-    # ---- the other BASELINE configs with a GPU workload: C2 (flush alone) and C4 (6-layer decode step)
+    # ---- the other BASELINE configs with a GPU workload: C2 (flush alone), C4 (6-layer decode step), C5 (engine loop)
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
     flush_c2 = c4 = e2e = e2e_398 = None
     if not a.c3_only:
         flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 200)
+        torch.cuda.empty_cache()
         cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
         c4 = bench_c4(torch, kh, dev, extra_steps, 20, cos4, sin4)
         del cos4, sin4
