@@ -185,3 +185,109 @@ def test_step_meta_matches_torch(hip):
     lens[4], lens[5] = 0, pages * ebs + 1
     slot, pos, _ = kv800_hip.step_meta(bt, lens, ebs)
     assert int(slot[4]) == -1 and int(pos[4]) == -1 and int(slot[5]) == -1 and int(pos[5]) == pages * ebs
+
+
+def test_vllm_decode_step_full_size(hip, oracle):
+    """BASELINE config 4's shape through the vLLM cache path: 398 rows with lengths U[1K, 32K] (rows 0-7 placed so
+    the step flushes a sub-block), a window + sinks layer (2, exact group B) and quantized layers 6 (group A) and 10
+    (group B) whose aux areas host layer 2's sinks. Caches hold N(0,1) bf16 histories written straight into shuffled
+    exact pages; the sub-blocks flushed before the step are quantized from those pages by the HIP quantizer. One step
+    (flushes ahead on the side stream, then each layer's write + decode): every output finite, and sampled rows
+    (shortest, longest, a flushing row, three more) within the decode bar of the oracle on their full histories."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    dev = torch.device(DEV)
+    R, lo_n, hi_n = 398, 1024, 32768
+    rng = np.random.RandomState(41)
+    L0 = rng.randint(lo_n, hi_n + 1, size=R).astype(np.int64)
+    L0[:8] = 256 * rng.randint(5, 120, size=8) + 127          # n - 128 = 256 k: sub-block k - 1 flushes this step
+    n = L0 + 1
+    nq_prev = np.maximum(L0 - 128, 0) // 256
+    assert ((np.maximum(n - 128, 0) // 256) > nq_prev).sum() >= 8
+    layers, group = (2, 6, 10), {2: "B", 6: "A", 10: "B"}
+    g = torch.Generator(device=dev).manual_seed(41)
+    # exact pages: row r owns ceil(n_r / 128) shuffled pages of group A and of group B
+    need = (n + EBS - 1) // EBS
+    epr = int(need.max())
+    bt = {}
+    for grp in "AB":
+        perm = rng.permutation(int(need.sum()))
+        t = np.zeros((R, epr), np.int32)
+        t[np.arange(epr)[None, :] < need[:, None]] = perm
+        bt[grp] = t
+    qneed = (n + QBLOCK - 1) // QBLOCK
+    qpr = int(qneed.max())
+    qbt = np.zeros((R, qpr), np.int32)
+    qbt[np.arange(qpr)[None, :] < qneed[:, None]] = rng.permutation(int(qneed.sum()))
+    say("full size: rows", R, "tokens", int(n.sum()), "exact pages per group", int(need.sum()))
+    ev, qv = {}, {}
+    for l in layers:
+        e = torch.empty(int(need.sum()), 4, EBS, 256, dtype=torch.bfloat16, device=dev)
+        for i in range(0, e.shape[0], 4096):
+            e[i:i + 4096] = torch.randn(e[i:i + 4096].shape, generator=g, device=dev).to(torch.bfloat16)
+        ev[l] = e
+    btd = {grp: torch.from_numpy(bt[grp]).to(dev).long() for grp in "AB"}
+
+    def rows_kv(l, rows, p0, p1):
+        """(len(rows), p1 - p0, 4, 128) K and V of positions [p0, p1) from the exact pages."""
+        pos = torch.arange(p0, p1, device=dev)
+        pg = btd[group[l]][torch.as_tensor(rows, device=dev)][:, pos // EBS]
+        blk = ev[l][pg, :, (pos % EBS)[None, :].expand_as(pg)]          # (rows, P, 4, 256)
+        return blk[..., :128], blk[..., 128:]
+
+    # quant pages: every sub-block j < nq_prev[r] from the HIP quantizer
+    pairs = [(r, j) for r in range(R) for j in range(int(nq_prev[r]))]
+    for l in (6, 10):
+        q_l = torch.zeros(int(qneed.sum()), QPAGE, dtype=torch.uint8, device=dev)
+        slots = q_l[:, :AUX].view(-1, 5, 51200)
+        for i in range(0, len(pairs), 2048):
+            part = pairs[i:i + 2048]
+            rr = torch.as_tensor([r for r, _ in part], device=dev)
+            pos = torch.as_tensor([256 * j for _, j in part], device=dev)[:, None] + torch.arange(256, device=dev)
+            pg = btd[group[l]][rr[:, None], pos // EBS]
+            blk = ev[l][pg, :, pos % EBS]                                  # (m, 256, 4, 256)
+            sb = hip.quantize_blocks(blk[..., :128].contiguous(), blk[..., 128:].contiguous())
+            qpage = torch.as_tensor([int(qbt[r, 256 * j // QBLOCK]) for r, j in part], device=dev)
+            qslot = torch.as_tensor([(256 * j) % QBLOCK // 256 for _, j in part], device=dev)
+            slots[qpage, qslot] = sb
+        qv[l] = q_l
+    # layer 2's sinks (positions 0-3): K in layer 6's aux, V in layer 10's, at each row's first quant page
+    ks, vs = rows_kv(2, list(range(R)), 0, 4)
+    for host, arr in ((6, ks), (10, vs)):
+        aux = qv[host].view(torch.bfloat16).view(-1, QPAGE // 2)[:, AUX // 2:AUX // 2 + 2048]
+        aux[torch.from_numpy(qbt[:, 0]).to(dev).long()] = arr.reshape(R, 2048)
+    torch.cuda.synchronize()
+
+    lay = {l: vc.KV800DecodeLayer(l, ev[l], qv.get(l)) for l in layers}
+    metas = {grp: vc.step_meta(torch.from_numpy(bt[grp]), torch.from_numpy(n), EBS, DEV) for grp in "AB"}
+    mq = vc.step_meta(torch.from_numpy(qbt), torch.from_numpy(n), QBLOCK, DEV)
+    cos, sin = oracle.rope_tables(hi_n + 64)
+    cos_d, sin_d = bf16_dev(cos), bf16_dev(sin)
+    qs = {l: torch.randn(R, 16, 128, generator=g, device=dev).to(torch.bfloat16) for l in layers}
+    kn = {l: torch.randn(R, 4, 128, generator=g, device=dev).to(torch.bfloat16) for l in layers}
+    vn = {l: torch.randn(R, 4, 128, generator=g, device=dev).to(torch.bfloat16) for l in layers}
+    say("full size: step")
+    vc.launch_flushes(list(lay.values()), {l: metas[group[l]] for l in layers}, mq)
+    outs = {l: lay[l].forward(qs[l], kn[l], vn[l], metas[group[l]], mq, hosts=lay, cos_t=cos_d, sin_t=sin_d)
+            for l in layers}
+    torch.cuda.synchronize()
+    for l in layers:
+        assert bool(torch.isfinite(outs[l].float()).all()), l
+
+    sample = sorted({int(np.argmin(n)), int(np.argmax(n)), 3, *rng.choice(np.arange(8, R), 3, replace=False).tolist()})
+    for l in layers:
+        Ks, Vs = [], []
+        for r in sample:
+            K, V = rows_kv(l, [r], 0, int(n[r]))
+            assert torch.equal(K[0, -1], kn[l][r]) and torch.equal(V[0, -1], vn[l][r]), (l, r)   # the step's row
+            Ks.append(bits_of(K[0]))
+            Vs.append(bits_of(V[0]))
+        case = oracle.build_paged(lambda b, p0, p1: (Ks[b][p0:p1], Vs[b][p0:p1]), [int(n[r]) for r in sample],
+                                  win=256 if l == 2 else 0, ebs=EBS, shuffle_seed=l)
+        want = oracle.decode(case, bits_of(qs[l][sample]), cos, sin)
+        o = outs[l][sample].float().cpu().numpy()
+        w = torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()
+        d = np.abs(o - w)
+        say(f"full size layer {l}: rows {sample} max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
+    del ev, qv, lay, outs
+    torch.cuda.empty_cache()
