@@ -1,4 +1,4 @@
-"""Benchmark of the 800h decode path on one MI355X: BASELINE config 3, one layer of paged split-K decode attention
+"""Benchmark of the 800h decode path on one MI355X: one layer of paged split-K decode attention
 over 64 sequences x 32,768 tokens (127 quantized 256-token sub-blocks + 256 exact tokens per sequence, permuted page
 tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape; same bytes and flops per token as
 32 / 8 / 64).
@@ -15,7 +15,7 @@ JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200
 duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
 cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on a sample of the same rows (the C
 oracle's time beside it). Extra
-fields: flush_c2 (the flush kernel alone), c4 (config 4, one decode step of all 6 attention
+fields: flush_c2 (config C2, the flush kernel alone), c4 (config 4, one decode step of all 6 attention
 layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
 sequences) and e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens). Every
 timed loop runs with the interpreter's garbage collector frozen (frozen_heap). --calib runs a plain copy of known size
@@ -111,7 +111,7 @@ FMA_PEAK = 256 * 64 * 2.4e9                         # non-packed fp32 fma/s: 256
 
 
 def bench_flush_c2(torch, kh, dev, steps, warmup):
-    """BASELINE config 2, the flush kernel alone: 64 sequences x a 2048-token prefill chunk in vLLM-geometry exact
+    """config C2, the flush kernel alone: 64 sequences x a 2048-token prefill chunk in vLLM-geometry exact
     pages (128 tokens x 4 heads x [K128 | V128] bf16 per page, shuffled physical pages), K / V ~ N(0,1) with 1 % of
     the elements x 8, flushed by one launch into shuffled 1280-token quant pages (5 x 51,200 B per 262,144-B page):
     448 sub-blocks. Per-launch HIP events on the current stream."""
@@ -157,7 +157,7 @@ C4_GROUP = {6: "A", 14: "A", 22: "A", 2: "B", 10: "B", 18: "B"}   # two exact KV
 
 
 def bench_c4(torch, kh, dev, steps, warmup, cos, sin):
-    """the 6 attention layers of an LFM3-1.7B-shaped stack (quantized 6, 10, 14, 22; window + sinks
+    """config C4: the 6 attention layers of an LFM3-1.7B-shaped stack (quantized 6, 10, 14, 22; window + sinks
     2, 18) over 398 sequences with lengths U[1K, 32K] (seeded), vLLM page geometry (exact: 128-token pages in two exact
     KV groups; quant: 1280-token pages in one group, sinks in the hosts' aux), one decode step per layer per step:
     the new token's rows, the flush of the sub-blocks that became eligible, decode tables and decode
@@ -238,7 +238,7 @@ E2E_R, E2E_MIN, E2E_MAX = 256, 1024, 32768
 
 
 def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
-    """greedy decode of a random-init LFM3-1.7B-shaped model (lfm3-kv800_amd/model.py: 24 layers,
+    """config C5: greedy decode of a random-init LFM3-1.7B-shaped model (lfm3-kv800_amd/model.py: 24 layers,
     13 short-conv, 6 full-attention on the 800h caches, 5 sliding-window; weights N(0, 0.02) bf16) over 256 sequences
     with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps; `lens` replaces the prompt lengths (the reference's
     published throughput point is 398 sequences of 32,768 tokens, RESULTS_RELEASE.md:90-96). tok/s = c (steps - 1) /
@@ -484,7 +484,7 @@ def main():
                                  N=C(P0.N), NQ=C(P0.NQ), nqmax=P0.nqmax, win=P0.win) if not a.no_cpu else None
     host_q, host_cos, host_sin = C(q), C(cos), C(sin)
 
-    # ---- the other BASELINE configs with a GPU workload: C2 (flush alone), C4 (6-layer decode step), C5 (engine loop)
+    # ---- the other BASELINE.json configs with a GPU workload: C2 (flush alone), C4 (6-layer decode step), C5 (engine loop)
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))

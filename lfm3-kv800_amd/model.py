@@ -1,4 +1,4 @@
-"""Decode loop of an LFM3-1.7B-shaped model whose attention layers run on the 800h path, without
+"""Decode loop of an LFM3-1.7B-shaped model whose attention layers run on the 800h path (config C5), without
 vLLM.
 
 The layer stack follows the reference's vLLM model (vllm_model.py:542-653) and its attention routing with

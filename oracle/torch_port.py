@@ -7,7 +7,7 @@ times the fp8 scale plus the fp8 offset, rounded to bf16; 1-bit V planes times t
 normalised Hadamard), the exact rows gathered from their pages, the sinks of window layers, every key rotated on the
 dim pairs (d, d + 64), d < 32, in fp32 and rounded to bf16, then one fp32 softmax over all positions (scale 128^-0.5)
 with 4 query heads per KV head. tests/test_oracle.py pins it against the C oracle (oracle/kv800_oracle.c) on the
-BASELINE config-1 inputs. Only tests/ and bench.py's cpu_baseline leg import it."""
+config C1 inputs. Only tests/ and bench.py's cpu_baseline leg import it."""
 import torch
 
 BLK, SUB, NSINK = 256, 51200, 4

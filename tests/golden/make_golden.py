@@ -6,7 +6,7 @@ regenerate them with case_inputs() and check them against the stored SHA-256.
 
 Cases (inputs from numpy's legacy RandomState, float32 normals rounded to bf16):
   parity : 2 sub-blocks, K = N(0,1) + 3 N(0,1) per-channel offset, V = N(0,1)  (tests/test_parity.py:85-86 shape)
-  outlier: 2 sub-blocks, K, V = N(0,1) with 1 % of the elements x 8              (BASELINE config 2)
+  outlier: 2 sub-blocks, K, V = N(0,1) with 1 % of the elements x 8              (config C2)
   edge   : 1 sub-block with constant channels (hi == lo), tiny and large magnitudes near fp8 boundaries, and
            V rows whose Hadamard transform is constant (all-equal V)
   scaled : 4 sub-blocks, K, V = 4 N(0,1) (SHA-256 of each 51,200-byte block only)."""

@@ -1,4 +1,4 @@
-"""The LFM3-shaped decode model (lfm3-kv800_amd/model.py) on an MI355X: its attention layers on the
+"""The LFM3-shaped decode model (lfm3-kv800_amd/model.py, config C5) on an MI355X: its attention layers on the
 HIP path (vLLM page geometry: quantized, window + sinks and native sliding layers) against the same model, same
 weights and conv states, whose attention is the CPU oracle's torch_decode restatement over each layer's full K / V
 history (quantized by the oracle quantizer, sinks and windows as torch_decode.py:27-80 selects them). Teacher forcing:

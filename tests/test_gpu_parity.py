@@ -2,7 +2,7 @@
 
 Bars:
   * quantizer / flush / dequantizer: bit-exact with the oracle and the golden fixtures;
-  * decode, every input (the BASELINE configs' N(0, 1) q / K / V, the reference's own 12 parity cases with K offset
+  * decode, every input (the benchmark configurations' N(0, 1) q / K / V, the reference's own 12 parity cases with K offset
     per channel by 3 N(0, 1) and q x 2, ragged batches, fp8 range edges): within 2e-2 max-abs and 1e-3 mean-abs of the
     oracle's restatement of torch_decode.py (both bf16 outputs, same cache bytes), and for the 12 parity cases also the
     reference's own bar, rel < 1e-2 against its independent check (tests/test_parity.py:104)."""
@@ -157,7 +157,7 @@ def test_flush_two_kv_groups(hip, oracle, latency):
 
 
 def test_flush_c2_full_size(hip, oracle):
-    """BASELINE config 2 at full size: 64 sequences x a 2048-token chunk in vLLM-geometry exact pages (shuffled), K / V
+    """config C2 at full size: 64 sequences x a 2048-token chunk in vLLM-geometry exact pages (shuffled), K / V
     ~ N(0,1) with 1 % of the elements x 8, one flush launch into shuffled 1280-token quant pages: all 448 sub-blocks
     (the flush rule gives 7 per sequence) must equal the oracle quantizer's bytes."""
     B, n, ebs = 64, 2048, 128
@@ -236,7 +236,7 @@ def test_decode_reference_cases(hip, oracle, win, n):
 
 @pytest.mark.parametrize("B,n", [(4, 1024), (2, 384), (3, 5000), (1, 9000)])
 def test_decode_baseline_inputs(hip, oracle, B, n):
-    """BASELINE config 1 (B = 4, n = 1024, q / K / V ~ N(0, 1)) and other lengths, shuffled pages: the strict bar."""
+    """config C1 (B = 4, n = 1024, q / K / V ~ N(0, 1)) and other lengths, shuffled pages: the strict bar."""
     rng = np.random.RandomState(B * 1000 + n)
     K = oracle.randn_bf16(rng, (B, n, 4, 128)); V = oracle.randn_bf16(rng, (B, n, 4, 128))
     q = oracle.randn_bf16(rng, (B, 16, 128))
@@ -344,7 +344,7 @@ def test_decode_stages_and_merge(hip, oracle):
 
 
 def test_decode_full_size_all_rows(hip, oracle):
-    """BASELINE config 3 at full size (64 x 32,768, permuted tables): cache built on the GPU by the HIP quantizer,
+    """config C3 at full size (64 x 32,768, permuted tables): cache built on the GPU by the HIP quantizer,
     decoded by the HIP kernels; every row is decoded again by the oracle from the downloaded pages (the strict bar), and
     every output is finite and within the range of its row's dequantized values."""
     import lfm3_kv800_amd.kv800 as kv

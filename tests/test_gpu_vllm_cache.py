@@ -188,7 +188,7 @@ def test_step_meta_matches_torch(hip):
 
 
 def test_vllm_decode_step_full_size(hip, oracle):
-    """BASELINE config 4's shape through the vLLM cache path: 398 rows with lengths U[1K, 32K] (rows 0-7 placed so
+    """the shape of config C4 through the vLLM cache path: 398 rows with lengths U[1K, 32K] (rows 0-7 placed so
     the step flushes a sub-block), a window + sinks layer (2, exact group B) and quantized layers 6 (group A) and 10
     (group B) whose aux areas host layer 2's sinks. Caches hold N(0,1) bf16 histories written straight into shuffled
     exact pages; the sub-blocks flushed before the step are quantized from those pages by the HIP quantizer. One step
