@@ -476,7 +476,7 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 // The table lookups of one instruction touch 4 tables (one per lane group) whose entries sit in disjoint LDS banks.
 constexpr int QWAVES = 4;
 constexpr float QLAZY = 0.f;   // rescale threshold (log2 units): p <= 2^QLAZY, and p vsc <= 448 stays far below 65,504
-constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 3;   // balanced schedule: sub-blocks per workgroup, most rounds
+constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 1;   // balanced schedule: sub-blocks per workgroup, most rounds
 constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
 constexpr int QROW = 132;
 constexpr int VBH = 34;        // staged vb rows per head: 32 + 2 of padding put head h + 2 16 banks away from head h
@@ -863,8 +863,9 @@ struct ExactArgs {
 //     one (which starts a row b) to slot groups + b, since no other workgroup enters row b from an earlier row. Every
 //     workgroup but the last has exactly C sub-blocks, however ragged the rows are.
 // Uniform rows whose count divides into whole rounds (64 x 127 sub-blocks: 8 slices of 16 a row, 512 workgroups,
-// one round) keep one segment per workgroup; otherwise the list-wise cut avoids a nearly empty last round (398 x 127:
-// 1592 slices of 33 is 4 rounds of 512, the list-wise cut 1532 pieces of 33, 3 rounds). The exact partial of row b is
+// one round) keep one segment per workgroup; otherwise the list-wise cut avoids a nearly empty last round (398 x 127
+// sub-blocks over 512 workgroups: 796 row-wise slices of 99 would take 2 rounds, the list-wise cut's 511 pieces of
+// 99 take one). The exact partial of row b is
 // slot groups + B + b. groups = 0: the fixed (row, split) grid, split s of row b in slot b (ns + 1) + s, the exact
 // partial in slot b (ns + 1) + ns (the reference's partial layout).
 struct Sched {
@@ -1307,7 +1308,8 @@ int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
   KV800_REQUIRE(B >= 0 && nqmax >= 0 && groups, "plan_balanced: bad arguments");
   // about BAL_CHUNK sub-blocks per workgroup at the batch's largest size B * nqmax (ragged batches hold fewer
   // sub-blocks, and each workgroup then takes proportionally fewer); beyond one round of resident workgroups, whole
-  // rounds, at most BAL_ROUNDS
+  // rounds, at most BAL_ROUNDS (one: longer spans in a single round measured faster than two or three rounds of
+  // shorter ones at 256-400 rows of up to 32K tokens)
   const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK, res = resident_groups();
   *groups = want < 1 ? 1 : want <= res ? want : min((want + res - 1) / res, BAL_ROUNDS) * res;
   return KV800_OK;
