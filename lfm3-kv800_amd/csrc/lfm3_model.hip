@@ -14,6 +14,8 @@
 //   argmax        index of the largest bf16 logit of a row (the greedy token; torch.argmax's choice among equals)
 // rms(x) = x rsqrt(mean(x^2) + eps) in fp32. Sums run in a fixed tree order, so results equal torch's up to the
 // order of fp32 additions inside a mean or a 7-term sum.
+#include <mutex>
+
 #include "kv800_common.h"
 #include "../../include/kv800_hip.h"
 #include "../../include/lfm3_model.h"
@@ -180,7 +182,7 @@ gate_mul_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ g, 
   store8(out + i, v);
 }
 
-// ---------------------------------------------------------------- greedy token (one workgroup of 256 threads per row)
+// ---------------------------------------------------------------- greedy token (one workgroup per row)
 // (a, ia) ranks before (b, ib): the larger value, the smaller index among equals; NaN ranks above every number, the
 // first NaN first (torch.argmax)
 __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
@@ -188,27 +190,30 @@ __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
   if (na || nb) return na && (!nb || ia < ib);
   return a > b || (a == b && ia < ib);
 }
-// thread t scans the 8-element pieces t, t + 256, ... of the row, eight loads at a time; the workgroup then reduces
-// the 256 bests (the order of the compares does not matter: ranks_before breaks ties by index)
-__global__ void __launch_bounds__(256)
+// thread t scans the 8-element pieces t, t + AT, ... of the row, eight loads at a time (a 65,536-wide row is one
+// round of loads for 1,024 threads, two for 512); the workgroup then reduces the AT bests (the order of the compares
+// does not matter: ranks_before breaks ties by index). 1,024 threads a row while every row has a CU of its own (one
+// workgroup per CU at 98 VGPRs); 512 beyond that, so that two rows share a CU in one round.
+template <int AT>
+__global__ void __launch_bounds__(AT)
 argmax_kernel(const uint16_t* __restrict__ x, int64_t V, int64_t stride, int64_t* __restrict__ out) {
-  __shared__ float rv[4];
-  __shared__ int ri[4];
+  __shared__ float rv[AT / 64];
+  __shared__ int ri[AT / 64];
   const uint16_t* row = x + (int64_t)blockIdx.x * stride;
   float cv[8];
   int ci[8];   // eight independent running bests, one per in-flight piece
 #pragma unroll
   for (int u = 0; u < 8; ++u) { cv[u] = -INFINITY; ci[u] = (int)V; }   // index V ranks after every element
-  for (int64_t p0 = threadIdx.x; p0 * 8 < V; p0 += 256 * 8) {   // 8 pieces' loads in flight, then their compares
+  for (int64_t p0 = threadIdx.x; p0 * 8 < V; p0 += AT * 8) {   // 8 pieces' loads in flight, then their compares
     float f[8][8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int64_t p = p0 + 256 * u;
+      const int64_t p = p0 + AT * u;
       if (p * 8 < V) load8(row + 8 * p, f[u]);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int64_t p = p0 + 256 * u;
+      const int64_t p = p0 + AT * u;
       if (p * 8 < V) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -232,7 +237,7 @@ argmax_kernel(const uint16_t* __restrict__ x, int64_t V, int64_t stride, int64_t
   __syncthreads();
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int k = 1; k < 4; ++k)
+    for (int k = 1; k < AT / 64; ++k)
       if (ranks_before(rv[k], ri[k], bv, bi)) { bv = rv[k]; bi = ri[k]; }
     out[blockIdx.x] = bi;
   }
@@ -242,6 +247,27 @@ argmax_kernel(const uint16_t* __restrict__ x, int64_t V, int64_t stride, int64_t
 }  // namespace lfm3
 
 using namespace lfm3;
+
+// CUs of the current device (cached per device; 256 if the query fails)
+static int64_t device_cus() {
+  static std::mutex mu;
+  static int64_t cache[64] = {0};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0) {
+      (void)hipGetLastError();
+      cu = 256;
+    }
+    cache[dev] = cu;
+  }
+  return cache[dev];
+}
 
 extern "C" {
 
@@ -304,7 +330,10 @@ int lfm3_hip_argmax(const uint16_t* x, int64_t R, int64_t V, int64_t stride, int
                 "argmax: needs 0 < V < 2^31, V and the row stride multiples of 8");
   if (R == 0) return KV800_OK;
   KV800_REQUIRE(x && out && ((uintptr_t)x % 16) == 0, "argmax: null or misaligned pointer");
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)R), dim3(256), 0, (hipStream_t)stream, x, V, stride, out);
+  if (R <= device_cus())
+    hipLaunchKernelGGL(argmax_kernel<1024>, dim3((unsigned)R), dim3(1024), 0, (hipStream_t)stream, x, V, stride, out);
+  else
+    hipLaunchKernelGGL(argmax_kernel<512>, dim3((unsigned)R), dim3(512), 0, (hipStream_t)stream, x, V, stride, out);
   return kv800::check_launch("argmax");
 }
 

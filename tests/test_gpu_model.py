@@ -278,7 +278,8 @@ def test_decode_graph_replays_match_eager(hip):
 
 def test_argmax_matches_torch(hip):
     """The greedy-token kernel against torch.argmax over the same bf16 values: random rows, rows whose maximum is
-    repeated (the first index wins), rows with NaN (the first NaN wins), -inf / +inf rows and a strided view."""
+    repeated (the first index wins), rows with NaN (the first NaN wins), -inf / +inf rows and a strided view; a batch of
+    600 rows takes the 512-thread form."""
     from lfm3_kv800_amd import model_ops as mo
     g = torch.Generator(device=DEV).manual_seed(3)
     R, V = 9, 65536
@@ -293,6 +294,15 @@ def test_argmax_matches_torch(hip):
         got, want = mo.argmax(t), t.float().argmax(-1)
         say("argmax", got.tolist(), want.tolist())
         assert torch.equal(got, want)
+    # more rows than CUs: the 512-thread workgroups (two rows per CU), same special rows repeated down the batch
+    big = torch.randn(600, V, generator=g, device=DEV).to(torch.bfloat16)
+    big[::60] = x[:1].expand(10, V)
+    big[1::60] = x[1:2].expand(10, V)
+    big[3::60] = x[3:4].expand(10, V)
+    big[4::60] = x[4:5].expand(10, V)
+    got, want = mo.argmax(big), big.float().argmax(-1)
+    say("argmax 600 rows: mismatches", int((got != want).sum()))
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("R,N,K,split", [(256, 2048, 2048, 1), (256, 16384, 2048, 1), (398, 3088, 2048, 1),
