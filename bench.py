@@ -8,8 +8,9 @@ tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Warm-up: the GPU reaches its sustained-load clocks only after tens of milliseconds of work (the first 50 C3 kernel
-launches after setup average 178 us, the following ones 152 us), so every timed section follows ~50-100 ms of its own
-untimed work: W = 500 layer steps and as many kernel launches for C3, 200 flushes for C2, 20 steps for C4.
+launches after setup average 178 us, the following ones 152 us), so every timed section follows its own untimed work
+whatever --warmup says: the C3 layer steps and the C3 kernel launches each at least max(W, 300) calls and 250 ms of
+GPU time (warm_up; the JSON records what ran), 200 flushes for C2, 20 steps for C4.
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
 JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
 duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
@@ -73,6 +74,24 @@ class frozen_heap:
         gc.enable()
         gc.unfreeze()
         return False
+
+
+C3_WARM_CALLS, C3_WARM_MS = 300, 250.0
+
+
+def warm_up(torch, fn, calls, min_ms):
+    """Untimed calls of fn(i) until at least `calls` calls and `min_ms` of wall time (GPU-bound: synchronized every 50
+    calls) have run. Returns (calls, ms) actually run."""
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        fn(i)
+        i += 1
+        if i % 50 == 0 or i >= calls:
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3
+            if i >= calls and ms >= min_ms:
+                return i, round(ms, 1)
 
 
 def build_layer(torch, kh, seed, dev):
@@ -243,8 +262,9 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
     with prompt lengths U[1K, 32K] (seeded), `steps` greedy steps; `lens` replaces the prompt lengths (the reference's
     published throughput point is 398 sequences of 32,768 tokens, RESULTS_RELEASE.md:90-96). tok/s = c (steps - 1) /
     time, time from the end of the first step to the end of the last (the reference's decode tok/s,
-    RESULTS_RELEASE.md:83-85). The prompts' K / V histories are synthetic N(0, 1), written into the caches (quantized by
-    the HIP quantizer) before the first step: prompt processing is not part of the measurement. Each step is launched
+    RESULTS_RELEASE.md:83-85). The prompts' K / V histories are synthetic N(0, 1), written into the caches before the
+    first step by the attention layers' own step path in 2048-token prefill chunks (exact pages, sinks, flushes:
+    model.PagedAttention800.fill); prompt processing is not part of the measurement. Each step is launched
     kernel by kernel from the host (the loop is GPU-bound at these batch sizes: replaying one recorded HIP graph of the
     step, graph=True / model.DecodeGraph, measured the same step time)."""
     import numpy as np
@@ -255,10 +275,16 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
     R = len(L0)
     g = torch.Generator(device=dev).manual_seed(seed)
 
+    # prompt K / V: slices of per-layer N(0, 1) pools at row- and position-dependent offsets (the fill asks for each
+    # row's history in prefill chunks, ~R x 16 x 11 slices at 32K prompts)
+    POOL = 1 << 16
+    pools = {}
+
     def history(l, r, p0, p1):
-        shape = (p1 - p0, 4, 128)
-        return (torch.randn(shape, generator=g, device=dev).to(torch.bfloat16),
-                torch.randn(shape, generator=g, device=dev).to(torch.bfloat16))
+        if l not in pools:
+            pools[l] = tuple(torch.randn(POOL, 4, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
+        o = (r * 7919 + p0 * 13) % (POOL - (p1 - p0) + 1)
+        return pools[l][0][o:o + p1 - p0], pools[l][1][o:o + p1 - p0]
 
     t = time.perf_counter()
     attn = M.PagedAttention800(L0.tolist(), steps + 1, dev, seed=seed)
@@ -288,11 +314,11 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
     out = {"workload": f"greedy decode, random-init LFM3-1.7B-shaped model (hidden 2048, 24 layers: 13 conv, "
                        f"6 full attention on 800h caches, 5 sliding 256; vocab {cfg.vocab}, ffn {cfg.ffn}), "
                        f"{R} seqs, prompts {prompts}, {steps} steps",
-           "data": "synthetic N(0,1) K/V prompt histories, random token ids",
+           "data": "synthetic N(0,1) K/V prompt histories written through the mixed-step cache path, random token ids",
            "tok_s": round(R * (steps - 1) / dt, 1), "ms_per_step": round(dt * 1e3 / (steps - 1), 3),
            "steps": steps, "seqs": R, "context_tokens_end": int(ctx.sum()),
            "launch": "one HIP graph per step" if graph else "eager"}
-    del attn, model
+    del attn, model, pools
     torch.cuda.empty_cache()
     return out
 
@@ -351,6 +377,37 @@ def cpu_baseline(torch, P, q, cos, sin, rows):
     oracle.decode(case, qb, cb, sb)
     t_c = time.perf_counter() - t0
     return (t_port, threads), (t_c, oracle.num_threads())
+
+
+C1_B, C1_N, C1_ITERS = 4, 1024, 10
+
+
+def build_c1(torch, dev):
+    """config C1: one quantized layer of 4 sequences x 1024 tokens in PagedStore's default geometry
+    (ebs 64, ring of 10 pages), q / K / V ~ N(0, 1) bf16 from seed 1, written and flushed by this build's HIP path
+    (3 sub-blocks + 256 exact tokens per row). Returns (Paged, q, cos, sin) on the device."""
+    import lfm3_kv800_amd.kv800 as kv
+    g = torch.Generator(device=dev).manual_seed(1)
+    st = kv.PagedStore(C1_B, C1_N + 8, dev)
+    st.append(torch.randn(C1_B, C1_N, 4, 128, generator=g, device=dev).to(torch.bfloat16),
+              torch.randn(C1_B, C1_N, 4, 128, generator=g, device=dev).to(torch.bfloat16))
+    q = torch.randn(C1_B, 16, 128, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = rope_tables(torch, C1_N + 8, dev)
+    return st.paged(), q, cos, sin
+
+
+def cpu_baseline_c1(torch, host, threads):
+    """C1 on this host's cores: the pure-torch restatement of torch_decode.decode (oracle/torch_port.py), one warm-up
+    call then C1_ITERS timed calls. Returns ms per call."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_port
+    torch.set_num_threads(threads)
+    P, q, cos, sin = host
+    torch_port.decode(P, q, cos, sin)
+    t0 = time.perf_counter()
+    for _ in range(C1_ITERS):
+        torch_port.decode(P, q, cos, sin)
+    return (time.perf_counter() - t0) * 1e3 / C1_ITERS
 
 
 def main():
@@ -425,9 +482,8 @@ def main():
 
     # ---- whole-layer timing: W warmup + K timed steps, synchronized on both sides
     with frozen_heap():
-        for i in range(a.warmup):
-            kh.decode(layers[i & 1], q, cos, sin)
-        torch.cuda.synchronize()
+        warm_layer = warm_up(torch, lambda i: kh.decode(layers[i & 1], q, cos, sin), max(a.warmup, C3_WARM_CALLS),
+                             C3_WARM_MS)
         t0 = time.perf_counter()
         for i in range(a.steps):
             kh.decode(layers[i & 1], q, cos, sin)
@@ -458,8 +514,7 @@ def main():
     # one event pair around each launch, so the average is the kernel's own duration (no dispatch gaps)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
     with torch.cuda.stream(s), frozen_heap():
-        for i in range(a.warmup):
-            quant(i)
+        warm_kernel = warm_up(torch, quant, max(a.warmup, C3_WARM_CALLS), C3_WARM_MS)
         for i in range(a.steps):
             ev[i][0].record(s)
             quant(i)
@@ -483,6 +538,23 @@ def main():
                                  e_hs=P0.e_hs, e_ts=P0.e_ts, e_v=P0.e_v, sk=None, sv=None, skoff=None, svoff=None,
                                  N=C(P0.N), NQ=C(P0.NQ), nqmax=P0.nqmax, win=P0.win) if not a.no_cpu else None
     host_q, host_cos, host_sin = C(q), C(cos), C(sin)
+    # C1: built and timed on the GPU here (whole kv800.decode call), its host copy timed on the CPU at the end
+    c1_gpu_ms = host_c1 = None
+    if not a.no_cpu:
+        P1, q1, cos1, sin1 = build_c1(torch, dev)
+        for _ in range(20):
+            kh.decode(P1, q1, cos1, sin1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(200):
+            kh.decode(P1, q1, cos1, sin1)
+        torch.cuda.synchronize()
+        c1_gpu_ms = (time.perf_counter() - t0) * 1e3 / 200
+        host_c1 = (SimpleNamespace(qpool=C(P1.qpool), boff=C(P1.boff), epool=C(P1.epool), eoff=C(P1.eoff),
+                                   ebs=P1.ebs, e_hs=P1.e_hs, e_ts=P1.e_ts, e_v=P1.e_v, sk=None, sv=None, skoff=None,
+                                   svoff=None, N=C(P1.N), NQ=C(P1.NQ), nqmax=P1.nqmax, win=P1.win),
+                   C(q1), C(cos1), C(sin1))
+        del P1, q1, cos1, sin1
 
     # ---- the other BASELINE.json configs with a GPU workload: C2 (flush alone), C4 (6-layer decode step), C5 (engine loop)
     del layers, structs
@@ -508,11 +580,20 @@ def main():
                "sample": f"pure-torch restatement of torch_decode.decode (oracle/torch_port.py) on rows 0..{rows - 1} "
                          f"of the 64 x 32768 layer, {cores} torch threads: {dt:.2f} s, scaled by 64/{rows}",
                "c_oracle_ms_per_layer": round(dt_c * 1e3 * B / rows, 1), "c_oracle_threads": cores_c}
+        c1_ms = cpu_baseline_c1(torch, host_c1, cores)
+        cpu["c1"] = {"workload": "C1: one quantized layer, 4 seqs x 1024 tokens (3 sub-blocks + 256 exact tokens per "
+                                 "seq), PagedStore default geometry, N(0,1) q/K/V",
+                     "cpu_ms_per_call": round(c1_ms, 3), "iters": C1_ITERS, "cores": cores,
+                     "gpu_ms_per_call": round(c1_gpu_ms, 4),
+                     "sample": f"oracle/torch_port.py decode of all 4 rows, {C1_ITERS} timed calls after one warm-up"}
     res = {
         "metric": "800h decode ms/layer @64x32K",
         "value": round(ms_step, 5), "unit": "ms", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8 codes / fp16 MFMA / fp32 accumulate", "data": "synthetic",
+        "dtype": "u8 codes / bf16 QK + fp16 PV MFMA / fp32 accumulate", "data": "synthetic",
+        "c3_warmup": {"layer_steps": warm_layer[0], "layer_ms": warm_layer[1], "kernel_launches": warm_kernel[0],
+                      "kernel_ms": warm_kernel[1], "rule": f"max(--warmup, {C3_WARM_CALLS}) calls and >= "
+                                                          f"{C3_WARM_MS:.0f} ms per timed C3 section"},
         "config": {"workload": "C3: one layer paged decode, 64 seqs x 32768 tokens, 16 q / 4 kv heads x 128, "
                                "NQ=127 sub-blocks + 256 exact tokens per seq, permuted page tables, 2 rotating copies",
                    "global_batch": B, "seq_len": N_CTX, "parallelism": "none (1 GPU)"},

@@ -185,12 +185,15 @@ int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq,
                             int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream);
 
 /* All per-step tables of the quant KV group in one launch: decode_tables' NQ / boff plus, where non-NULL,
- * NP[r] = max(N[r] - nnew - 128, 0) / 256 (sub-blocks flushed before the step's nnew tokens: the flush range is
- * [NP, NQ), vllm_attn.py:297-317), qbt64 = qbt as int64 (R, qbt_stride) for kv800_hip_flush, and
- * aux[r] = qbt[r, 0] * aux_scale + aux_add (the sink aux area of each row's first quant page, vllm_attn.py:276-291). */
+ * NP[r] = max(N[r] - m_r - 128, 0) / 256 with m_r = nnew_rows[r] if nnew_rows is non-NULL, else nnew (the sub-blocks
+ * flushed before the step's m_r tokens of row r, i.e. nq(seq_len - query_len): the flush range is [NP, NQ),
+ * vllm_attn.py:270-277, 297-317; a mixed step's decode rows have m_r = 1, its extend rows their chunk length),
+ * qbt64 = qbt as int64 (R, qbt_stride) for kv800_hip_flush, and aux[r] = qbt[r, 0] * aux_scale + aux_add (the sink
+ * aux area of each row's first quant page, vllm_attn.py:276-291). */
 int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
-                          int64_t R, int64_t nqmax, int64_t nnew, int64_t* boff, int32_t* NQ, int32_t* NP,
-                          int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add, void* stream);
+                          int64_t R, int64_t nqmax, int64_t nnew, const int32_t* nnew_rows, int64_t* boff,
+                          int32_t* NQ, int32_t* NP, int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add,
+                          void* stream);
 
 /* One decode step's metadata of a KV group (every row appends one token): for r < R with lens[r] = n (int64, the
  * length including the new token), pos[r] = n - 1, slot[r] = bt[r, pos / ebs] * ebs + pos % ebs (int64; -1 for n = 0

@@ -43,7 +43,8 @@ write_exact_kernel(uint16_t* __restrict__ ep, int64_t s0, int64_t s1, int64_t s2
 
 __global__ void __launch_bounds__(256)
 step_tables_kernel(const int32_t* __restrict__ qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0,
-                   const int32_t* __restrict__ N, int64_t R, int64_t nqmax, int64_t nnew, int64_t* __restrict__ boff,
+                   const int32_t* __restrict__ N, int64_t R, int64_t nqmax, int64_t nnew,
+                   const int32_t* __restrict__ nnew_rows, int64_t* __restrict__ boff,
                    int32_t* __restrict__ NQ, int32_t* __restrict__ NP, int64_t* __restrict__ qbt64,
                    int64_t* __restrict__ aux, int64_t aux_scale, int64_t aux_add) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -52,7 +53,7 @@ step_tables_kernel(const int32_t* __restrict__ qbt, int64_t qbt_stride, int64_t 
   const int64_t r = i / w, j = i % w;
   if (j == 0) {
     NQ[r] = max(N[r] - LAG, 0) / BLK;
-    if (NP) NP[r] = max(N[r] - (int)nnew - LAG, 0) / BLK;
+    if (NP) NP[r] = max(N[r] - (nnew_rows ? max(nnew_rows[r], 0) : (int)nnew) - LAG, 0) / BLK;
     if (aux) aux[r] = (int64_t)qbt[r * qbt_stride] * aux_scale + aux_add;
   }
   if (j < nqmax) {
@@ -113,8 +114,9 @@ int kv800_hip_write_exact(uint16_t* epool, int64_t s0, int64_t s1, int64_t s2, i
 }
 
 int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
-                          int64_t R, int64_t nqmax, int64_t nnew, int64_t* boff, int32_t* NQ, int32_t* NP,
-                          int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add, void* stream) {
+                          int64_t R, int64_t nqmax, int64_t nnew, const int32_t* nnew_rows, int64_t* boff,
+                          int32_t* NQ, int32_t* NP, int64_t* qbt64, int64_t* aux, int64_t aux_scale, int64_t aux_add,
+                          void* stream) {
   KV800_REQUIRE(R >= 0 && nqmax >= 0 && nnew >= 0, "step_tables: R, nqmax and nnew must be >= 0");
   if (R == 0) return KV800_OK;
   KV800_REQUIRE(N && NQ && (!nqmax || boff) && ((!nqmax && !qbt64 && !aux) || (qbt && qbt_stride > 0)),
@@ -127,14 +129,15 @@ int kv800_hip_step_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, i
   const int64_t n = R * w;
   KV800_REQUIRE(n <= 0x7FFFFFFFLL * 256, "step_tables: table too large");
   hipLaunchKernelGGL(step_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, qbt,
-                     qbt_stride, bsq, qs0, N, R, nqmax, nnew, boff, NQ, NP, qbt64, aux, aux_scale, aux_add);
+                     qbt_stride, bsq, qs0, N, R, nqmax, nnew, nnew_rows, boff, NQ, NP, qbt64, aux, aux_scale,
+                     aux_add);
   return check_launch("step_tables");
 }
 
 int kv800_hip_decode_tables(const int32_t* qbt, int64_t qbt_stride, int64_t bsq, int64_t qs0, const int32_t* N,
                             int64_t R, int64_t nqmax, int64_t* boff, int32_t* NQ, void* stream) {
-  return kv800_hip_step_tables(qbt, qbt_stride, bsq, qs0, N, R, nqmax, 0, boff, NQ, nullptr, nullptr, nullptr, 0, 0,
-                               stream);
+  return kv800_hip_step_tables(qbt, qbt_stride, bsq, qs0, N, R, nqmax, 0, nullptr, boff, NQ, nullptr, nullptr, nullptr,
+                               0, 0, stream);
 }
 
 int kv800_hip_page_offsets(const int32_t* bt, int64_t bt_stride, int64_t R, int64_t npages, int64_t scale, int64_t add,

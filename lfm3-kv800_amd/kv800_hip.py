@@ -61,8 +61,8 @@ SIGNATURES = {
     "kv800_hip_write_exact": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP, _VP,
                                      _VP]),
     "kv800_hip_decode_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _VP, _VP, _VP]),
-    "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
-                                     _VP]),
+    "kv800_hip_step_tables": (_I32, [_VP, _I64, _I64, _I64, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _I64,
+                                     _I64, _VP]),
     "kv800_hip_page_offsets": (_I32, [_VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP]),
     "kv800_hip_step_meta": (_I32, [_VP, _I64, _I64, _VP, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
@@ -226,11 +226,18 @@ def decode_tables(qbt, bsq, qs0, N, nqmax):
 
 def step_tables(qbt, bsq, qs0, N, nqmax, nnew=1, aux_scale=None, aux_add=0):
     """All per-step tables of the quant KV group in one launch (kv800_hip_step_tables): (boff, NQ, NP, qbt64, aux) with
-    NP = sub-blocks flushed before the step's nnew tokens, qbt64 = qbt as int64 and, if aux_scale is given,
+    NP = sub-blocks flushed before the step's new tokens (nnew: an int for every row, or an (R,) int32 device tensor of
+    per-row counts, a mixed step's query lengths), qbt64 = qbt as int64 and, if aux_scale is given,
     aux = qbt[:, 0] * aux_scale + aux_add (else None)."""
     L = ops()
     dev = N.device
     _need(qbt, "qbt", torch.int32, dev); _need(N, "N", torch.int32, dev)
+    rows = None
+    if torch.is_tensor(nnew):
+        _need(nnew, "nnew", torch.int32, dev)
+        if nnew.shape != (N.shape[0],):
+            raise ValueError("per-row nnew must be (R,)")
+        rows, nnew = nnew.contiguous(), 0
     if qbt.stride(-1) != 1:
         raise ValueError("qbt rows must be contiguous")
     R = N.shape[0]
@@ -240,7 +247,8 @@ def step_tables(qbt, bsq, qs0, N, nqmax, nnew=1, aux_scale=None, aux_add=0):
     qbt64 = torch.empty(R, qbt.shape[1], dtype=torch.int64, device=dev)
     aux = torch.empty(R, dtype=torch.int64, device=dev) if aux_scale is not None else None
     _check(L.kv800_hip_step_tables(_ptr(qbt), qbt.stride(0), int(bsq), int(qs0), _ptr(N.contiguous()), R, int(nqmax),
-                                   int(nnew), _ptr(boff), _ptr(NQ), _ptr(NP), _ptr(qbt64), _ptr(aux),
+                                   int(nnew), _ptr(rows) if rows is not None else None, _ptr(boff), _ptr(NQ),
+                                   _ptr(NP), _ptr(qbt64), _ptr(aux),
                                    int(aux_scale or 0), int(aux_add), _stream(dev)))
     return boff, NQ, NP, qbt64, aux
 

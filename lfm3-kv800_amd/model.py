@@ -161,11 +161,14 @@ class Lfm3Decoder:
 class PagedAttention800:
     """The model's 11 attention layers on libkv800_hip.so with vLLM's page geometry: one quant KV group (1280-token
     pages of 262,144 B) for layers 6, 10, 14, 22; exact KV groups A (2, 10, 18) and B (6, 14, 22) of ebs-token pages
-    holding each row's last positions (window 640); sliding KV groups C (4, 12, 20) and D (8, 16) (window 256). Pages
-    are given to rows through shuffled block tables; only the positions a row can still read get a page of their own,
-    the rest of its logical pages point at a shared spare page that is never read.
+    holding each row's last positions; sliding KV groups C (4, 12, 20) and D (8, 16) (window 256). Each row of an exact
+    or sliding group owns a ring of `ring` shuffled physical pages and logical page p maps to its (p % ring)-th one
+    (the pages a sliding-window KV group recycles): the ring holds a prompt chunk of FILL tokens plus the 384 exact
+    positions before it, and the decode steps' windows.
 
     lens0: the rows' history lengths; steps: decode steps to provide for."""
+
+    FILL = 2048   # prompt tokens per row per fill step (the reference's prefill chunk, vllm_attn.py:196)
 
     def __init__(self, lens0, steps, device, ebs=128, seed=0):
         self.dev, self.ebs = device, ebs
@@ -176,27 +179,23 @@ class PagedAttention800:
         rng = torch.Generator().manual_seed(seed)
         lp = nmax // ebs + 1                                                   # logical exact pages per row
 
-        def table(first_pos):
-            """block table (R, lp) int32 with unique shuffled pages for logical pages >= first_pos // ebs, page 0 spare."""
-            need = [lp - int(f) // ebs for f in first_pos]
-            perm = (torch.randperm(sum(need), generator=rng) + 1).tolist()
-            bt = torch.zeros(R, lp, dtype=torch.int32)
-            c = 0
-            for r in range(R):
-                f = int(first_pos[r]) // ebs
-                bt[r, f:] = torch.tensor(perm[c:c + need[r]], dtype=torch.int32)
-                c += need[r]
-            return bt.to(device), sum(need) + 1
+        # a fill step writes FILL positions and flushes sub-blocks starting up to 383 positions before them; a decode
+        # step reads the 384 positions before its token: the ring spans both with a page to spare
+        self.ring = ring = max(self.FILL, 384 + steps + 1) // ebs + 5
 
-        nq0 = torch.clamp(self.lens - kv800.LAG, min=0) // kv800.BLK
+        def table():
+            """block table (R, lp) int32: row r's logical page p -> the (p % ring)-th of its ring of shuffled pages."""
+            perm = torch.randperm(R * ring, generator=rng).view(R, ring).to(torch.int32)
+            return perm[:, torch.arange(lp) % ring].contiguous(), R * ring
+
         self.bt, npages = {}, {}
-        for grp in EXACT_GROUPS:
-            # quantized layers read exact positions >= 256 NQ, window layers >= n - 256: both >= n - 384
-            self.bt[grp], npages[grp] = table(torch.minimum(nq0 * kv800.BLK, torch.clamp(self.lens - 256, min=0)))
-        for grp in SLIDE_GROUPS:
-            self.bt[grp], npages[grp] = table(torch.clamp(self.lens - 256, min=0))
+        for grp in (*EXACT_GROUPS, *SLIDE_GROUPS):
+            bt, npages[grp] = table()
+            self.bt[grp] = bt.to(device)
+        self.bt_cpu = {g: t.cpu() for g, t in self.bt.items()}
         qlp = nmax // vc.QBLOCK + 1
-        self.qbt = (torch.randperm(R * qlp, generator=rng).view(R, qlp).to(torch.int32)).to(device)
+        self.qbt_cpu = torch.randperm(R * qlp, generator=rng).view(R, qlp).to(torch.int32)
+        self.qbt = self.qbt_cpu.to(device)
         self.group_of = {l: g for g, ls in {**EXACT_GROUPS, **SLIDE_GROUPS}.items() for l in ls}
         self.layers = {}
         for l in (2, 6, 10, 14, 18, 22):
@@ -211,38 +210,29 @@ class PagedAttention800:
 
     # ---- prompt history
     def fill(self, history):
-        """Write every row's history into the caches. history(l, r, p0, p1) -> (K, V) (p1 - p0, 4, 128) bf16 on the
-        device: pre-RoPE K for full layers, post-RoPE K for sliding layers. Quant layers get sub-blocks j < NQ(n)
-        quantized by the HIP quantizer and the positions from 256 NQ(n) on in exact pages; window layers the positions
-        from n - 256 on and their sinks (positions < 4) in the hosts' aux areas; sliding layers the last 256 positions."""
-        ebs, per_page = self.ebs, vc.QBLOCK // kv800.BLK
-        for l, layer in self.layers.items():
-            bt = self.bt[self.group_of[l]].cpu()
-            quant = l in vc.QUANT_LAYERS
-            # a quant page as its 5 sub-block slots (the aux area after them is not part of this view)
-            qslots = layer.qv[:, :vc.AUX_BYTES].view(-1, per_page, kv800.SUB) if quant else None
-            for r in range(self.R):
-                n = int(self.lens[r])
-                nq = max(0, n - kv800.LAG) // kv800.BLK
-                lo = nq * kv800.BLK if quant else max(0, n - 256)
-                if quant and nq:
-                    K, V = history(l, r, 0, nq * kv800.BLK)
-                    sb = kv800_hip.quantize_blocks(K.view(nq, kv800.BLK, 4, 128), V.view(nq, kv800.BLK, 4, 128))
-                    j = torch.arange(nq, device=self.dev)
-                    qslots[self.qbt[r, j // per_page].long(), j % per_page] = sb
-                if n > lo:
-                    K, V = history(l, r, lo, n)
-                    pos = torch.arange(lo, n)
-                    pages = bt[r, pos // ebs].long().to(self.dev)
-                    slots = (pos % ebs).to(self.dev)
-                    layer.ev[pages, :, slots, :128] = K
-                    layer.ev[pages, :, slots, 128:] = V
-                if l in vc.WINDOW_LAYERS and n > 0:
-                    K, V = history(l, r, 0, min(kv800.NSINK, n))
-                    page0 = int(self.qbt[r, 0])
-                    for src, host in zip((K, V), vc.SINK_HOST[l]):
-                        aux = self.layers[host].qv[page0, vc.AUX_BYTES:].view(torch.bfloat16)
-                        aux[:src.numel()] = src.reshape(-1)
+        """Write every row's history into the caches through the layers' step path (vllm_cache write_step: exact rows,
+        sinks of window layers in the hosts' aux areas, flush of every sub-block that becomes eligible, from the
+        layer's own exact group), in prefill steps of up to FILL positions per row, as vLLM schedules prompt chunks:
+        step c carries positions [c FILL, min(n, (c + 1) FILL)) of every row still short of its length n. Prompt
+        attention is not computed (no queries exist for a synthetic history). history(l, r, p0, p1) -> (K, V)
+        (p1 - p0, 4, 128) bf16 on the device: pre-RoPE K for full layers, post-RoPE K for sliding layers."""
+        lens = self.lens
+        for c0 in range(0, int(lens.max()) if self.R else 0, self.FILL):
+            rows = torch.nonzero(lens > c0).flatten()
+            sl = torch.clamp(lens[rows], max=c0 + self.FILL)
+            ql = sl - c0
+            me = {g: vc.mixed_step_meta(self.bt_cpu[g][rows], sl, ql, self.ebs, self.dev, num_decodes=0)
+                  for g in self.bt}
+            mq = vc.mixed_step_meta(self.qbt_cpu[rows], sl, ql, vc.QBLOCK, self.dev, num_decodes=0)
+            for l, layer in self.layers.items():
+                parts = [history(l, int(r), c0, int(n)) for r, n in zip(rows.tolist(), sl.tolist())]
+                K = torch.cat([p[0] for p in parts])
+                V = torch.cat([p[1] for p in parts])
+                if isinstance(layer, vc.KV800SlideLayer):
+                    layer.write_step(K, V, me[self.group_of[l]])
+                else:
+                    layer.write_step(K, V, me[self.group_of[l]], mq, hosts=self.layers)
+                del K, V, parts
 
     # ---- decode steps
     def freeze(self, steps):

@@ -1,7 +1,7 @@
-"""Decode step of the 800h attention layers on caches with vLLM's page geometry, without vLLM.
+"""One step of the 800h attention layers on caches with vLLM's page geometry, without vLLM.
 
-Counterpart of the decode path of the reference's vLLM integration (vllm_attn.py:214-350, KV800Attention.forward for
-decode rows), with the same cache layout so that pages written here are the pages vLLM would hold:
+Counterpart of the reference's vLLM integration (vllm_attn.py:214-402, KV800Attention.forward), with the same cache
+layout so that pages written here are the pages vLLM would hold:
 
   quantized layers (6, 10, 14, 22): a quant cache of 1280-token pages, 5 x 51,200-byte sub-blocks padded to 262,144 B
       (vllm_attn.py:36-37, 126-131), block table shared by the four layers (one FullAttention KV group), plus an exact
@@ -9,10 +9,13 @@ decode rows), with the same cache layout so that pages written here are the page
   window layers (2, 18): the exact cache only; their 4 sink tokens live in the 6,144-byte aux area at byte 256,000 of
       the first quant page of the host layers (6, 10) / (14, 22) (vllm_attn.py:3-9, 276-291).
 
-One step of one layer = the step's K / V rows into the exact pages (and sink aux), the flush of the sub-blocks that
-became eligible (n >= 256 j + 384) from this layer's own exact group (the 0.1.1 fix, vllm_attn.py:301), the decode
-tables and the fused decode. Every piece is a launch of libkv800_hip.so on the current stream; the only host values
-are the ones the reference also reads on the host (the rows' sequence lengths, for nqmax and the flush width)."""
+One step of one layer takes a vLLM-shaped batch: decode rows (one token each) first, then extend / prefill rows of
+any chunk length (query_start_loc, seq_lens). It writes the K / V rows of every scheduled token into the exact pages
+(and positions < 4 into the sink aux), flushes the sub-blocks that became eligible (n >= 256 j + 384) in
+[nq(seq_len - query_len), nq(seq_len)) per row from this layer's own exact group (the 0.1.1 fix, vllm_attn.py:301),
+decodes the decode rows with the fused decode and attends the extend rows over their compressed history
+(vllm_attn.py:351-402). Every piece is a launch of libkv800_hip.so on the current stream; the only host values are
+the ones the reference also reads on the host (the rows' sequence and query lengths)."""
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -30,16 +33,27 @@ AUX_BYTES = (QBLOCK // kv800.BLK) * kv800.SUB  # 256,000: start of the aux area 
 
 @dataclass
 class StepMeta:
-    """Per-step metadata of one KV-cache group (the KV800Meta fields the decode path reads, vllm_attn.py:64-75).
-    block_table (R, blocks) int32; slot_mapping (R,) int64 slot of the step's token (-1: none); seq_lens (R,) int32
-    including the step's token; seq_lens_cpu the same on the host; positions (R,) int64. `cache` holds values shared
-    by the layers of the group within the step."""
+    """Per-step metadata of one KV-cache group (the KV800Meta fields the attention reads, vllm_attn.py:64-75).
+    block_table (R, blocks) int32; slot_mapping (T,) int64 slot of each scheduled token (-1: none); seq_lens (R,)
+    int32 including the step's tokens; seq_lens_cpu the same on the host; positions (T,) int64. `cache` holds values
+    shared by the layers of the group within the step.
+    Mixed steps (mixed_step_meta) also carry query_start_loc_cpu (R + 1,) host int64, num_decodes (rows
+    [0, num_decodes) have one token each, the rest are extend rows), query_lens (R,) int32 and req_of_tok (T,) int64
+    (each token's row) on the device; a decode step (step_meta) leaves them None: one token per row, T = R."""
     block_table: torch.Tensor
     slot_mapping: torch.Tensor
     seq_lens: torch.Tensor
     seq_lens_cpu: torch.Tensor
     positions: torch.Tensor
     cache: dict = field(default_factory=dict)
+    query_start_loc_cpu: torch.Tensor = None
+    num_decodes: int = None
+    query_lens: torch.Tensor = None
+    req_of_tok: torch.Tensor = None
+
+    @property
+    def mixed(self):
+        return self.query_start_loc_cpu is not None
 
 
 def step_lens(seq_lens_cpu, device):
@@ -65,6 +79,49 @@ def step_meta(block_table, seq_lens_cpu, ebs, device, seq_lens_dev=None):
     return StepMeta(bt, slot, dsl.to(torch.int32), sl, pos)
 
 
+def mixed_step_meta(block_table, seq_lens_cpu, query_lens_cpu, ebs, device, num_decodes=None):
+    """StepMeta of a vLLM-shaped step of one KV group: row r schedules query_lens[r] >= 1 tokens at positions
+    seq_lens[r] - query_lens[r] .. seq_lens[r] - 1 (decode rows first, then extend rows, as vLLM orders a batch,
+    vllm_attn.py:244-277). block_table (R, blocks) on the host; num_decodes defaults to the leading rows with one
+    token. Slots and positions are formed on the host, as vLLM's scheduler forms slot_mapping."""
+    bt = torch.as_tensor(block_table).to(torch.int32).cpu()
+    sl = torch.as_tensor(seq_lens_cpu).to(torch.int64).cpu()
+    ql = torch.as_tensor(query_lens_cpu).to(torch.int64).cpu()
+    R = sl.shape[0]
+    if bt.dim() != 2 or bt.shape[0] != R or ql.shape != (R,):
+        raise ValueError("block_table (R, blocks), seq_lens (R,) and query_lens (R,) must agree")
+    if bool((ql < 1).any()) or bool((ql > sl).any()):
+        raise ValueError("every row needs 1 <= query_len <= seq_len")
+    qsl = torch.zeros(R + 1, dtype=torch.int64)
+    qsl[1:] = torch.cumsum(ql, 0)
+    T = int(qsl[-1])
+    req = torch.repeat_interleave(torch.arange(R), ql)
+    pos = torch.arange(T) - qsl[:-1][req] + (sl - ql)[req]
+    if bool((pos // ebs >= bt.shape[1]).any()):
+        raise ValueError("the block table does not cover the step's positions")
+    slot = bt[req, pos // ebs].to(torch.int64) * ebs + pos % ebs
+    if num_decodes is None:
+        nd = 0
+        while nd < R and int(ql[nd]) == 1:
+            nd += 1
+    else:
+        nd = int(num_decodes)
+        if not 0 <= nd <= R or bool((ql[:nd] != 1).any()):
+            raise ValueError("decode rows must come first, one token each")
+    dev = torch.device(device)
+    up = (lambda t: t.pin_memory().to(dev, non_blocking=True)) if dev.type == "cuda" else (lambda t: t.to(dev))
+    return StepMeta(up(bt), up(slot), up(sl.to(torch.int32)), sl, up(pos), query_start_loc_cpu=qsl, num_decodes=nd,
+                    query_lens=up(ql.to(torch.int32)), req_of_tok=up(req))
+
+
+def _max_flush(m):
+    """Most sub-blocks any row of the step becomes eligible for (host values): nq(seq_len) - nq(seq_len - query_len)."""
+    sl = m.seq_lens_cpu.to(torch.int64)
+    ql = (m.query_start_loc_cpu[1:] - m.query_start_loc_cpu[:-1]) if m.mixed else torch.ones_like(sl)
+    nq = lambda n: torch.clamp(n - kv800.LAG, min=0) // kv800.BLK
+    return int((nq(sl) - nq(sl - ql)).max()) if sl.numel() else 0
+
+
 class KV800DecodeLayer:
     """One LFM3 full-attention layer's decode step over its 800h caches. exact: (pages, 4, ebs, 256) bf16 [K | V];
     quant: (qpages, 262144) uint8 for quantized layers, None for window layers."""
@@ -84,10 +141,13 @@ class KV800DecodeLayer:
         self._zeros = None   # NQ = 0 rows of the window decode
 
     def forward(self, q, k, v, mx: StepMeta, mq: StepMeta = None, hosts=None, cos_t=None, sin_t=None, max_new=1):
-        """q (R, 16, 128) post-RoPE, k (R, 4, 128) pre-RoPE, v (R, 4, 128), all bf16, one decode token per row.
+        """q (T, 16, 128) post-RoPE, k (T, 4, 128) pre-RoPE, v (T, 4, 128), all bf16, one row per scheduled token.
         mx: this layer's exact-group metadata; mq: the quant group's (quantized layers, and the sink hosts of window
         layers); hosts: {layer: KV800DecodeLayer} holding the sink hosts' quant caches (window layers); cos_t / sin_t
-        (P, 32) bf16 RoPE tables; max_new: most sub-blocks any row can become eligible for in this step (1 for decode)."""
+        (P, 32) bf16 RoPE tables; max_new: most sub-blocks any row can become eligible for in a decode step (1).
+        A mixed step (mx.mixed) runs the decode rows and the extend rows of the batch (vllm_attn.py:244-402)."""
+        if mx.mixed:
+            return self._forward_mixed(q, k, v, mx, mq, hosts, cos_t, sin_t)
         ev, ebs = self.ev, self.ebs
         s0, s1, s2 = ev.stride(0), ev.stride(1), ev.stride(2)
         R = q.shape[0]
@@ -118,6 +178,72 @@ class KV800DecodeLayer:
         P = kv800.Paged(qpool=self.qv, boff=boff, epool=ev, eoff=eoff, ebs=ebs, e_hs=s1, e_ts=s2, e_v=128, sk=None,
                         sv=None, skoff=None, svoff=None, N=N, NQ=NQ, nqmax=nqmax, win=0)
         return kv800_hip.decode(P, q, cos_t, sin_t)
+
+    def _sinks(self, hosts):
+        """The sink buffers of a window layer: the quant caches of its two host layers as bf16."""
+        kh, vh = (hosts[h] for h in SINK_HOST[self.l])
+        return kh.qv.view(torch.bfloat16), vh.qv.view(torch.bfloat16)
+
+    def write_step(self, k, v, mx: StepMeta, mq: StepMeta, hosts=None):
+        """The cache half of a step (vllm_attn.py:255-317): the K / V rows of every scheduled token (k, v (T, 4, 128)
+        bf16, pre-RoPE K) into this layer's exact pages; window layers also put positions < 4 into the sink aux of
+        their hosts; quantized layers then flush, from their own exact group, the sub-blocks [NP, NQ) of every row
+        (NP = nq(seq_len - query_len)), after this step's rows are in the pages (an extend row's new sub-blocks are
+        made of them)."""
+        ev = self.ev
+        boff, NQ, NP, qbt64, aux, nqmax = _step_tables(mq)
+        if self.win:
+            skb, svb = self._sinks(hosts)
+            at = aux.index_select(0, mx.req_of_tok) if mx.mixed else aux
+            kv800_hip.write_exact(ev, mx.slot_mapping, k, v, pos=mx.positions, sk=skb, sv=svb, skoff=at, svoff=at)
+            return
+        kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        mnew = _max_flush(mq)
+        if mnew > 0:
+            kv800_hip.flush(ev, self._eoff(mx), self.ebs, ev.stride(1), ev.stride(2), 128, self.qv, qbt64, QBLOCK, QPAGE,
+                            NP, NQ, mnew, latency=mnew <= 2)
+
+    def _forward_mixed(self, q, k, v, mx, mq, hosts, cos_t, sin_t):
+        """A mixed step: write_step, then the decode rows through the fused decode and the extend rows through the
+        prefill over compressed history (quantized layers: the row's nq(prev) sub-blocks dequantized, the exact rows
+        from 256 nq(prev) on, then its new rows; window layers: sinks, the last 255 exact rows, the new rows)."""
+        ev, ebs = self.ev, self.ebs
+        s1, s2 = ev.stride(1), ev.stride(2)
+        qsl = mx.query_start_loc_cpu
+        R, T, nd = qsl.shape[0] - 1, int(qsl[-1]), mx.num_decodes
+        self.write_step(k, v, mx, mq, hosts)
+        eoff = self._eoff(mx)
+        boff, NQ, NP, qbt64, aux, nqmax = _step_tables(mq)
+        out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device=q.device)
+        prev = (mx.seq_lens_cpu - (qsl[1:] - qsl[:-1])).tolist()
+        t0 = int(qsl[nd])
+        eq = (qsl[nd:] - t0).tolist()
+        if self.win:
+            skb, svb = self._sinks(hosts)
+            if self._zeros is None or self._zeros.shape[0] < R:
+                self._zeros = torch.zeros(max(R, 64), dtype=torch.int32, device=ev.device)
+            if nd:
+                P = kv800.Paged(qpool=ev, boff=eoff[:nd], epool=ev, eoff=eoff[:nd], ebs=ebs, e_hs=s1, e_ts=s2, e_v=128,
+                                sk=skb, sv=svb, skoff=aux[:nd], svoff=aux[:nd], N=mx.seq_lens[:nd],
+                                NQ=self._zeros[:nd], nqmax=0, win=kv800.WIN)
+                out[:nd] = kv800_hip.decode(P, q[:nd], cos_t, sin_t)
+            if R > nd:
+                P = kv800.Paged(qpool=None, boff=None, epool=ev, eoff=eoff[nd:], ebs=ebs, e_hs=s1, e_ts=s2, e_v=128,
+                                sk=skb, sv=svb, skoff=aux[nd:], svoff=aux[nd:], N=mx.seq_lens[nd:],
+                                NQ=self._zeros[:R - nd], nqmax=0, win=kv800.WIN)
+                out[t0:] = prefill_window_rows(P, q[t0:T], k[t0:T], v[t0:T], eq, prev[nd:], cos_t, sin_t)
+            return out
+        if nd:
+            P = kv800.Paged(qpool=self.qv, boff=boff[:nd], epool=ev, eoff=eoff[:nd], ebs=ebs, e_hs=s1, e_ts=s2, e_v=128,
+                            sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens[:nd], NQ=NQ[:nd], nqmax=nqmax,
+                            win=0)
+            out[:nd] = kv800_hip.decode(P, q[:nd], cos_t, sin_t)
+        if R > nd:
+            P = kv800.Paged(qpool=self.qv, boff=boff[nd:], epool=ev, eoff=eoff[nd:], ebs=ebs, e_hs=s1, e_ts=s2, e_v=128,
+                            sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens[nd:], NQ=NP[nd:], nqmax=nqmax,
+                            win=0)
+            out[t0:] = prefill_quant_rows(P, q[t0:T], k[t0:T], v[t0:T], eq, prev[nd:], cos_t, sin_t)
+        return out
 
     def _eoff(self, mx):
         """The exact group's page offsets for this cache's page stride (one launch per group and step)."""
@@ -157,30 +283,53 @@ class KV800SlideLayer:
                            torch.zeros(n, 32, dtype=torch.bfloat16, device=self.ev.device))
         return self._ident
 
+    def write_step(self, k, v, mx: StepMeta):
+        """The K / V rows (post-RoPE K) of every scheduled token into the sliding pages."""
+        kv800_hip.write_exact(self.ev, mx.slot_mapping, k, v)
+
     def forward(self, q, k, v, mx: StepMeta):
-        """q (R, 16, 128) post-RoPE, k (R, 4, 128) POST-RoPE, v (R, 4, 128), bf16, one decode token per row;
-        mx: the layer's sliding-group metadata."""
+        """q (T, 16, 128) post-RoPE, k (T, 4, 128) POST-RoPE, v (T, 4, 128), bf16, one row per scheduled token;
+        mx: the layer's sliding-group metadata. A mixed step's extend rows attend their last 255 positions and their
+        new rows (vllm_attn.py:351-402 with slide=True)."""
         ev, ebs = self.ev, self.ebs
-        R = q.shape[0]
+        R = mx.seq_lens.shape[0]
         key = ("eoff", ev.stride(0))
         if key not in mx.cache:
             mx.cache[key] = kv800_hip.page_offsets(mx.block_table, ev.stride(0))
         eoff = mx.cache[key]
-        kv800_hip.write_exact(ev, mx.slot_mapping, k, v)
+        self.write_step(k, v, mx)
         if self._zeros is None or self._zeros.shape[0] < R:
             self._zeros = torch.zeros(max(R, 64), dtype=torch.int32, device=ev.device)
+        nd = mx.num_decodes if mx.mixed else R
         cos1, sin0 = self.identity_tables(int(mx.seq_lens_cpu.max()) + 1)
-        P = kv800.Paged(qpool=ev, boff=eoff, epool=ev, eoff=eoff, ebs=ebs, e_hs=ev.stride(1), e_ts=ev.stride(2),
-                        e_v=128, sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens, NQ=self._zeros[:R], nqmax=0,
-                        win=kv800.WIN)
-        return kv800_hip.decode(P, q, cos1, sin0)
+        out = torch.empty(q.shape[0], 16, 128, dtype=torch.bfloat16, device=q.device) if mx.mixed else None
+        if nd:
+            P = kv800.Paged(qpool=ev, boff=eoff[:nd], epool=ev, eoff=eoff[:nd], ebs=ebs, e_hs=ev.stride(1),
+                            e_ts=ev.stride(2), e_v=128, sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens[:nd],
+                            NQ=self._zeros[:nd], nqmax=0, win=kv800.WIN)
+            o = kv800_hip.decode(P, q[:nd], cos1, sin0)
+            if not mx.mixed:
+                return o
+            out[:nd] = o
+        if R > nd:
+            qsl = mx.query_start_loc_cpu
+            t0, T = int(qsl[nd]), int(qsl[-1])
+            prev = (mx.seq_lens_cpu - (qsl[1:] - qsl[:-1])).tolist()
+            P = kv800.Paged(qpool=None, boff=None, epool=ev, eoff=eoff[nd:], ebs=ebs, e_hs=ev.stride(1),
+                            e_ts=ev.stride(2), e_v=128, sk=None, sv=None, skoff=None, svoff=None, N=mx.seq_lens[nd:],
+                            NQ=self._zeros[:R - nd], nqmax=0, win=kv800.WIN)
+            out[t0:] = prefill_window_rows(P, q[t0:T], k[t0:T], v[t0:T], (qsl[nd:] - t0).tolist(), prev[nd:], None,
+                                           None)
+        return out
 
 
 def _step_tables(mq):
-    """(boff, NQ, NP, qbt64, aux, nqmax) of the quant group for this step, built once (kv800_hip_step_tables)."""
+    """(boff, NQ, NP, qbt64, aux, nqmax) of the quant group for this step, built once (kv800_hip_step_tables); NP
+    counts each row's sub-blocks before its query_len new tokens (one for a decode step)."""
     if ("step",) not in mq.cache:
         nqmax = int(torch.clamp(mq.seq_lens_cpu.to(torch.int64) - kv800.LAG, min=0).max()) // kv800.BLK
-        mq.cache[("step",)] = kv800_hip.step_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax, nnew=1,
+        nnew = mq.query_lens if mq.mixed else 1
+        mq.cache[("step",)] = kv800_hip.step_tables(mq.block_table, QBLOCK, QPAGE, mq.seq_lens, nqmax, nnew=nnew,
                                                     aux_scale=QPAGE // 2, aux_add=AUX_BYTES // 2) + (nqmax,)
     return mq.cache[("step",)]
 
@@ -194,9 +343,10 @@ def launch_flushes(layers, metas, mq, max_new=1):
     flush reads tokens written in earlier steps only (sub-block j flushes at n >= 256 j + 384, so it ends 128 tokens
     before the step's token), and the side stream first waits for everything queued so far on the current stream.
     layers: the KV800DecodeLayer objects of the step; metas: {layer index: its exact group's StepMeta}; mq: the quant
-    group's StepMeta. Call once per step, before the step's first attention layer."""
+    group's StepMeta. Call once per step, before the step's first attention layer. A mixed step starts none (its
+    extend rows flush sub-blocks made of this step's own tokens): each layer's forward flushes after its writes."""
     quant = [l for l in layers if not l.win]
-    if not quant:
+    if not quant or mq.mixed:
         return
     dev = quant[0].ev.device
     main = torch.cuda.current_stream(dev)

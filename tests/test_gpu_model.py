@@ -237,6 +237,58 @@ def _decode_setup(lens0, steps):
     return model, attn
 
 
+def test_model_full_size_c5(hip, oracle):
+    """config C5 at full size: 256 rows with prompt lengths U[1K, 32K] (the bench's seed), the
+    prompt caches written through the attention layers' step path in 2048-token prefill chunks
+    (PagedAttention800.fill -> vllm_cache write_step: exact pages, sinks, flushes), then 3 greedy steps of the
+    LFM3-shaped model: every step's logits finite and tokens in range; sub-blocks the fill flushed (first, middle and
+    last of two rows, quantized layers 6 and 22) equal the oracle quantizer's bytes of the rows' history."""
+    from lfm3_kv800_amd import model as M
+    from lfm3_kv800_amd import model_ops as mo
+    cfg = M.Lfm3Config()
+    R, steps = 256, 3
+    lens0 = np.random.RandomState(51).randint(1024, 32768 + 1, size=R).astype(np.int64)
+    g = torch.Generator(device=DEV).manual_seed(51)
+    POOL = 1 << 16
+    pools = {}
+
+    def history(l, r, p0, p1):
+        if l not in pools:
+            pools[l] = tuple(torch.randn(POOL, 4, 128, generator=g, device=DEV).to(torch.bfloat16) for _ in range(2))
+        o = (r * 7919 + p0 * 13) % (POOL - (p1 - p0) + 1)
+        return pools[l][0][o:o + p1 - p0], pools[l][1][o:o + p1 - p0]
+
+    say("full-size C5: fill", R, "rows,", int(lens0.sum()), "prompt tokens")
+    attn = M.PagedAttention800(lens0.tolist(), steps + 1, DEV, seed=51)
+    attn.fill(history)
+    torch.cuda.synchronize()
+    F = attn.FILL
+    for l in (6, 22):
+        qv = attn.layers[l].qv
+        for r in (int(np.argmin(lens0)), int(np.argmax(lens0))):
+            n = int(lens0[r])
+            m = max(0, n - 128) // 256
+            for j in sorted({0, m // 2, m - 1}):
+                c0 = (256 * j) // F * F
+                K, V = history(l, r, c0, min(n, c0 + F))
+                i0 = 256 * j - c0
+                want = oracle.quantize_blocks(bits_of(K[i0:i0 + 256])[None], bits_of(V[i0:i0 + 256])[None])[0]
+                pg, off = int(attn.qbt_cpu[r, 256 * j // 1280]), (256 * j) % 1280 // 256 * 51200
+                assert np.array_equal(qv[pg, off:off + 51200].cpu().numpy(), want), (l, r, j)
+    say("full-size C5: model and", steps, "greedy steps")
+    model = M.Lfm3Decoder(cfg, attn, R, DEV, seed=51)
+    model.randomize_conv_states(51)
+    tok = torch.randint(0, cfg.vocab, (R,), generator=g, device=DEV)
+    for s in range(steps):
+        logits = model.step(tok, attn.begin_step(), fp32=False)
+        tok = mo.argmax(logits)
+        torch.cuda.synchronize()
+        say(f"step {s}: logits finite {bool(torch.isfinite(logits.float()).all())}")
+        assert bool(torch.isfinite(logits.float()).all()) and bool(((tok >= 0) & (tok < cfg.vocab)).all()), s
+    del model, attn, pools
+    torch.cuda.empty_cache()
+
+
 def test_decode_graph_replays_match_eager(hip):
     """DecodeGraph (the first step eager, the others replays of one recorded step, lengths advanced on the device and
     the step metadata's host values taken at the last step's lengths) against the same steps launched one kernel at a

@@ -205,14 +205,16 @@ QUANT_NS = (50, 383, 384, 700, 1500, 5000)
 WINDOW_NS = (3, 10, 200, 259, 260, 1500)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
 @pytest.mark.parametrize("win,n", [(0, n) for n in QUANT_NS] + [(256, n) for n in WINDOW_NS])
-def test_decode_reference_cases(hip, oracle, win, n):
-    """tests/test_parity.py's 12 cases through the product PagedStore (HIP flush) and kv800.decode."""
+def test_decode_reference_cases(hip, oracle, win, n, seed):
+    """tests/test_parity.py's 12 cases (its run_case takes a seed, test_parity.py:80) at seeds 0, 1 and 2, through the
+    product PagedStore (HIP flush) and kv800.decode."""
     import lfm3_kv800_amd.kv800 as kv
     import test_oracle as T
-    q, K, V = T.parity_inputs(oracle, n, win)
+    q, K, V = T.parity_inputs(oracle, n, win, seed=seed)
     cos, sin = oracle.rope_tables(8192)
-    say("decode case", win, n)
+    say("decode case", win, n, "seed", seed)
     st = kv.PagedStore(2, n + 8, DEV, window=win)
     pre = max(1, n - 5)
     st.append(to_dev_bf16(K[:, :pre]), to_dev_bf16(V[:, :pre]))
@@ -229,9 +231,9 @@ def test_decode_reference_cases(hip, oracle, win, n):
     ref = oracle.reference_f64(q, K, V, cos, sin, window=win)
     o = oracle.bf16_to_f32(ob).astype(np.float64)
     rel = np.linalg.norm(o - ref) / np.linalg.norm(ref)
-    say(f"win={win} n={n}: rel {rel:.2e} vs the independent check")
+    say(f"win={win} n={n} seed={seed}: rel {rel:.2e} vs the independent check")
     assert rel < 1e-2
-    close(ob, want, f"win={win} n={n} vs oracle")
+    close(ob, want, f"win={win} n={n} seed={seed} vs oracle")
 
 
 @pytest.mark.parametrize("B,n", [(4, 1024), (2, 384), (3, 5000), (1, 9000)])

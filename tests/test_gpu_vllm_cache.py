@@ -188,12 +188,14 @@ def test_step_meta_matches_torch(hip):
 
 
 def test_vllm_decode_step_full_size(hip, oracle):
-    """the shape of config C4 through the vLLM cache path: 398 rows with lengths U[1K, 32K] (rows 0-7 placed so
-    the step flushes a sub-block), a window + sinks layer (2, exact group B) and quantized layers 6 (group A) and 10
-    (group B) whose aux areas host layer 2's sinks. Caches hold N(0,1) bf16 histories written straight into shuffled
-    exact pages; the sub-blocks flushed before the step are quantized from those pages by the HIP quantizer. One step
-    (flushes ahead on the side stream, then each layer's write + decode): every output finite, and sampled rows
-    (shortest, longest, a flushing row, three more) within the decode bar of the oracle on their full histories."""
+    """the shape of config C4 through the vLLM cache path, all six attention layers: 398 rows with
+    lengths U[1K, 32K] (rows 0-7 placed so the step flushes a sub-block), window + sinks layers 2 and 18 (sinks in the
+    aux areas of 6 / 10 and 14 / 22) and quantized layers 6, 10, 14, 22, in two exact KV groups (A: 6, 14, 22; B: 2,
+    10, 18). Each row's history is a slice of a per-layer N(0,1) pool; its last 640 positions sit in a ring of 8
+    shuffled exact pages, its sub-blocks j < nq(n - 1) are quantized from the slice by the HIP quantizer. One step
+    (flushes ahead on the side stream, then each layer's write + decode): every output finite, the flushed sub-blocks
+    of rows 0-7 equal the oracle quantizer's bytes, and sampled rows (shortest, longest, a flushing row, three more)
+    are within the decode bar of the oracle on their full histories."""
     from lfm3_kv800_amd import vllm_cache as vc
     dev = torch.device(DEV)
     R, lo_n, hi_n = 398, 1024, 32768
@@ -203,58 +205,59 @@ def test_vllm_decode_step_full_size(hip, oracle):
     n = L0 + 1
     nq_prev = np.maximum(L0 - 128, 0) // 256
     assert ((np.maximum(n - 128, 0) // 256) > nq_prev).sum() >= 8
-    layers, group = (2, 6, 10), {2: "B", 6: "A", 10: "B"}
+    layers = (2, 6, 10, 14, 18, 22)
+    group = {6: "A", 14: "A", 22: "A", 2: "B", 10: "B", 18: "B"}
     g = torch.Generator(device=dev).manual_seed(41)
-    # exact pages: row r owns ceil(n_r / 128) shuffled pages of group A and of group B
-    need = (n + EBS - 1) // EBS
-    epr = int(need.max())
-    bt = {}
-    for grp in "AB":
-        perm = rng.permutation(int(need.sum()))
-        t = np.zeros((R, epr), np.int32)
-        t[np.arange(epr)[None, :] < need[:, None]] = perm
-        bt[grp] = t
+    POOL, RING = 1 << 16, 8
+    pools = {l: tuple(torch.randn(POOL, 4, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
+             for l in layers}
+    base = torch.from_numpy((np.arange(R) * 7919) % (POOL - hi_n - 2)).to(dev)
+
+    def hist(l, rows, p0, p1):
+        """(len(rows), p1 - p0, 4, 128) K and V of positions [p0, p1) of the rows (p0, p1 scalars)."""
+        idx = base[torch.as_tensor(rows, device=dev)][:, None] + torch.arange(p0, p1, device=dev)
+        return pools[l][0][idx], pools[l][1][idx]
+
+    # exact pages: row r's logical page p is page perm[r, p % RING] of its group
+    lp = (hi_n + 1) // EBS + 2
+    bt = {grp: np.ascontiguousarray(rng.permutation(R * RING).reshape(R, RING)[:, np.arange(lp) % RING], np.int32)
+          for grp in "AB"}
     qneed = (n + QBLOCK - 1) // QBLOCK
     qpr = int(qneed.max())
     qbt = np.zeros((R, qpr), np.int32)
     qbt[np.arange(qpr)[None, :] < qneed[:, None]] = rng.permutation(int(qneed.sum()))
-    say("full size: rows", R, "tokens", int(n.sum()), "exact pages per group", int(need.sum()))
+    say("full size: rows", R, "tokens", int(n.sum()), "layers", layers)
     ev, qv = {}, {}
-    for l in layers:
-        e = torch.empty(int(need.sum()), 4, EBS, 256, dtype=torch.bfloat16, device=dev)
-        for i in range(0, e.shape[0], 4096):
-            e[i:i + 4096] = torch.randn(e[i:i + 4096].shape, generator=g, device=dev).to(torch.bfloat16)
-        ev[l] = e
+    W = 640
+    pos = torch.from_numpy(L0[:, None] - W + np.arange(W)[None, :]).to(dev)         # (R, W) last positions
+    rr = torch.arange(R, device=dev)[:, None].expand(R, W)
     btd = {grp: torch.from_numpy(bt[grp]).to(dev).long() for grp in "AB"}
-
-    def rows_kv(l, rows, p0, p1):
-        """(len(rows), p1 - p0, 4, 128) K and V of positions [p0, p1) from the exact pages."""
-        pos = torch.arange(p0, p1, device=dev)
-        pg = btd[group[l]][torch.as_tensor(rows, device=dev)][:, pos // EBS]
-        blk = ev[l][pg, :, (pos % EBS)[None, :].expand_as(pg)]          # (rows, P, 4, 256)
-        return blk[..., :128], blk[..., 128:]
-
+    for l in layers:
+        e = torch.zeros(R * RING, 4, EBS, 256, dtype=torch.bfloat16, device=dev)
+        idx = base[:, None] + pos
+        pg = btd[group[l]][rr, pos // EBS]
+        e[pg, :, pos % EBS, :128] = pools[l][0][idx]
+        e[pg, :, pos % EBS, 128:] = pools[l][1][idx]
+        ev[l] = e
     # quant pages: every sub-block j < nq_prev[r] from the HIP quantizer
-    pairs = [(r, j) for r in range(R) for j in range(int(nq_prev[r]))]
-    for l in (6, 10):
+    pairs = np.array([(r, j) for r in range(R) for j in range(int(nq_prev[r]))], np.int64)
+    for l in (6, 10, 14, 22):
         q_l = torch.zeros(int(qneed.sum()), QPAGE, dtype=torch.uint8, device=dev)
         slots = q_l[:, :AUX].view(-1, 5, 51200)
         for i in range(0, len(pairs), 2048):
-            part = pairs[i:i + 2048]
-            rr = torch.as_tensor([r for r, _ in part], device=dev)
-            pos = torch.as_tensor([256 * j for _, j in part], device=dev)[:, None] + torch.arange(256, device=dev)
-            pg = btd[group[l]][rr[:, None], pos // EBS]
-            blk = ev[l][pg, :, pos % EBS]                                  # (m, 256, 4, 256)
-            sb = hip.quantize_blocks(blk[..., :128].contiguous(), blk[..., 128:].contiguous())
-            qpage = torch.as_tensor([int(qbt[r, 256 * j // QBLOCK]) for r, j in part], device=dev)
-            qslot = torch.as_tensor([(256 * j) % QBLOCK // 256 for _, j in part], device=dev)
-            slots[qpage, qslot] = sb
+            part = torch.from_numpy(pairs[i:i + 2048]).to(dev)
+            idx = base[part[:, 0]][:, None] + 256 * part[:, 1:2] + torch.arange(256, device=dev)
+            sb = hip.quantize_blocks(pools[l][0][idx], pools[l][1][idx])
+            qpage = torch.from_numpy(qbt).to(dev).long()[part[:, 0], 256 * part[:, 1] // QBLOCK]
+            slots[qpage, (256 * part[:, 1]) % QBLOCK // 256] = sb
         qv[l] = q_l
-    # layer 2's sinks (positions 0-3): K in layer 6's aux, V in layer 10's, at each row's first quant page
-    ks, vs = rows_kv(2, list(range(R)), 0, 4)
-    for host, arr in ((6, ks), (10, vs)):
-        aux = qv[host].view(torch.bfloat16).view(-1, QPAGE // 2)[:, AUX // 2:AUX // 2 + 2048]
-        aux[torch.from_numpy(qbt[:, 0]).to(dev).long()] = arr.reshape(R, 2048)
+    # sinks (positions 0-3) of the window layers: K in the first host's aux, V in the second's
+    qbt0 = torch.from_numpy(qbt[:, 0]).to(dev).long()
+    for wl in (2, 18):
+        ks, vs = hist(wl, list(range(R)), 0, 4)
+        for host, arr in zip(vc.SINK_HOST[wl], (ks, vs)):
+            aux = qv[host].view(torch.bfloat16).view(-1, QPAGE // 2)[:, AUX // 2:AUX // 2 + 2048]
+            aux[qbt0] = arr.reshape(R, 2048)
     torch.cuda.synchronize()
 
     lay = {l: vc.KV800DecodeLayer(l, ev[l], qv.get(l)) for l in layers}
@@ -273,21 +276,38 @@ def test_vllm_decode_step_full_size(hip, oracle):
     for l in layers:
         assert bool(torch.isfinite(outs[l].float()).all()), l
 
+    # the sub-block each of rows 0-7 flushed in this step, against the oracle quantizer
+    for l in (6, 10, 14, 22):
+        qb = qv[l]
+        for r in range(8):
+            j = int(nq_prev[r])
+            K, V = hist(l, [r], 256 * j, 256 * j + 256)
+            want = oracle.quantize_blocks(bits_of(K), bits_of(V))[0]
+            pg, off = int(qbt[r, 256 * j // QBLOCK]), (256 * j) % QBLOCK // 256 * 51200
+            assert np.array_equal(qb[pg, off:off + 51200].cpu().numpy(), want), (l, r, j)
+
     sample = sorted({int(np.argmin(n)), int(np.argmax(n)), 3, *rng.choice(np.arange(8, R), 3, replace=False).tolist()})
     for l in layers:
         Ks, Vs = [], []
         for r in sample:
-            K, V = rows_kv(l, [r], 0, int(n[r]))
-            assert torch.equal(K[0, -1], kn[l][r]) and torch.equal(V[0, -1], vn[l][r]), (l, r)   # the step's row
-            Ks.append(bits_of(K[0]))
-            Vs.append(bits_of(V[0]))
+            pg = int(bt[group[l]][r, L0[r] // EBS])                        # the step's row in the exact pages
+            assert torch.equal(ev[l][pg, :, L0[r] % EBS, :128], kn[l][r]), (l, r)
+            assert torch.equal(ev[l][pg, :, L0[r] % EBS, 128:], vn[l][r]), (l, r)
+            K, V = hist(l, [r], 0, int(L0[r]))
+            Ks.append(np.concatenate([bits_of(K[0]), bits_of(kn[l][r:r + 1])]))
+            Vs.append(np.concatenate([bits_of(V[0]), bits_of(vn[l][r:r + 1])]))
+        if l in vc.WINDOW_LAYERS:                         # the window layer's sinks come from the host layers' aux
+            for b, r in enumerate(sample):
+                for hl, arr in zip(vc.SINK_HOST[l], (Ks, Vs)):
+                    aux = qv[hl].view(torch.bfloat16).view(-1, QPAGE // 2)[int(qbt[r, 0]), AUX // 2:AUX // 2 + 2048]
+                    assert np.array_equal(bits_of(aux).reshape(4, 4, 128), arr[b][:4]), (l, r)
         case = oracle.build_paged(lambda b, p0, p1: (Ks[b][p0:p1], Vs[b][p0:p1]), [int(n[r]) for r in sample],
-                                  win=256 if l == 2 else 0, ebs=EBS, shuffle_seed=l)
+                                  win=256 if l in vc.WINDOW_LAYERS else 0, ebs=EBS, shuffle_seed=l)
         want = oracle.decode(case, bits_of(qs[l][sample]), cos, sin)
         o = outs[l][sample].float().cpu().numpy()
         w = torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()
         d = np.abs(o - w)
         say(f"full size layer {l}: rows {sample} max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
         assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
-    del ev, qv, lay, outs
+    del ev, qv, lay, outs, pools
     torch.cuda.empty_cache()
