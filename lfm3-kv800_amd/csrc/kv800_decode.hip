@@ -477,7 +477,7 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 constexpr int QWAVES = 4;
 constexpr float QLAZY = 0.f;   // rescale threshold (log2 units): p <= 2^QLAZY, and p vsc <= 448 stays far below 65,504
 constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 1;   // balanced schedule: sub-blocks per workgroup, most rounds
-constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords (kind, head, channel quad, lane group)
+constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords: (kind, head, channel quad, channel)
 constexpr int QROW = 132;
 constexpr int VBH = 34;        // staged vb rows per head: 32 + 2 of padding put head h + 2 16 banks away from head h
 struct QWaveLds {
@@ -526,12 +526,6 @@ __device__ __forceinline__ void rope4(const uint32_t (&k)[4], const uint32_t (&c
       : "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(cs[0]), "v"(cs[1]), "v"(cs[2]), "v"(cs[3]), "v"(sw[0]),
         "v"(sw[1]), "v"(sw[2]), "v"(sw[3]));
 }
-// (a & m) | (b & ~m) as one v_bfi_b32
-__device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
-  return r;
-}
 __device__ __forceinline__ b8 pack8b(const uint32_t (&x)[4]) { return as_b8(u4v{x[0], x[1], x[2], x[3]}); }
 
 // The K scale bytes of the 4 tables lane l builds, t = 4 l + e (kind t >> 7 = l >> 5, head (t >> 5) & 3, channel
@@ -539,17 +533,29 @@ __device__ __forceinline__ b8 pack8b(const uint32_t (&x)[4]) { return as_b8(u4v{
 // consecutive channels, one aligned dword each, byte e for table e (combined only when the tables are built, a
 // pair of chunks after they are issued).
 struct TabWords { uint32_t la, lb, sa, sb; };
-__device__ __forceinline__ TabWords table_words(const uint8_t* __restrict__ sb, int lane) {
-  const uint8_t* p = sb + KLO_O + 128 * ((lane >> 3) & 3) + 32 * (lane >> 5) + 4 * (lane & 7);
-  return TabWords{*reinterpret_cast<const uint32_t*>(p), *reinterpret_cast<const uint32_t*>(p + 64),
-                  *reinterpret_cast<const uint32_t*>(p + KSC_O - KLO_O),
-                  *reinterpret_cast<const uint32_t*>(p + KSC_O - KLO_O + 64)};
+// Sub-block reads go through a buffer resource of the sub-block (base and size in SGPRs, built per sub-block by
+// scalar instructions): each load's address is a lane constant plus a wave-uniform SGPR offset plus its immediate, so
+// no per-lane address arithmetic runs per chunk, and a read past the 51,200 bytes returns zeros.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;   // raw (untyped, unswizzled) buffer access on gfx9-family parts
+__device__ __forceinline__ rsrc_t sub_rsrc(const uint8_t* sb) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(sb), (short)0, SUB, RSRC_WORD3);
+}
+__device__ __forceinline__ TabWords table_words(rsrc_t rs, int lane) {
+  const int o = 128 * ((lane >> 3) & 3) + 32 * (lane >> 5) + 4 * (lane & 7);
+  return TabWords{__builtin_amdgcn_raw_buffer_load_b32(rs, o, KLO_O, 0),
+                  __builtin_amdgcn_raw_buffer_load_b32(rs, o + 64, KLO_O, 0),
+                  __builtin_amdgcn_raw_buffer_load_b32(rs, o, KSC_O, 0),
+                  __builtin_amdgcn_raw_buffer_load_b32(rs, o + 64, KSC_O, 0)};
 }
 // Table t of a wave's LUT: entry (ca, cb) = bf16(ca ksc_a + klo_a) | bf16(cb ksc_b + klo_b) << 16 (kv800.py:84-86:
-// the product is exact in fp32, so the fused multiply-add rounds where torch's add does). The tables of channels
-// 8 g + 4 d + e, e < 4, fill the 256-byte block ((kind 4 + h) 2 + d) 4 + g, table e in its 64-byte slot e ^ (g & 1),
-// entry (ca, cb) at dword ca + 4 cb of the slot: the 32 lanes of a half-wave read two lane groups' tables, whose 16
-// entries each occupy one half of the 32 LDS banks.
+// the product is exact in fp32, so the fused multiply-add rounds where torch's add does). Channel j = 8 g + 4 d + e of
+// (kind, head h) has its table in the 256-byte block ((kind 4 + h) 2 + d) 4 + e, entry (ca, cb) at byte
+// 4 ca + 16 g + 64 cb: the four lane groups' tables of one (kind, h, d, e) interleave in one block, so a lookup's
+// address is the masked kc byte (4 ca + 64 cb, code_lookup) or'ed with the lane's 16 g and the wave's LUT base, and
+// its block is the instruction's immediate offset. Lane group g's 16 entries sit in banks 4 g .. 4 g + 3 and
+// 16 + 4 g .. + 3 of the 32: the two groups of a half-wave never meet; within a group, entries whose cb differ by 2
+// share a bank.
 __device__ __forceinline__ void lut_build4(uint32_t* lut, int lane, const TabWords& tw) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -561,24 +567,30 @@ __device__ __forceinline__ void lut_build4(uint32_t* lut, int lane, const TabWor
     uint32_t pa[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) pa[c] = bfpk(fmaf((float)c, v[2], v[0]), fmaf((float)c, v[3], v[1]));
-    uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + g) + 16 * (e ^ (g & 1));
-    // row cb of the table at dword 4 cb; write k stores row (k + r) & 3 with r = d | (j >> 3 & 2): the 8 lanes of one
-    // 128-byte write cycle (lanes 8 m .. 8 m + 7: same kind, head and e) then cover the 32 banks once, bank group
-    // 4 (slot & 1) + row
-    const int r = d | ((j >> 3) & 2);
+    uint32_t* tab = lut + 64 * (((kind * 4 + h) * 2 + d) * 4 + e) + 4 * g;
+    // row cb (entries ca = 0..3) at dword 16 cb; write k stores row (k + d) & 3: the 8 lanes of one 128-byte write
+    // cycle (same kind, head and e; d = lane & 1, g = (lane & 7) >> 1) then cover the 32 banks once
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int cb = (k + r) & 3;
+      const int cb = (k + d) & 3;
       const uint32_t hi = (cb & 2 ? (cb & 1 ? pa[3] : pa[2]) : (cb & 1 ? pa[1] : pa[0])) & 0xFFFF0000u;
-      *reinterpret_cast<u4v*>(tab + 4 * cb) =
+      *reinterpret_cast<u4v*>(tab + 16 * cb) =
           u4v{(pa[0] & 0xFFFFu) | hi, (pa[1] & 0xFFFFu) | hi, (pa[2] & 0xFFFFu) | hi, (pa[3] & 0xFFFFu) | hi};
     }
   }
 }
+// Byte E of x, zero-extended, or'ed with base: one v_or_b32_sdwa (the compiler forms it from two instructions).
+template <int E>
+__device__ __forceinline__ uint32_t byte_or(uint32_t x, uint32_t base) {
+  uint32_t r;
+  asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c3 src1_sel:DWORD"
+      : "=v"(r) : "v"(x), "v"(base), "n"(E));
+  return r;
+}
 // vlo / vsc bytes of token t (both head groups)
-__device__ __forceinline__ uint32_t scale_bytes(const uint8_t* __restrict__ sb, int t) {
-  return (uint32_t)*reinterpret_cast<const uint16_t*>(sb + VLO_O + 2 * t) |
-         ((uint32_t)*reinterpret_cast<const uint16_t*>(sb + VSC_O + 2 * t) << 16);
+__device__ __forceinline__ uint32_t scale_bytes(rsrc_t rs, int t0, int lane) {   // token t0 + lane
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, 2 * lane, VLO_O + 2 * t0, 0) |
+         ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, 2 * lane, VSC_O + 2 * t0, 0) << 16);
 }
 
 struct QChunk {                // one chunk's data in registers
@@ -586,21 +598,23 @@ struct QChunk {                // one chunk's data in registers
   u4v cs[2][2];                // [tile u][d]: (cos, sin) bf16 pairs of channels 8 g + 4 d .. + 3 at the token's position
   u4v vb[2];                   // vb bytes 32 lane .. 32 lane + 31 of the chunk: token lane / 2, heads 2 (lane % 2), + 1
 };
-__device__ __forceinline__ void qload(QChunk& C, const uint8_t* __restrict__ sb, const uint32_t* __restrict__ csb, int t0,
-                                      int lane) {
+// rs: the sub-block; rc: the rope pair table, cpos: the sub-block's first position (token t0 of the sub-block is
+// at position cpos + t0)
+__device__ __forceinline__ void qload(QChunk& C, rsrc_t rs, rsrc_t rc, int cpos, int t0, int lane) {
   const int g = lane >> 4, n = lane & 15;
+  const int ok = n * 128 + 8 * g, oc = n * 128 + 32 * g;   // lane parts of the kc and pair-table offsets
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int t = t0 + 16 * u + n;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) C.kc[u][h] = *reinterpret_cast<const uint2*>(sb + KC_O + t * 128 + 32 * h + 8 * g);
-    const uint32_t* cp = csb + t * 32 + 8 * g;
-    C.cs[u][0] = *reinterpret_cast<const u4v*>(cp);
-    C.cs[u][1] = *reinterpret_cast<const u4v*>(cp + 4);
+    for (int h = 0; h < 4; ++h)
+      C.kc[u][h] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, ok + 2048 * u + 32 * h,
+                                                                                   KC_O + t0 * 128, 0));
+    C.cs[u][0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rc, oc + 2048 * u, (cpos + t0) * 128, 0));
+    C.cs[u][1] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rc, oc + 2048 * u + 16,
+                                                                               (cpos + t0) * 128, 0));
   }
-  const uint8_t* vp = sb + VB_O + t0 * 64 + 32 * lane;
-  C.vb[0] = *reinterpret_cast<const u4v*>(vp);
-  C.vb[1] = *reinterpret_cast<const u4v*>(vp + 16);
+  C.vb[0] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * lane, VB_O + t0 * 64, 0));
+  C.vb[1] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * lane + 16, VB_O + t0 * 64, 0));
 }
 
 static_assert(sizeof(XLds) <= 65536, "exact-tail scratch too large");
@@ -616,7 +630,8 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
                                            float* __restrict__ lo_out, float* __restrict__ ao, float scale, const int b,
                                            const int j0, const int j1, const int64_t prow) {
   QLds& L = *reinterpret_cast<QLds*>(lds_raw);
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // the wave index as a scalar: the span's sub-block offsets, buffer resources and loop bounds stay in SGPRs
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 4, n = lane & 15, hn = n >> 2;
   QWaveLds& W = L.wv[w];
   const char* lutc = reinterpret_cast<const char*>(&L.lut[0][0]);
@@ -641,8 +656,6 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       bq[2 + d] = pack8b(p);
     }
   }
-  // byte e of cg: 64 (e ^ (g & 1)), the slot of channel e's table in lane group g's block
-  const uint32_t cg = (g & 1) ? 0x80C00040u : 0xC0804000u;
 
   float m = NEG_BIG, lsum = 0.f, lvs = 0.f;
   f4 acc[8];
@@ -656,7 +669,7 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   };
 
   // One chunk of 32 tokens (tokens 64 w + 32 cc ..) of the current sub-block.
-  auto chunk = [&](const QChunk& C, int cc, uint32_t gw) {
+  auto chunk = [&](const QChunk& C, int cc, uint32_t kg) {
     {   // the chunk's vb rows into the wave's LDS copy (the previous chunk's reads were issued before)
       const int t = lane >> 1, s = vb_slot(t), h0 = 2 * (lane & 1);
       asm volatile("" ::: "memory");
@@ -674,16 +687,19 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const uint32_t x = d ? C.kc[u][h].y : C.kc[u][h].x;
-        // byte e: 4 ca + 16 cb + 64 slot, the entry's byte offset in the block (rope: ca = c0, cb = c2; nope: c1, c3)
-        const uint32_t R = bfi32(0x0C0C0C0Cu, x << 2, (x & 0x30303030u) | cg);
-        const uint32_t N = bfi32(0x0C0C0C0Cu, x, ((x >> 2) & 0x30303030u) | cg);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t sel = 0x0C0C0104u + (uint32_t)e;
-          const uint32_t ra = __builtin_amdgcn_perm(R, gw, sel), na = __builtin_amdgcn_perm(N, gw, sel);
-          kk[pb][u][e] = *reinterpret_cast<const uint32_t*>(lutc + ra + 1024 * (h * 2 + d));
-          an[pb][u][e] = *reinterpret_cast<const uint32_t*>(lutc + na + 1024 * ((4 + h) * 2 + d));
-        }
+        // byte e of xr: 4 c0 + 64 c2 (rope), of xn: 4 c1 + 64 c3 (nope); with kg (wave base + 16 g) the entry's
+        // address; the table's block (kind, h, d, e) is the immediate offset
+        const uint32_t xr = (x << 2) & 0xCCCCCCCCu, xn = x & 0xCCCCCCCCu;
+        const char* br = lutc + 256 * ((h * 2 + d) * 4);
+        const char* bn = lutc + 256 * (((4 + h) * 2 + d) * 4);
+        kk[pb][u][0] = *reinterpret_cast<const uint32_t*>(br + byte_or<0>(xr, kg));
+        an[pb][u][0] = *reinterpret_cast<const uint32_t*>(bn + byte_or<0>(xn, kg));
+        kk[pb][u][1] = *reinterpret_cast<const uint32_t*>(br + 256 + byte_or<1>(xr, kg));
+        an[pb][u][1] = *reinterpret_cast<const uint32_t*>(bn + 256 + byte_or<1>(xn, kg));
+        kk[pb][u][2] = *reinterpret_cast<const uint32_t*>(br + 512 + byte_or<2>(xr, kg));
+        an[pb][u][2] = *reinterpret_cast<const uint32_t*>(bn + 512 + byte_or<2>(xn, kg));
+        kk[pb][u][3] = *reinterpret_cast<const uint32_t*>(br + 768 + byte_or<3>(xr, kg));
+        an[pb][u][3] = *reinterpret_cast<const uint32_t*>(bn + 768 + byte_or<3>(xn, kg));
       }
     };
     // wave priority by phase: of a SIMD's two waves, the one in its LDS -> VALU -> MFMA QK chain (3) or softmax (2)
@@ -772,29 +788,35 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
     int64_t base = sanitize(brow[jb], jb);
     int64_t nraw = brow[min(jb + 1, j1 - 1)];   // the next sub-block's offset, loaded a sub-block ahead of its use
     const uint8_t* sb = qpool + (base < 0 ? 0 : base);
+    rsrc_t rs = sub_rsrc(sb);
+    const rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(cs2), (short)0,
+                                                        (int)min(rope_rows * 128, (int64_t)INT32_MAX), RSRC_WORD3);
+    int cpos = base < 0 ? 0 : jb * BLK;
     uint32_t* lut = L.lut[w];
-    const uint32_t gw = (((uint32_t)w << 6) | (uint32_t)g) << 8;   // byte 1: the wave's LUT and the lane group
+    const uint32_t kg = (uint32_t)w * (LUT_WORDS * 4) + 16u * (uint32_t)g;   // the wave's LUT and the lane group
     QChunk C0, C1;
-    qload(C0, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * pin, lane);
-    lut_build4(lut, lane, table_words(sb, lane));
-    stage_scales(scale_bytes(sb, 64 * pin + lane));
+    qload(C0, rs, rc, cpos, 64 * pin, lane);
+    lut_build4(lut, lane, table_words(rs, lane));
+    stage_scales(scale_bytes(rs, 64 * pin, lane));
     for (int P = P0; P < P1; ++P) {
       const bool more = P + 1 < P1, cross = more && pin == 3;   // the next pair is in the next sub-block
       const int njb = cross ? jb + 1 : jb, npin = cross ? 0 : (pin + 1) & 3;
       int64_t nbase = base;
-      const uint8_t* nsb = sb;
+      rsrc_t nrs = rs;
+      int ncpos = cpos;
       if (cross) {
         nbase = sanitize(nraw, njb);
-        nsb = qpool + (nbase < 0 ? 0 : nbase);
+        nrs = sub_rsrc(qpool + (nbase < 0 ? 0 : nbase));
+        ncpos = nbase < 0 ? 0 : njb * BLK;
         nraw = brow[min(njb + 1, j1 - 1)];
       }
       // the next sub-block's table words (used after this pair's chunks) and the next pair's scale bytes
-      const TabWords ntw = table_words(nsb, lane);
-      const uint32_t nsc = scale_bytes(nsb, 64 * npin + lane);
-      qload(C1, sb, cs2 + (int64_t)(base < 0 ? 0 : jb) * BLK * 32, 64 * pin + 32, lane);
-      if (base >= 0) chunk(C0, 0, gw);
-      qload(C0, nsb, cs2 + (int64_t)(nbase < 0 ? 0 : njb) * BLK * 32, 64 * npin, lane);
-      if (base >= 0) chunk(C1, 1, gw);
+      const TabWords ntw = table_words(nrs, lane);
+      const uint32_t nsc = scale_bytes(nrs, 64 * npin, lane);
+      qload(C1, rs, rc, cpos, 64 * pin + 32, lane);
+      if (base >= 0) chunk(C0, 0, kg);
+      qload(C0, nrs, rc, ncpos, 64 * npin, lane);
+      if (base >= 0) chunk(C1, 1, kg);
       if (more) {   // the wave's own LDS: its lookups and scale reads of this pair were issued before these writes
         if (cross) lut_build4(lut, lane, ntw);
         stage_scales(nsc);
@@ -802,11 +824,10 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
       jb = njb;
       pin = npin;
       base = nbase;
-      sb = nsb;
+      rs = nrs;
+      cpos = ncpos;
     }
-  }
-
-  // ---- combine the 4 waves of the span
+  }  // ---- combine the 4 waves of the span
   lsum = sum4rows(lsum);
   lvs = sum4rows(lvs);
   __syncthreads();

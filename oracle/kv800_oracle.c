@@ -305,10 +305,11 @@ static void score16(const float qf[16][128], const float* kr, float* sc, int64_t
   }
 }
 
-/* One row b of torch_decode.decode. q (16,128) bf16 bits, cos/sin (P,32) bf16 bits; out (16,128) bf16 bits.
+/* One row b of torch_decode.decode. q (16,128) bf16 bits, cos/sin (P,32) bf16 bits; out (16,128) bf16 bits and, if
+ * outf is not NULL, the same outputs before their bf16 rounding (f32).
  * Scratch: V (S, 512) f32 and sc (16, S) f32 with S >= nq*256 + 4 + (n - lo). */
 static void decode_row(const oracle_paged_t* P, int64_t b, const uint16_t* q, const uint16_t* cos_t,
-                       const uint16_t* sin_t, uint16_t* out, float* V, float* sc, int64_t smax) {
+                       const uint16_t* sin_t, uint16_t* out, float* outf, float* V, float* sc, int64_t smax) {
   const int64_t n = P->N[b], nq_b = P->NQ[b];
   const int64_t nqmax = P->win ? 0 : P->nqmax;
   const int64_t nq = nq_b < nqmax ? nq_b : nqmax;
@@ -365,7 +366,10 @@ static void decode_row(const oracle_paged_t* P, int64_t b, const uint16_t* q, co
     score16(qf, kr, sc, smax, S);
     ++S;
   }
-  if (S == 0) { for (int i = 0; i < 16 * 128; ++i) out[i] = 0; return; }
+  if (S == 0) {
+    for (int i = 0; i < 16 * 128; ++i) { out[i] = 0; if (outf) outf[i] = 0.f; }
+    return;
+  }
   const float scale = (float)pow(128.0, -0.5);
   for (int r = 0; r < 16; ++r) {
     float* sr = sc + (int64_t)r * smax;
@@ -381,13 +385,17 @@ static void decode_row(const oracle_paged_t* P, int64_t b, const uint16_t* q, co
       const float* vr = V + s * 512 + h * 128;
       for (int d = 0; d < 128; ++d) acc[d] += p * (double)vr[d];
     }
-    for (int d = 0; d < 128; ++d) out[r * 128 + d] = f2bf((float)acc[d]);
+    for (int d = 0; d < 128; ++d) {
+      out[r * 128 + d] = f2bf((float)acc[d]);
+      if (outf) outf[r * 128 + d] = (float)acc[d];
+    }
   }
 }
 
-/* torch_decode.decode over all B rows (rows in parallel). q (B,16,128) bf16; out (B,16,128) bf16. */
-int oracle_decode(const oracle_paged_t* P, int64_t B, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
-                  uint16_t* out) {
+/* torch_decode.decode over all B rows (rows in parallel). q (B,16,128) bf16; out (B,16,128) bf16; outf (B,16,128)
+ * f32 (or NULL): the outputs before their final bf16 rounding. */
+int oracle_decode_f32(const oracle_paged_t* P, int64_t B, const uint16_t* q, const uint16_t* cos_t,
+                      const uint16_t* sin_t, uint16_t* out, float* outf) {
   int64_t smax = 1;
   for (int64_t b = 0; b < B; ++b) {
     int64_t s = (int64_t)P->NQ[b] * BLK + NSINK + (P->N[b] > 0 ? P->N[b] : 0);
@@ -403,11 +411,17 @@ int oracle_decode(const oracle_paged_t* P, int64_t B, const uint16_t* q, const u
       bad = 1;
     } else {
 #pragma omp for schedule(dynamic, 1)
-      for (int64_t b = 0; b < B; ++b) decode_row(P, b, q + b * 2048, cos_t, sin_t, out + b * 2048, V, sc, smax);
+      for (int64_t b = 0; b < B; ++b)
+        decode_row(P, b, q + b * 2048, cos_t, sin_t, out + b * 2048, outf ? outf + b * 2048 : NULL, V, sc, smax);
     }
     free(V); free(sc);
   }
   return bad ? -1 : 0;
+}
+
+int oracle_decode(const oracle_paged_t* P, int64_t B, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
+                  uint16_t* out) {
+  return oracle_decode_f32(P, B, q, cos_t, sin_t, out, NULL);
 }
 
 /* kv800.py:231-236: MO, LO (B, ns+1, 16) f32; AO (B, ns+1, 16, 128) f32 -> out (B, 16, 128) bf16 bits. */

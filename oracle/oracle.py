@@ -53,6 +53,8 @@ def lib():
         L.oracle_dequantize_blocks.argtypes = [vp, i64, vp, vp]
         L.oracle_decode.argtypes = [ctypes.POINTER(Paged), i64, vp, vp, vp, vp]
         L.oracle_decode.restype = ctypes.c_int
+        L.oracle_decode_f32.argtypes = [ctypes.POINTER(Paged), i64, vp, vp, vp, vp, vp]
+        L.oracle_decode_f32.restype = ctypes.c_int
         L.oracle_combine.argtypes = [vp, vp, vp, i64, i64, vp]
         L.oracle_fake_quant_k.argtypes = [vp, i64, i64, vp]
         L.oracle_fake_quant_v.argtypes = [vp, i64, vp]
@@ -241,6 +243,19 @@ def decode(case, q_bits, cos_bits, sin_bits):
     if rc != 0:
         raise MemoryError("oracle decode scratch allocation failed")
     return out
+
+
+def decode_f32(case, q_bits, cos_bits, sin_bits):
+    """decode() and, beside its bf16 bits, the same outputs before their final bf16 rounding (float32)."""
+    q = np.ascontiguousarray(q_bits, np.uint16)
+    cs = np.ascontiguousarray(cos_bits, np.uint16); sn = np.ascontiguousarray(sin_bits, np.uint16)
+    out = np.empty((q.shape[0], 16, 128), np.uint16)
+    outf = np.empty((q.shape[0], 16, 128), np.float32)
+    st = case.c_struct()
+    rc = lib().oracle_decode_f32(ctypes.byref(st), q.shape[0], _p(q), _p(cs), _p(sn), _p(out), _p(outf))
+    if rc != 0:
+        raise MemoryError("oracle decode scratch allocation failed")
+    return out, outf
 
 
 def num_threads():

@@ -12,7 +12,7 @@ Layers: window + sinks 2 (exact group A, sinks in the aux of 6 (K) and 10 (V)), 
     byte for byte: sub-block j of a row is the oracle quantizer's bytes of positions [256 j, 256 j + 256) for every
     j < nq(seq_len), nothing else was written;
   * decode rows are within 2e-2 max-abs / 1e-3 mean-abs of the oracle's torch_decode over a cache built
-    independently from the same history;
+    independently from the same history (near-tie roundings excepted: decode_bar.py);
   * extend rows are within the same bar of a float64 attention over the keys the reference assembles for them
     (vllm_attn.py:351-402): quantized layers their nq(prev) dequantized sub-blocks, the exact rows from 256 nq(prev)
     on and the new rows; window layers the sinks, the last 255 positions and the new rows; sampled queries on long
@@ -20,6 +20,8 @@ Layers: window + sinks 2 (exact group A, sinks in the aux of 6 (K) and 10 (V)), 
 import numpy as np
 import pytest
 import torch
+
+import decode_bar
 
 from test_gpu_prefill import history_np, rope_np
 
@@ -150,10 +152,8 @@ def test_mixed_prefill_decode_steps(hip, oracle):
                 sn = np.zeros_like(sin)
             else:
                 cs, sn = cos, sin
-            want = as_f32(oracle.decode(case, q[l][:nd], cs, sn))
-            d = np.abs(outs[l][:nd] - want)
-            say(f"step {'ABC'[si]} layer {l} decode rows: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
-            assert np.isfinite(outs[l][:nd]).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
+            decode_bar.check(outs[l][:nd], oracle.decode_f32(case, q[l][:nd], cs, sn),
+                             f"step {'ABC'[si]} layer {l} decode rows", say)
 
         # ---- extend rows against float64 attention over the keys the reference assembles
         for l in LAYERS:

@@ -9,10 +9,12 @@ shuffled; window layer 2 keeps its sinks in the aux area of layers 6 (K) and 10 
   * every sub-block that became eligible was flushed from the layer's own exact group, bit-exact with the oracle
     quantizer, and no other quant sub-block changed;
   * each layer's decode output is within 2e-2 max-abs / 1e-3 mean-abs of the oracle's torch_decode over a cache built
-    independently from the rows' full K / V history."""
+    independently from the rows' full K / V history (near-tie roundings excepted: decode_bar.py)."""
 import numpy as np
 import pytest
 import torch
+
+import decode_bar
 
 pytestmark = pytest.mark.gpu
 
@@ -138,13 +140,7 @@ def test_vllm_decode_step(hip, oracle, early_flush):
         K, V = hist[l]
         case = oracle.build_paged(lambda b, p0, p1: (K[b, p0:p1], V[b, p0:p1]), list(n), win=256 if l == 2 else 0,
                                   ebs=EBS, shuffle_seed=l)
-        want = oracle.decode(case, q[l], cos, sin)
-        o = torch.from_numpy(outs[l].view(np.int16)).view(torch.bfloat16).float().numpy()
-        w = torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()
-        d = np.abs(o - w)
-        say(f"layer {l}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
-        assert np.isfinite(o).all()
-        assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
+        decode_bar.check(outs[l], oracle.decode_f32(case, q[l], cos, sin), f"layer {l}", say)
 
 
 def test_step_tables(hip):
@@ -303,11 +299,7 @@ def test_vllm_decode_step_full_size(hip, oracle):
                     assert np.array_equal(bits_of(aux).reshape(4, 4, 128), arr[b][:4]), (l, r)
         case = oracle.build_paged(lambda b, p0, p1: (Ks[b][p0:p1], Vs[b][p0:p1]), [int(n[r]) for r in sample],
                                   win=256 if l in vc.WINDOW_LAYERS else 0, ebs=EBS, shuffle_seed=l)
-        want = oracle.decode(case, bits_of(qs[l][sample]), cos, sin)
-        o = outs[l][sample].float().cpu().numpy()
-        w = torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()
-        d = np.abs(o - w)
-        say(f"full size layer {l}: rows {sample} max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
-        assert d.max() < MAX_ABS and d.mean() < MEAN_ABS, (l, d.max(), d.mean())
+        decode_bar.check(outs[l][sample].float().cpu().numpy(), oracle.decode_f32(case, bits_of(qs[l][sample]), cos, sin),
+                         f"full size layer {l}: rows {sample}", say)
     del ev, qv, lay, outs, pools
     torch.cuda.empty_cache()
