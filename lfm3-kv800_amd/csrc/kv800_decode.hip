@@ -861,9 +861,11 @@ __device__ __forceinline__ void quant_span(char* lds_raw, const uint16_t* __rest
   *reinterpret_cast<float4*>(ao + row * 128 + d0 + 4) = r1;
 }
 
-// Exact-tail work carried by the quantized-split grid: workgroups [0, nexact) each run the exact tail of one row's
-// KV head(s) (its exact partial slot, as decode_exact_kernel<false>) before the split workgroups, so their memory
-// latency overlaps the splits' VALU work on the same CUs instead of following it.
+// Exact-tail work carried by the quantized-split grid: the workgroups after the split workgroups, [nwork, nwork +
+// nexact), each run the exact tail of one row's KV head(s) (its exact partial slot, as decode_exact_kernel<false>).
+// Placed last, they take the slots the split workgroups free as they finish: placed first, they would hold half of
+// the CUs' workgroup slots for their latency-bound few microseconds while the split workgroups queued behind them,
+// whose one round of resident workgroups then ended that much later.
 struct ExactArgs {
   kv800_paged_t P;
   const uint16_t* cos_t;
@@ -952,15 +954,16 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
                     float* __restrict__ lo_out, float* __restrict__ ao, int ns, int spb, float scale, ExactArgs X,
                     Sched S) {
   __shared__ __align__(16) char lds_raw[QLDS_BYTES];
-  if ((int)blockIdx.x < X.nexact) {
+  const int nwork = (int)gridDim.x - X.nexact;
+  if ((int)blockIdx.x >= nwork) {
     constexpr int G = 4 / XNH_TAIL;   // workgroups per row
-    const int b = (int)blockIdx.x / G;
-    exact_row<XNH_TAIL, false>(*reinterpret_cast<XLds*>(lds_raw), b, ((int)blockIdx.x % G) * XNH_TAIL, X.P, q, X.cos_t,
+    const int xb = (int)blockIdx.x - nwork, b = xb / G;
+    exact_row<XNH_TAIL, false>(*reinterpret_cast<XLds*>(lds_raw), b, (xb % G) * XNH_TAIL, X.P, q, X.cos_t,
                                X.sin_t, X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns,
                                X.xs0 + b * X.xst, scale, X.nsink, nullptr);
     return;
   }
-  const int blk = (int)blockIdx.x - X.nexact;
+  const int blk = (int)blockIdx.x;
   int b, j0, j1;
   int64_t prow;
   bool rowwise = true;   // one span per workgroup (the fixed grid, the row-wise cut)
