@@ -433,20 +433,23 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
   }
 }
 
-// KV heads per workgroup of the fused exact kernel (window layers) and of the exact-tail workgroups of the quantized
-// grid, which must finish early to free their CUs for the split work. The standalone partial-writing variant uses the
-// tails' split, so its partials are bit-identical to the ones the quantized grid computes in-grid.
-constexpr int XNH = 4, XNH_TAIL = 1;
-template <bool MERGE> constexpr int exact_nh() { return MERGE ? XNH : XNH_TAIL; }
+// KV heads per workgroup of the exact-tail workgroups of the quantized grid, which must finish early to free their CUs
+// for the split work. The standalone partial-writing variant uses the tails' split, so its partials are bit-identical
+// to the ones the quantized grid computes in-grid. The fused exact kernel (window layers) takes NH = 1 while the 4 B
+// workgroups of that split fit one round of resident workgroups (more waves per row's chunks) and NH = 4 beyond
+// (one workgroup per row: fewer, longer workgroups keep more of the pool streaming per CU). MI355X, window 256 + 4
+// sinks at 32K: B = 64 / 96 / 128 take 14.0 / 19.0 / 19.6 us with NH = 1 and 25.1 / 25.3 / 25.3 us with NH = 4;
+// B = 160 / 192 / 256 / 398 take 27.1 / 28.6 / 33.3 / 50.2 us with NH = 1 and 25.4 / 25.5 / 27.4 / 45.7 us with NH = 4.
+constexpr int XNH_TAIL = 1;
 
-template <bool MERGE>
+template <int NH, bool MERGE>
 __global__ void __launch_bounds__(256)
 decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
                     const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
                     int nsink, uint16_t* __restrict__ out) {
   __shared__ XLds X;
-  constexpr int NH = exact_nh<MERGE>(), G = 4 / NH;   // KV heads per workgroup, workgroups per row
+  constexpr int G = 4 / NH;   // workgroups per row
   const int b = blockIdx.x / G;
   exact_row<NH, MERGE>(X, b, (blockIdx.x % G) * NH, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
                         lo_out, ao, ns, (int64_t)b * (ns + 1) + ns, scale, nsink, out);
@@ -1183,20 +1186,26 @@ int check_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t
 }
 
 // Launches decode_exact_kernel; with out != null the fused variant that also merges the quantized splits and writes
-// the bf16 rows.
+// the bf16 rows, with nh (1 or 4) KV heads per workgroup.
 int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
                  int64_t rope_rows, int64_t epool_elems, int64_t sink_elems, float* mo, float* lo, float* ao, int64_t B,
-                 int64_t ns, float scale, uint16_t* out, void* stream) {
+                 int64_t ns, float scale, uint16_t* out, int nh, void* stream) {
   if (B == 0) return KV800_OK;
   int nsink = 0, rc;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &nsink)) != KV800_OK) return rc;
-  const unsigned grid = (unsigned)(B * (4 / (out ? exact_nh<true>() : exact_nh<false>())));
-  if (out)
-    hipLaunchKernelGGL(decode_exact_kernel<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t, sin_t,
-                       rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
+  if (!out) nh = XNH_TAIL;
+  KV800_REQUIRE(nh == 1 || nh == 4, "decode_exact: 1 or 4 KV heads per workgroup");
+  const unsigned grid = (unsigned)(B * (4 / nh));
+  if (out && nh == 4)
+    hipLaunchKernelGGL((decode_exact_kernel<4, true>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
+                       sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
+  else if (out)
+    hipLaunchKernelGGL((decode_exact_kernel<1, true>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
+                       sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
   else
-    hipLaunchKernelGGL(decode_exact_kernel<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t, sin_t,
-                       rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, (uint16_t*)nullptr);
+    hipLaunchKernelGGL((decode_exact_kernel<XNH_TAIL, false>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q,
+                       cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink,
+                       (uint16_t*)nullptr);
   return check_launch(out ? "decode_exact_merge" : "decode_exact");
 }
 
@@ -1272,7 +1281,8 @@ int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_
 int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t,
                                  const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream) {
-  return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, nullptr, stream);
+  return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, nullptr,
+                      XNH_TAIL, stream);
 }
 
 int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
@@ -1364,7 +1374,9 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
     float* mo = (float*)ws;
     float* lo = (float*)(ws + align256(B * 16 * 4));
     float* ao = (float*)(ws + 2 * align256(B * 16 * 4));
-    return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, 0, scale, out, stream);
+    const int nh = 4 * B <= resident_groups() ? 1 : 4;
+    return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, 0, scale, out, nh,
+                        stream);
   }
   // spb > 0: fixed (row, split) grid of spb sub-blocks per split; spb == 0: balanced schedule with the library's group
   // count; spb < 0: balanced schedule with -spb groups
