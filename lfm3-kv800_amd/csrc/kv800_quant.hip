@@ -107,8 +107,9 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
   float* col_den = S.col_den;
 
   // ---------------- K: wave w = tokens 32w .. 32w + 31, lane = columns 8 lane .. 8 lane + 7 (head lane / 16). The
-  // rows are read in groups of KG tokens, twice (min / max, then codes; the second pass hits L2). KG = 4 keeps the
-  // pass within the 64 VGPRs of the V pass it shares a grid with (8 waves per SIMD).
+  // rows are read in groups of KG tokens, twice (min / max, then codes): the code pass walks the groups in reverse, so
+  // it starts with the rows read last, the ones most likely still in L2 while the rest of the grid streams through it.
+  // KG = 4 keeps the pass within the 64 VGPRs of the V pass it shares a grid with (8 waves per SIMD).
   const int h = lane >> 4, c0 = 8 * (lane & 15);
   float mn[8], mx[8];
 #pragma unroll
@@ -151,7 +152,7 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
     for (int e = 0; e < 8; ++e) { lof[e] = col_lo[hc0 + e]; den[e] = col_den[hc0 + e]; }
     const int p = (lane & 15) >> 2, q = lane & 3;   // plane of these 8 channels, byte quarter 8q .. 8q + 7
 #pragma unroll 1
-    for (int t0 = 0; t0 < TPW; t0 += KG) {
+    for (int t0 = TPW - KG; t0 >= 0; t0 -= KG) {
       uint4 kx[KG];
 #pragma unroll
       for (int tt = 0; tt < KG; ++tt) kx[tt] = *reinterpret_cast<const uint4*>(src.krow(TPW * w + t0 + tt, h) + c0);
