@@ -18,7 +18,10 @@ cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on
 oracle's time beside it). Extra
 fields: flush_c2 (config C2, the flush kernel alone), c4 (config 4, one decode step of all 6 attention
 layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
-sequences) and e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens). Every
+sequences), e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens), prefill
+(prefill over compressed history: 8 rows x a 2048-token chunk over 16K-token histories, the attention kernel against
+the MFMA peak), fake_quant (training fake quantization of one layer's K and V) and hbm_copy (a plain 1 GiB device
+copy: the bandwidth the box sustains). Every
 timed loop runs with the interpreter's garbage collector frozen (frozen_heap). --calib runs a plain copy of known size
 instead (rocprof FETCH/WRITE calibration)."""
 import argparse
@@ -323,6 +326,102 @@ def bench_e2e(torch, dev, steps, lens=None, seed=51, graph=False):
     return out
 
 
+PF_R, PF_HIST, PF_NEW = 8, 16384, 2048                # prefill rows, history tokens per row, new tokens per row
+MFMA_BF16_PEAK = 2500.0                               # TFLOP/s, MI355X dense bf16 / fp16
+
+
+def events_ms(torch, fn, n, warmup):
+    """Average duration of fn() over n calls, one HIP event pair per call on the current stream, after warmup calls."""
+    for _ in range(warmup):
+        fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    ev[-1][1].synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / n
+
+
+def bench_prefill(torch, kh, dev, steps, warmup):
+    """SURVEY f3, prefill over compressed history (vllm_attn.py:351-402 for quantized layers): PF_R rows, each
+    extending a PF_HIST-token history by one PF_NEW-query chunk (the reference's prefill chunk, vllm_attn.py:190-200),
+    through vllm_cache.prefill_quant_rows: the history producer (flushed sub-blocks dequantized and rotated to bf16,
+    exact rows rotated), the new rows' key RoPE, one flash-attention launch over all rows. The cache is a PagedStore
+    filled with seeded N(0,1) K / V by the HIP row writes and flushes. Whole calls host-timed (the row bookkeeping is
+    host work, as in the reference); the attention kernel alone by HIP events, against the MFMA bf16 peak: 4 x 128
+    flops per (query, visible key, query head)."""
+    import lfm3_kv800_amd.kv800 as kv
+    from lfm3_kv800_amd import vllm_cache as vc
+    g = torch.Generator(device=dev).manual_seed(61)
+    st = kv.PagedStore(PF_R, PF_HIST + 8, dev)
+    for c0 in range(0, PF_HIST, 2048):
+        n = min(PF_HIST, c0 + 2048) - c0
+        st.append(torch.randn(PF_R, n, 4, 128, generator=g, device=dev).to(torch.bfloat16),
+                  torch.randn(PF_R, n, 4, 128, generator=g, device=dev).to(torch.bfloat16))
+    P = st.paged()
+    T = PF_R * PF_NEW
+    q = torch.randn(T, 16, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(T, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = rope_tables(torch, PF_HIST + PF_NEW + 8, dev)
+    qsl = [i * PF_NEW for i in range(PF_R + 1)]
+    prev = [PF_HIST] * PF_R
+    run = lambda: vc.prefill_quant_rows(P, q, k, v, qsl, prev, cos, sin)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    assert bool(torch.isfinite(out.float()).all())
+    args = vc.prefill_quant_inputs(P, q, k, v, qsl, prev, cos, sin)
+    ms_k = events_ms(torch, lambda: kh.prefill(*args, window=0), steps, warmup)
+    pairs = PF_R * (PF_NEW * PF_HIST + PF_NEW * (PF_NEW + 1) // 2)      # (query, visible key) pairs, causal
+    flop = pairs * 16 * 4 * 128
+    tflops = flop / (ms_k * 1e-3) / 1e12
+    return {"workload": f"f3: prefill over compressed history, {PF_R} rows x {PF_NEW}-token chunk over "
+                        f"{PF_HIST}-token histories ({(PF_HIST - 128) // 256} flushed sub-blocks each), "
+                        "PagedStore geometry, N(0,1) q/K/V",
+            "ms": round(ms, 4), "tok_s": round(T / (ms * 1e-3), 1), "attention_kernel_ms": round(ms_k, 4),
+            "attention_flop": flop, "tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK, 4),
+            "bound": "mfma"}
+
+
+FQ_B, FQ_T = 8, 4096                                  # training batch of the fake-quant measurement
+
+
+def bench_fake_quant(torch, kh, dev, steps, warmup):
+    """SURVEY f4, training fake quantization (train.py:82-100): one quantized layer's keys and values of a training
+    batch of FQ_B sequences x FQ_T tokens, float32, 4 KV heads x 128: kv800_hip_fake_quant_k over (B, T / 256, 256,
+    512) and kv800_hip_fake_quant_v over (B T, 4, 128), HIP events per launch. Each reads and writes its tensor once;
+    V also runs the quantizer's and the dequantizer's fp32 Hadamard chains per token."""
+    g = torch.Generator(device=dev).manual_seed(71)
+    x = torch.randn(FQ_B, FQ_T // 256, 256, 512, generator=g, device=dev)
+    vv = torch.randn(FQ_B * FQ_T, 4, 128, generator=g, device=dev)
+    ms_k = events_ms(torch, lambda: kh.fake_quant_k(x), steps, warmup)
+    ms_v = events_ms(torch, lambda: kh.fake_quant_v(vv), steps, warmup)
+    nb = x.numel() * 4 * 2                                            # float32 read + written
+    return {"workload": f"f4: fake quantization of one layer's K and V, {FQ_B} x {FQ_T} tokens x 4 heads x 128, "
+                        "float32, N(0,1)",
+            "k_ms": round(ms_k, 4), "v_ms": round(ms_v, 4), "bytes_each": nb,
+            "k_gbps": round(nb / (ms_k * 1e-3) / 1e9, 1), "v_gbps": round(nb / (ms_v * 1e-3) / 1e9, 1),
+            "tok_s": round(FQ_B * FQ_T / ((ms_k + ms_v) * 1e-3), 1)}
+
+
+def bench_copy(torch, dev, steps):
+    """A plain 1 GiB device copy (read + write), HIP events: the HBM bandwidth this box sustains, beside the 8 TB/s
+    peak the roofline fractions use."""
+    x = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+    y = torch.empty_like(x)
+    ms = events_ms(torch, lambda: y.copy_(x), steps, 3)
+    gbps = 2 * x.numel() * 4 / (ms * 1e-3) / 1e9
+    del x, y
+    return {"bytes": 2 * (1 << 30), "ms": round(ms, 4), "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4)}
+
+
 def rope_tables(torch, n, dev):
     """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
     inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
@@ -560,8 +659,13 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = c4 = e2e = e2e_398 = None
+    flush_c2 = c4 = e2e = e2e_398 = prefill = fake_quant = copy = None
     if not a.c3_only:
+        copy = bench_copy(torch, dev, 10)
+        prefill = bench_prefill(torch, kh, dev, max(3, min(a.steps, 10)), 2)
+        torch.cuda.empty_cache()
+        fake_quant = bench_fake_quant(torch, kh, dev, extra_steps, 5)
+        torch.cuda.empty_cache()
         flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 200)
         torch.cuda.empty_cache()
         cos4, sin4 = rope_tables(torch, C4_MAX + 64, dev)
@@ -607,6 +711,9 @@ def main():
         "c4": c4,
         "e2e": e2e,
         "e2e_398x32k": e2e_398,
+        "prefill": prefill,
+        "fake_quant": fake_quant,
+        "hbm_copy": copy,
     }
     print(json.dumps(res), flush=True)
 

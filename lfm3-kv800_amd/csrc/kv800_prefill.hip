@@ -12,16 +12,21 @@
 //                     (the quantized, window + sinks and sliding masks of vllm_attn.py:168-184). fp32 scores and
 //                     online softmax, bf16 probabilities for the P.V product, fp32 accumulation, bf16 out.
 //
-// prefill_kernel, one workgroup = 16 consecutive queries of one row and one KV head g; wave w computes query head
-// 4 g + w, so the 4 waves share each 64-key tile staged in LDS. Per wave and tile, with v_mfma_f32_16x16x32_bf16
-// (lane l: D column l % 16, D rows 4 (l / 16) + 0..3; A row l % 16 and B column l % 16 over k = 8 (l / 16) + 0..7):
-//   S^T = K . Q^T   (keys x queries): A = K rows from LDS, B = the wave's 16 queries held in registers,
-//   O^T += V^T . P^T (dims x queries): A = V^T rows from LDS, B = the lane's own probabilities.
-// Both results keep one query per lane column (l % 16), so the softmax statistics of a query live in the four lanes
-// l % 16 and are combined with two cross-lane steps, and the O rescale needs no data movement. P^T's B operand is the
-// lane's 8 probabilities of keys 4 G + i and 16 + 4 G + i (G = l / 16) of each 32-key half; V^T is written to LDS with
-// its keys in that order (position 8 G + i and 8 G + 4 + i) so that its A operand is one 16-byte read.
-// Key tiles outside [first key a query of the tile can see, last key not in its future] are skipped: for window
+// prefill_kernel, one workgroup = 32 consecutive queries of one row and one KV head g; wave w computes query head
+// 4 g + w for its 32 queries as two 16-query blocks, so the 4 waves share each 64-key tile staged in LDS. Per wave and
+// tile, with v_mfma_f32_16x16x32_bf16 (lane l: D column l % 16, D rows 4 (l / 16) + 0..3; A row l % 16 and B column
+// l % 16 over k = 8 (l / 16) + 0..7):
+//   S^T = K . Q^T   (keys x queries): A = K rows from LDS, B = the wave's queries held in registers;
+//   O^T += V^T . P^T (dims x queries): A = V^T read from the V rows by ds_read_b64_tr_b16, B = the lane's own
+//                    probabilities;
+// each A operand feeds both query blocks. Both results keep one query per lane column (l % 16), so the softmax
+// statistics of a query live in the four lanes l % 16 and are combined with two cross-lane steps, and the O rescale
+// (lazy: only when a query's running max grows by more than PLAZY) needs no data movement. P^T's B operand is the
+// lane's 8 probabilities of keys 4 G + i and 16 + 4 G + i (G = l / 16) of each 32-key half, the key order in which
+// the transposed reads deliver V^T. The tiles are double-buffered in LDS (the next tile's loads, through a buffer
+// resource whose reads past the row's keys return zeros, are in flight while the current one is multiplied; one
+// barrier per tile), and a tile whose keys are all in range and precede the workgroup's first query is not masked.
+// Key tiles outside [first key a query of the workgroup can see, last key not in its future] are skipped: for window
 // layers only the sink keys and the keys of the window are read.
 #include "kv800_common.h"
 #include "../../include/kv800_hip.h"
@@ -33,6 +38,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef short b8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
 
 __device__ __forceinline__ f4 mfma_bf(u4v a, u4v b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0, 0);
@@ -58,17 +66,40 @@ rope_rows_kernel(const uint16_t* __restrict__ k, const int64_t* __restrict__ pos
   out[base + d + 64] = (uint16_t)f2bf(hi * c + lo * s);
 }
 
+// two floats -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32; equal to f2bf for finite values)
+__device__ __forceinline__ uint32_t bfpk(float a, float b) {
+  const bf2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // ---------------------------------------------------------------- flash attention of ragged rows
-constexpr int PQ = 16;      // queries per workgroup
+// A workgroup of 4 waves takes PQW = 32 consecutive queries of one row (the interface's query tiles 2 t and 2 t + 1
+// of the row: the workgroup of an odd tile returns at once) and one KV head g; wave w computes query head 4 g + w for
+// its 32 queries as two column blocks of 16. Keys come in tiles of 64, staged in LDS as K and V rows and
+// double-buffered: the next tile's loads are in flight while the current one is multiplied, one barrier per tile. Per
+// wave and tile on f32_16x16x32_bf16: S^T = K . Q^T (keys x queries: 4 key blocks x 2 query blocks x 4 k-steps, every
+// K operand read once for both query blocks) and O^T += V^T . P^T (8 dim blocks x 2 query blocks x 2 k-steps; the
+// V^T operand is read from the V rows by two ds_read_b64_tr_b16, in the key order of the lane's own probabilities,
+// once for both query blocks), so both results keep one query per lane column: a query's softmax statistics live in
+// four lanes (two cross-lane steps) and the O rescale moves no data. A tile whose keys all precede the workgroup's
+// first query (and are all in range) needs no mask: in a chunk over a long history, nearly every tile.
+constexpr int PQ = 16;      // queries per interface tile (tile_off counts these)
+constexpr int PQW = 32;     // queries per workgroup
 constexpr int PK = 64;      // keys per LDS tile
 constexpr int KROW = 136;   // K tile row stride (elements): 272 B, rows 4 banks apart for the 16-byte A reads
-constexpr int VROW = 72;    // V^T tile row stride (elements): 144 B, likewise
+constexpr int VROW = 144;   // V tile row stride (elements): 288 B, conflict-free transposed reads
 
-struct PLds {
+struct alignas(16) PTile {
   uint16_t k[PK * KROW];
-  uint16_t vt[128 * VROW];
+  uint16_t v[PK * VROW];
   int32_t kp[PK];
 };
+struct alignas(16) PLds {
+  PTile t[2];
+};
+constexpr float PLAZY = 8.f;   // log2 units a query's running max may lag its scores (p <= 2^8 in bf16)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;   // raw (untyped, unswizzled) buffer access on gfx9-family parts
 
 // first index in [0, n) with a[index] > x (a ascending)
 __device__ __forceinline__ int64_t upper(const int32_t* a, int64_t n, int64_t x) {
@@ -80,23 +111,16 @@ __device__ __forceinline__ int64_t upper(const int32_t* a, int64_t n, int64_t x)
   return lo;
 }
 
-// LDS position of key k (0..63) in the V^T tile: within each 32-key half, keys 4 G + i -> 8 G + i, 16 + 4 G + i ->
-// 8 G + 4 + i
-__device__ __forceinline__ int vt_pos(int k) {
-  const int h = k & 31;
-  return (k & 32) + 8 * ((h & 15) >> 2) + 4 * (h >> 4) + (h & 3);
-}
-
 __device__ __forceinline__ float xmax(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, const int64_t* __restrict__ qpos0,
                const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, const int32_t* __restrict__ kp,
                const int64_t* __restrict__ ksl, const int64_t* __restrict__ tile_off, int64_t R, int64_t window,
                int64_t nsink, float scale_log2, uint16_t* __restrict__ out) {
-  __shared__ PLds lds;
+  __shared__ __align__(16) PLds lds;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = blockIdx.y, h = 4 * g + w;
   const int col = lane & 15, G = lane >> 4;
@@ -107,12 +131,14 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     const int64_t mid = (lo + hi) >> 1;
     if (tile_off[mid] <= t) lo = mid; else hi = mid;
   }
-  const int64_t row = lo;
-  const int64_t q0 = qsl[row] + (t - tile_off[row]) * PQ;
-  const int nq = (int)min((int64_t)PQ, qsl[row + 1] - q0);
+  const int64_t row = lo, lt = t - tile_off[row];
+  if (lt & 1) return;   // covered by the workgroup of tile t - 1 (uniform over the workgroup)
+  const int64_t q0 = qsl[row] + lt * PQ;
+  const int nq = (int)min((int64_t)PQW, qsl[row + 1] - q0);
   const int64_t p0 = qpos0[row] + (q0 - qsl[row]);
   const int64_t ks = ksl[row], S = ksl[row + 1] - ks;
   const int32_t* kpr = kp + ks;
+
   // ---- key ranges: [0, sink_end) and [kbeg, kend)
   const int64_t kend = upper(kpr, S, p0 + nq - 1);
   int64_t kbeg = 0, sink_end = 0;
@@ -121,114 +147,178 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     sink_end = min(upper(kpr, S, nsink - 1), kbeg);
     if (kbeg <= sink_end) { kbeg = 0; sink_end = 0; }
   }
-  // ---- the wave's queries as the B operand of S^T = K . Q^T (4 k-steps of 32 dims)
-  const bool qok = col < nq;
-  const int64_t qpos = p0 + col;
-  u4v qb[4];
+  const int n0 = (int)((sink_end + PK - 1) / PK), nt = n0 + (int)((kend - kbeg + PK - 1) / PK);
+  // ---- the wave's queries as the B operands of S^T = K . Q^T (query block cq, 4 k-steps of 32 dims)
+  bool qok[2];
+  int qpos[2];
+  u4v qb[2][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    qb[s] = qok ? *reinterpret_cast<const u4v*>(q + ((q0 + col) * 16 + h) * 128 + 32 * s + 8 * G) : u4v{0, 0, 0, 0};
+  for (int cq = 0; cq < 2; ++cq) {
+    qok[cq] = 16 * cq + col < nq;
+    qpos[cq] = (int)(p0 + 16 * cq + col);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qb[cq][s] = qok[cq] ? *reinterpret_cast<const u4v*>(q + ((q0 + 16 * cq + col) * 16 + h) * 128 + 32 * s + 8 * G)
+                          : u4v{0, 0, 0, 0};
   }
-  f4 o[8];
+  f4 o[2][8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = f4{0.f, 0.f, 0.f, 0.f};
-  float m = -1e30f, lsum = 0.f;
+  for (int cq = 0; cq < 2; ++cq)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[cq][j] = f4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};
 
-  for (int range = 0; range < 2; ++range) {
-    const int64_t r0 = range ? kbeg : 0, r1 = range ? kend : sink_end;
-    for (int64_t k0 = r0; k0 < r1; k0 += PK) {
-      __syncthreads();                               // the previous tile has been read by every wave
-      // ---- stage K rows, V^T and positions of keys [k0, k0 + 64) clipped to r1
+  // ---- tile i's keys [k0, k0 + 64) clipped to r1: from the sink range, then from the main range
+  auto range_of = [&](int i, int64_t& k0, int64_t& r1) {
+    if (i < n0) { k0 = (int64_t)i * PK; r1 = sink_end; }
+    else { k0 = kbeg + (int64_t)(i - n0) * PK; r1 = kend; }
+  };
+  u4v sk[4], sv[4];            // the next tile's K and V rows in flight
+  int32_t skp = 0;
+  auto fetch = [&](int i) {
+    int64_t k0, r1;
+    range_of(i, k0, r1);
+    // the tile's K and V rows as buffers (base and size in SGPRs): a read past the row's S keys returns zeros, so every
+    // staging load is issued unconditionally (keys past a range's end carry the position 0x7FFFFFFF and are masked)
+    const int nbytes = (int)(min(S - k0, (int64_t)PK) * 1024);
+    const rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(K + (ks + k0) * 512), (short)0, nbytes,
+                                                        RSRC_WORD3);
+    const rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(V + (ks + k0) * 512), (short)0, nbytes,
+                                                        RSRC_WORD3);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = tid + 256 * r, j = c >> 4, part = c & 15;
-        u4v x = {0, 0, 0, 0};
-        if (k0 + j < r1) x = *reinterpret_cast<const u4v*>(K + ((ks + k0 + j) * 4 + g) * 128 + 8 * part);
-        *reinterpret_cast<u4v*>(&lds.k[j * KROW + 8 * part]) = x;
+    for (int r = 0; r < 4; ++r) {
+      const int c = tid + 256 * r, j = c >> 4, part = c & 15, off = j * 1024 + g * 256 + 16 * part;
+      sk[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      sv[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    }
+    if (tid < PK) skp = (k0 + tid < r1) ? kpr[k0 + tid] : 0x7FFFFFFF;
+  };
+  auto store = [&](PTile& T) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = tid + 256 * r, j = c >> 4, part = c & 15;
+      *reinterpret_cast<u4v*>(&T.k[j * KROW + 8 * part]) = sk[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = tid + 256 * r, j = c >> 4, part = c & 15;
+      *reinterpret_cast<u4v*>(&T.v[j * VROW + 8 * part]) = sv[r];
+    }
+    if (tid < PK) T.kp[tid] = skp;
+  };
+
+  if (nt > 0) {
+    fetch(0);
+    store(lds.t[0]);
+  }
+  __syncthreads();
+  for (int i = 0; i < nt; ++i) {
+    const PTile& T = lds.t[i & 1];
+    if (i + 1 < nt) fetch(i + 1);
+    // ---- S^T = K . Q^T: 4 blocks of 16 keys x 2 blocks of 16 queries
+    f4 sc[2][4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u4v a = *reinterpret_cast<const u4v*>(&T.k[(nb * 16 + col) * KROW + 32 * s + 8 * G]);
+        a0 = mfma_bf(a, qb[0][s], a0);
+        a1 = mfma_bf(a, qb[1][s], a1);
       }
+      sc[0][nb] = a0;
+      sc[1][nb] = a1;
+    }
+    // ---- mask, scale, online softmax per query block (the lane's 16 keys: nb * 16 + 4 G + i). No mask when every key
+    // of the tile is in range and precedes the workgroup's first query (quantized layers: no window).
+    int64_t tk0, tr1;
+    range_of(i, tk0, tr1);
+    const bool full = window <= 0 && tk0 + PK <= tr1 && (int64_t)T.kp[PK - 1] <= p0;
+    uint32_t pb[2][4][2];   // bf16 probabilities, packed in key pairs
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int u = tid + 256 * r, jp = u >> 4, part = u & 15, j = 2 * jp;
-        u4v a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-        if (k0 + j < r1) a = *reinterpret_cast<const u4v*>(V + ((ks + k0 + j) * 4 + g) * 128 + 8 * part);
-        if (k0 + j + 1 < r1) b = *reinterpret_cast<const u4v*>(V + ((ks + k0 + j + 1) * 4 + g) * 128 + 8 * part);
-        const int pcol = vt_pos(j);
+    for (int cq = 0; cq < 2; ++cq) {
+      if (!full) {
+        const int wlo = window > 0 ? (int)max((int64_t)qpos[cq] - window, (int64_t)INT32_MIN) : INT32_MIN;
+        const int ns = window > 0 ? (int)nsink : 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo2 = (a[e] & 0xFFFFu) | (b[e] << 16), hi2 = (a[e] >> 16) | (b[e] & 0xFFFF0000u);
-          *reinterpret_cast<uint32_t*>(&lds.vt[(8 * part + 2 * e) * VROW + pcol]) = lo2;
-          *reinterpret_cast<uint32_t*>(&lds.vt[(8 * part + 2 * e + 1) * VROW + pcol]) = hi2;
+        for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+          for (int i2 = 0; i2 < 4; ++i2) {
+            const int kpos = T.kp[nb * 16 + 4 * G + i2];
+            const bool keep = qok[cq] & (kpos <= qpos[cq]) & ((kpos > wlo) | (kpos < ns));
+            sc[cq][nb][i2] = keep ? sc[cq][nb][i2] : -INFINITY;
+          }
         }
       }
-      if (tid < PK) lds.kp[tid] = (k0 + tid < r1) ? kpr[k0 + tid] : 0x7FFFFFFF;
-      __syncthreads();
-      // ---- S^T = K . Q^T: 4 blocks of 16 keys
-      f4 sc[4];
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const u4v a = *reinterpret_cast<const u4v*>(&lds.k[(nb * 16 + col) * KROW + 32 * s + 8 * G]);
-          acc = mfma_bf(a, qb[s], acc);
-        }
-        sc[nb] = acc;
-      }
-      // ---- mask, scale, online softmax (the lane's 16 keys: nb * 16 + 4 G + i)
       float tmax = -INFINITY;
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
+      for (int nb = 0; nb < 4; ++nb)
+        tmax = fmaxf(tmax, fmaxf(fmaxf(sc[cq][nb][0], sc[cq][nb][1]), fmaxf(sc[cq][nb][2], sc[cq][nb][3])));
+      tmax = xmax(xmax(tmax, 16), 32) * scale_log2;   // scale > 0: the max of the scaled scores
+      if (__any(tmax > m[cq] + PLAZY)) {   // rescale only when a query's max outgrows its state (wave-uniform)
+        const float mnew = fmaxf(m[cq], tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m[cq] - mnew);
+        m[cq] = mnew;
+        lsum[cq] *= alpha;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t kpos = lds.kp[nb * 16 + 4 * G + i];
-          const bool keep = qok && kpos <= qpos && (window <= 0 || kpos > qpos - window || kpos < nsink);
-          const float x = keep ? sc[nb][i] * scale_log2 : -INFINITY;
-          sc[nb][i] = x;
-          tmax = fmaxf(tmax, x);
-        }
+        for (int j = 0; j < 8; ++j) o[cq][j] *= alpha;
       }
-      tmax = xmax(xmax(tmax, 16), 32);
-      const float mnew = fmaxf(m, tmax);
-      const float alpha = exp2f(m - mnew);
-      m = mnew;
+      const float mnew = m[cq];
       float psum = 0.f;
-      uint32_t pb[4][2];                             // bf16 probabilities, packed in key pairs
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = exp2f(sc[nb][i] - mnew);
-          psum += p[i];
+        for (int i2 = 0; i2 < 4; ++i2) {
+          p[i2] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[cq][nb][i2], scale_log2, -mnew));   // masked: -inf -> 0
+          psum += p[i2];
         }
-        pb[nb][0] = f2bf(p[0]) | (f2bf(p[1]) << 16);
-        pb[nb][1] = f2bf(p[2]) | (f2bf(p[3]) << 16);
+        pb[cq][nb][0] = bfpk(p[0], p[1]);
+        pb[cq][nb][1] = bfpk(p[2], p[3]);
       }
-      lsum = lsum * alpha + psum;
+      lsum[cq] += psum;
+    }
+    // ---- O^T += V^T . P^T: 2 halves of 32 keys x 8 blocks of 16 dims x 2 query blocks. A = V^T (row = dim; K = the
+    // half's keys 4 G .. 4 G + 3 and 16 + 4 G .. + 3, whose probabilities the lane holds) by two transposed reads
+    const int vrow = 4 * G + (col >> 2), vcol = 4 * (col & 3);
+    asm volatile("" ::: "memory");
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] *= alpha;
-      // ---- O^T += V^T . P^T: 2 halves of 32 keys x 8 blocks of 16 dims
+    for (int hh = 0; hh < 2; ++hh) {
+      const u4v b0 = {pb[0][2 * hh][0], pb[0][2 * hh][1], pb[0][2 * hh + 1][0], pb[0][2 * hh + 1][1]};
+      const u4v b1 = {pb[1][2 * hh][0], pb[1][2 * hh][1], pb[1][2 * hh + 1][0], pb[1][2 * hh + 1][1]};
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const u4v b = {pb[2 * hh][0], pb[2 * hh][1], pb[2 * hh + 1][0], pb[2 * hh + 1][1]};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const u4v a = *reinterpret_cast<const u4v*>(&lds.vt[(16 * j + col) * VROW + 32 * hh + 8 * G]);
-          o[j] = mfma_bf(a, b, o[j]);
-        }
+      for (int j = 0; j < 8; ++j) {
+        const s4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow) * VROW + 16 * j + vcol]));
+        const s4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow + 16) * VROW + 16 * j + vcol]));
+        const u4v a = {__builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 0, 1)),
+                       __builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 2, 3)),
+                       __builtin_bit_cast(uint32_t, __builtin_shufflevector(t1, t1, 0, 1)),
+                       __builtin_bit_cast(uint32_t, __builtin_shufflevector(t1, t1, 2, 3))};
+        o[0][j] = mfma_bf(a, b0, o[0][j]);
+        o[1][j] = mfma_bf(a, b1, o[1][j]);
       }
     }
+    asm volatile("" ::: "memory");
+    // the next tile into the other buffer, whose last reads (tile i - 1) ended at the previous barrier
+    if (i + 1 < nt) store(lds.t[(i + 1) & 1]);
+    __syncthreads();
   }
-  // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query col
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (!qok) return;
-  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-  uint16_t* dst = out + ((q0 + col) * 16 + h) * 128 + 4 * G;
+  // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query 16 cq + col
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const u2v v2 = {f2bf(o[j][0] * inv) | (f2bf(o[j][1] * inv) << 16), f2bf(o[j][2] * inv) | (f2bf(o[j][3] * inv) << 16)};
-    *reinterpret_cast<u2v*>(dst + 16 * j) = v2;
+  for (int cq = 0; cq < 2; ++cq) {
+    float l = lsum[cq];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (!qok[cq]) continue;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    uint16_t* dst = out + ((q0 + 16 * cq + col) * 16 + h) * 128 + 4 * G;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u2v v2 = {bfpk(o[cq][j][0] * inv, o[cq][j][1] * inv), bfpk(o[cq][j][2] * inv, o[cq][j][3] * inv)};
+      *reinterpret_cast<u2v*>(dst + 16 * j) = v2;
+    }
   }
 }
 

@@ -388,6 +388,12 @@ def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     (dequantized, rotated, bf16), the new keys out of one kv800_hip_rope_rows launch; each row's keys are its history
     followed by its new rows, and one kv800_hip_prefill launch attends all rows. qsl / prev are host sequences.
     Returns (T, 16, 128) bf16."""
+    return kv800_hip.prefill(*prefill_quant_inputs(P, q, k, v, qsl, prev, cos_t, sin_t), window=0)
+
+
+def prefill_quant_inputs(P, q, k, v, qsl, prev, cos_t, sin_t):
+    """The arguments of prefill_quant_rows' attention launch, (q, qsl, prev, K, V, key positions, key row starts):
+    the rows' keys (history, then new rows) and values assembled as prefill_quant_rows describes."""
     dev = q.device
     prev, qsl = [int(x) for x in prev], [int(x) for x in qsl]
     R = len(prev)
@@ -404,7 +410,7 @@ def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     Kc = torch.cat((Kh, Kn)).index_select(0, idx)
     Vc = torch.cat((Vh, v[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
     kp = torch.from_numpy(_ranges([0] * R, np.asarray(prev) + np.asarray(new)).astype(np.int32))
-    return kv800_hip.prefill(q, qsl, prev, Kc, Vc, kp, ksl, window=0)
+    return q, qsl, prev, Kc, Vc, kp, ksl
 
 
 def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
