@@ -4,7 +4,7 @@ tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape
 32 / 8 / 64).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--calib]
-                    [--c2-only | --c4-only | --e2e-only [--e2e-which both|256|398] [--e2e-steps S]]
+                    [--c2-only | --c4-only | --prefill-only | --e2e-only [--e2e-which both|256|398] [--e2e-steps S]]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Warm-up: the GPU reaches its sustained-load clocks only after tens of milliseconds of work (the first 50 C3 kernel
@@ -521,6 +521,7 @@ def main():
     ap.add_argument("--e2e-only", action="store_true", help="only the C5 decode loop; prints its record")
     ap.add_argument("--c2-only", action="store_true", help="only the C2 flush (counter passes of the flush kernel)")
     ap.add_argument("--c4-only", action="store_true", help="only the C4 step; prints its record")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prefill workload; prints its record")
     ap.add_argument("--e2e-steps", type=int, default=128)
     ap.add_argument("--e2e-which", choices=("both", "256", "398"), default="both",
                     help="with --e2e-only: the 256-sequence loop, the 398 x 32K one, or both")
@@ -547,6 +548,10 @@ def main():
 
     if a.c2_only:
         print(json.dumps({"flush_c2": bench_flush_c2(torch, kh, dev, a.steps, a.warmup)}), flush=True)
+        return
+
+    if a.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(torch, kh, dev, max(3, a.steps), 2)}), flush=True)
         return
 
     if a.c4_only:
