@@ -111,8 +111,20 @@ __device__ __forceinline__ int64_t upper(const int32_t* a, int64_t n, int64_t x)
   return lo;
 }
 
-__device__ __forceinline__ float xmax(float v, int mask) {
-  return fmaxf(v, __shfl_xor(v, mask, 64));
+// max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 without an LDS round trip: v_permlane16_swap and
+// v_permlane32_swap on two copies of x leave both 16-lane (32-lane) halves in every lane of a pair. All 64 lanes must
+// be active.
+__device__ __forceinline__ float max4rows(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum4rows(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __global__ void __launch_bounds__(256, 2)
@@ -254,7 +266,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
         tmax = fmaxf(tmax, fmaxf(fmaxf(sc[cq][nb][0], sc[cq][nb][1]), fmaxf(sc[cq][nb][2], sc[cq][nb][3])));
-      tmax = xmax(xmax(tmax, 16), 32) * scale_log2;   // scale > 0: the max of the scaled scores
+      tmax = max4rows(tmax) * scale_log2;   // scale > 0: the max of the scaled scores
       if (__any(tmax > m[cq] + PLAZY)) {   // rescale only when a query's max outgrows its state (wave-uniform)
         const float mnew = fmaxf(m[cq], tmax);
         const float alpha = __builtin_amdgcn_exp2f(m[cq] - mnew);
@@ -281,7 +293,6 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     // ---- O^T += V^T . P^T: 2 halves of 32 keys x 8 blocks of 16 dims x 2 query blocks. A = V^T (row = dim; K = the
     // half's keys 4 G .. 4 G + 3 and 16 + 4 G .. + 3, whose probabilities the lane holds) by two transposed reads
     const int vrow = 4 * G + (col >> 2), vcol = 4 * (col & 3);
-    asm volatile("" ::: "memory");
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const u4v b0 = {pb[0][2 * hh][0], pb[0][2 * hh][1], pb[0][2 * hh + 1][0], pb[0][2 * hh + 1][1]};
@@ -300,7 +311,6 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
         o[1][j] = mfma_bf(a, b1, o[1][j]);
       }
     }
-    asm volatile("" ::: "memory");
     // the next tile into the other buffer, whose last reads (tile i - 1) ended at the previous barrier
     if (i + 1 < nt) store(lds.t[(i + 1) & 1]);
     __syncthreads();
@@ -308,9 +318,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
   // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query 16 cq + col
 #pragma unroll
   for (int cq = 0; cq < 2; ++cq) {
-    float l = lsum[cq];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = sum4rows(lsum[cq]);
     if (!qok[cq]) continue;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     uint16_t* dst = out + ((q0 + 16 * cq + col) * 16 + h) * 128 + 4 * G;
