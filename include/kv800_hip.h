@@ -162,7 +162,7 @@ int kv800_hip_rope_rows(const uint16_t* k, const int64_t* pos, int64_t S, const 
  * kp <= the query's position and, with window > 0, kp > position - window or kp < nsink (nsink 4 for window + sinks
  * layers, 0 for sliding layers; window 0 for quantized layers). Scale 128^-0.5, fp32 scores and softmax, bf16
  * probabilities times bf16 V with fp32 accumulation, bf16 out (T, 16, 128). tile_off (R + 1, int64) is the prefix sum of
- * ceil((qsl[r+1] - qsl[r]) / 16) (the rows' 16-query tiles), ntiles = tile_off[R]. */
+ * ceil((qsl[r+1] - qsl[r]) / 32) (the rows' 32-query tiles), ntiles = tile_off[R] < 2^29. */
 int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
                       const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off, int64_t R,
                       int64_t ntiles, int64_t window, int64_t nsink, uint16_t* out, void* stream);

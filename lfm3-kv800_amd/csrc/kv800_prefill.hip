@@ -28,6 +28,8 @@
 // barrier per tile), and a tile whose keys are all in range and precede the workgroup's first query is not masked.
 // Key tiles outside [first key a query of the workgroup can see, last key not in its future] are skipped: for window
 // layers only the sink keys and the keys of the window are read.
+// The grid is one workgroup per (KV head, 32-query tile), numbered so that each XCD runs whole (KV head, row) runs of
+// tiles: the 64 workgroups of a 2048-query chunk walk the same key tiles together through one L2.
 #include "kv800_common.h"
 #include "../../include/kv800_hip.h"
 
@@ -73,9 +75,11 @@ __device__ __forceinline__ uint32_t bfpk(float a, float b) {
 }
 
 // ---------------------------------------------------------------- flash attention of ragged rows
-// A workgroup of 4 waves takes PQW = 32 consecutive queries of one row (the interface's query tiles 2 t and 2 t + 1
-// of the row: the workgroup of an odd tile returns at once) and one KV head g; wave w computes query head 4 g + w for
-// its 32 queries as two column blocks of 16. Keys come in tiles of 64, staged in LDS as K and V rows and
+// A workgroup of 4 waves takes PQ = 32 consecutive queries of one row (one interface tile) and one KV head g; wave w
+// computes query head 4 g + w for its 32 queries as two column blocks of 16. Every workgroup of the grid has work (a
+// grid whose idle workgroups sat at every other index put all the work on half the XCDs under round-robin dispatch),
+// and the workgroups of one (KV head, row) run on one XCD, in order, so the row's key tiles are read once into that
+// XCD's L2 for its 64 query tiles. Keys come in tiles of 64, staged in LDS as K and V rows and
 // double-buffered: the next tile's loads are in flight while the current one is multiplied, one barrier per tile. Per
 // wave and tile on f32_16x16x32_bf16: S^T = K . Q^T (keys x queries: 4 key blocks x 2 query blocks x 4 k-steps, every
 // K operand read once for both query blocks) and O^T += V^T . P^T (8 dim blocks x 2 query blocks x 2 k-steps; the
@@ -83,8 +87,7 @@ __device__ __forceinline__ uint32_t bfpk(float a, float b) {
 // once for both query blocks), so both results keep one query per lane column: a query's softmax statistics live in
 // four lanes (two cross-lane steps) and the O rescale moves no data. A tile whose keys all precede the workgroup's
 // first query (and are all in range) needs no mask: in a chunk over a long history, nearly every tile.
-constexpr int PQ = 16;      // queries per interface tile (tile_off counts these)
-constexpr int PQW = 32;     // queries per workgroup
+constexpr int PQ = 32;      // queries per workgroup = per interface tile (tile_off counts these)
 constexpr int PK = 64;      // keys per LDS tile
 constexpr int KROW = 136;   // K tile row stride (elements): 272 B, rows 4 banks apart for the 16-byte A reads
 constexpr int VROW = 144;   // V tile row stride (elements): 288 B, conflict-free transposed reads
@@ -134,19 +137,23 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
                int64_t nsink, float scale_log2, uint16_t* __restrict__ out) {
   __shared__ __align__(16) PLds lds;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = blockIdx.y, h = 4 * g + w;
+  // workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous run L = [x per + min(x, rem),
+  // ...) of the (g, t) order (t fastest), so the workgroups sharing a row's keys of one KV head share that XCD's L2
+  const int nb = (int)gridDim.x, xcd = (int)blockIdx.x & 7, per = nb >> 3, rem = nb & 7;
+  const int L = xcd * per + min(xcd, rem) + ((int)blockIdx.x >> 3);
+  const int ntl = nb >> 2;
+  const int g = L / ntl, h = 4 * g + w;
   const int col = lane & 15, G = lane >> 4;
   // ---- row of this tile: last i with tile_off[i] <= t
-  const int64_t t = blockIdx.x;
+  const int64_t t = L - g * ntl;
   int64_t lo = 0, hi = R;
   while (hi - lo > 1) {
     const int64_t mid = (lo + hi) >> 1;
     if (tile_off[mid] <= t) lo = mid; else hi = mid;
   }
   const int64_t row = lo, lt = t - tile_off[row];
-  if (lt & 1) return;   // covered by the workgroup of tile t - 1 (uniform over the workgroup)
   const int64_t q0 = qsl[row] + lt * PQ;
-  const int nq = (int)min((int64_t)PQW, qsl[row + 1] - q0);
+  const int nq = (int)min((int64_t)PQ, qsl[row + 1] - q0);
   const int64_t p0 = qpos0[row] + (q0 - qsl[row]);
   const int64_t ks = ksl[row], S = ksl[row + 1] - ks;
   const int32_t* kpr = kp + ks;
@@ -358,9 +365,9 @@ int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos
   KV800_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 &&
                 ((uintptr_t)out % 8) == 0, "prefill: q, K, V need 16-byte and out 8-byte alignment");
   KV800_REQUIRE(window >= 0 && nsink >= 0, "prefill: negative window or sink count");
-  KV800_REQUIRE(ntiles < (1ll << 31), "prefill: too many query tiles");
+  KV800_REQUIRE(ntiles < (1ll << 29), "prefill: too many query tiles");
   const float scale_log2 = 0.088388347648318440f * 1.4426950408889634f;   // 128^-0.5 * log2(e)
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)ntiles, 4), dim3(256), 0, (hipStream_t)stream, q, qsl, qpos0, K, V,
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)ntiles * 4), dim3(256), 0, (hipStream_t)stream, q, qsl, qpos0, K, V,
                      kp, ksl, tile_off, R, window, nsink, scale_log2, out);
   return check_launch("prefill");
 }

@@ -376,7 +376,7 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
     tiles = [0]
     for a, b in zip(qsl, qsl[1:]):
-        tiles.append(tiles[-1] + (b - a + 15) // 16)
+        tiles.append(tiles[-1] + (b - a + 31) // 32)   # 32-query tiles, one workgroup per tile and KV head
     if R == 0 or tiles[-1] == 0:
         return out
     meta = torch.tensor(qsl + ksl + qpos0 + tiles, dtype=torch.int64).to(dev)
