@@ -284,24 +284,36 @@ def page_offsets(bt, scale, add=0):
     return out
 
 
-def history(P, lens, cos_t=None, sin_t=None):
+def history(P, lens, cos_t=None, sin_t=None, out=None, offs=None):
     """Prefill over compressed history (kv800_hip_history, vllm_attn.py:351-380): rows b < len(lens) of the paged cache
     P, positions [0, lens[b]), as contiguous bf16 K (rotated with the (P, 32) cos_t / sin_t tables, or unrotated when
     they are None) and V, (sum(lens), 4, 128) each, row b's positions starting at offs[b]. Positions below
-    256 * P.NQ[b] are dequantized from their sub-blocks, the others read from the exact pages. Returns (K, V, offs)."""
+    256 * P.NQ[b] are dequantized from their sub-blocks, the others read from the exact pages. With out = (K, V)
+    ((S, 4, 128) bf16 each) and offs (R,) the rows are written there instead, row b's positions at rows offs[b] + p
+    (ranges that must fit in S); the other rows of out are left as they are. Returns (K, V, offs)."""
     L = ops()
     dev = P.epool.device
     lens = [int(x) for x in (lens.tolist() if torch.is_tensor(lens) else lens)]
     R = len(lens)
     if any(x < 0 for x in lens):
         raise ValueError("lens must be >= 0")
-    S = sum(lens)
-    K = torch.empty(S, 4, 128, dtype=torch.bfloat16, device=dev)
-    V = torch.empty_like(K)
-    offs = [0] * R
-    for b in range(1, R):
-        offs[b] = offs[b - 1] + lens[b - 1]
-    if R == 0 or S == 0:
+    if out is None:
+        S = sum(lens)
+        K = torch.empty(S, 4, 128, dtype=torch.bfloat16, device=dev)
+        V = torch.empty_like(K)
+        offs = [0] * R
+        for b in range(1, R):
+            offs[b] = offs[b - 1] + lens[b - 1]
+    else:
+        K, V = out
+        _need(K, "K", torch.bfloat16, dev); _need(V, "V", torch.bfloat16, dev)
+        if K.shape != V.shape or K.dim() != 3 or K.shape[1:] != (4, 128) or not (K.is_contiguous() and
+                                                                               V.is_contiguous()):
+            raise ValueError("out must be two contiguous (S, 4, 128) bf16 tensors")
+        offs = [int(x) for x in offs]
+        if len(offs) != R or any(o < 0 or o + n > K.shape[0] for o, n in zip(offs, lens)):
+            raise ValueError("offs must give each row's range inside out")
+    if R == 0 or sum(lens) == 0:
         return K, V, offs
     rot = cos_t is not None
     if rot:

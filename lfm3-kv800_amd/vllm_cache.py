@@ -398,17 +398,17 @@ def prefill_quant_inputs(P, q, k, v, qsl, prev, cos_t, sin_t):
     prev, qsl = [int(x) for x in prev], [int(x) for x in qsl]
     R = len(prev)
     new = [b - a for a, b in zip(qsl, qsl[1:])]
-    Kh, Vh, offs = kv800_hip.history(P, prev, cos_t, sin_t)
+    # key order: row 0's history, row 0's new rows, row 1's history, ...; the history launch writes each row's history
+    # in place, the new rows (rotated) follow by one index_copy_ each for K and V
+    ksl = np.concatenate(([0], np.cumsum(np.asarray(prev) + np.asarray(new)))).astype(np.int64)
+    Kc = torch.empty(int(ksl[-1]), 4, 128, dtype=torch.bfloat16, device=dev)
+    Vc = torch.empty_like(Kc)
+    kv800_hip.history(P, prev, cos_t, sin_t, out=(Kc, Vc), offs=ksl[:-1])
     pos_new = torch.from_numpy(_ranges(prev, new)).to(dev)
     Kn = kv800_hip.rope_rows(k[:qsl[-1]].to(torch.bfloat16), pos_new, cos_t, sin_t)
-    # key order: row 0's history, row 0's new rows, row 1's history, ... as rows of cat(Kh, Kn)
-    H = Kh.shape[0]
-    order = np.concatenate([np.concatenate((o + np.arange(n0), H + q0 + np.arange(c)))
-                            for o, n0, q0, c in zip(offs, prev, qsl[:-1], new)]) if R else np.zeros(0, np.int64)
-    ksl = np.concatenate(([0], np.cumsum(np.asarray(prev) + np.asarray(new)))).astype(np.int64)
-    idx = torch.from_numpy(order).to(dev)
-    Kc = torch.cat((Kh, Kn)).index_select(0, idx)
-    Vc = torch.cat((Vh, v[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
+    idx = torch.from_numpy(_ranges(ksl[:-1] + np.asarray(prev, np.int64), new)).to(dev)
+    Kc.index_copy_(0, idx, Kn)
+    Vc.index_copy_(0, idx, v[:qsl[-1]].to(torch.bfloat16))
     kp = torch.from_numpy(_ranges([0] * R, np.asarray(prev) + np.asarray(new)).astype(np.int32))
     return q, qsl, prev, Kc, Vc, kp, ksl
 
