@@ -13,6 +13,8 @@ import math
 import os
 from collections import OrderedDict
 
+import numpy as np
+
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -129,6 +131,18 @@ def _stream(dev):
 def _extent(t):
     """Elements from t's first element to the end of its storage (what the kernels may address from data_ptr)."""
     return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
+def host_to_device(x, dtype, dev):
+    """A host sequence or array as a tensor on dev: through pinned memory and an asynchronous copy on the current
+    stream on a GPU (a pageable copy waits for the stream's queued work, stalling the host behind the last launch)."""
+    t = x if torch.is_tensor(x) else torch.as_tensor(np.asarray(x), dtype=dtype)
+    t = t.to(dtype)
+    if t.device == dev:
+        return t
+    if dev.type == "cuda":
+        return t.pin_memory().to(dev, non_blocking=True)
+    return t.to(dev)
 
 
 def _need(t, name, dtype, dev):
@@ -328,7 +342,7 @@ def history(P, lens, cos_t=None, sin_t=None, out=None, offs=None):
     s = Paged()
     s.epool, s.eoff, s.eoff_stride = P.epool.data_ptr(), P.eoff.data_ptr(), P.eoff.stride(0)
     s.ebs, s.e_hs, s.e_ts, s.e_v = int(P.ebs), int(P.e_hs), int(P.e_ts), int(P.e_v)
-    N = torch.tensor(lens, dtype=torch.int32, device=dev)   # the output extents, from the host lengths
+    N = host_to_device(lens, torch.int32, dev)   # the output extents, from the host lengths
     s.N, s.NQ = N.data_ptr(), P.NQ.data_ptr()
     qbytes = 0
     if P.qpool is not None and P.boff is not None and P.boff.numel():
@@ -337,7 +351,7 @@ def history(P, lens, cos_t=None, sin_t=None, out=None, offs=None):
             raise ValueError("boff must cover the rows with contiguous rows")
         s.qpool, s.boff, s.boff_stride = P.qpool.data_ptr(), P.boff.data_ptr(), P.boff.stride(0)
         qbytes = _extent(P.qpool)
-    offt = torch.tensor(offs, dtype=torch.int64, device=dev)
+    offt = host_to_device(offs, torch.int64, dev)
     _check(L.kv800_hip_history(ctypes.byref(s), R, max(lens), _ptr(cos_t) if rot else None,
                                _ptr(sin_t) if rot else None, cos_t.shape[0] if rot else 0, qbytes, _extent(P.epool),
                                _ptr(offt), _ptr(K), _ptr(V), _stream(dev)))
@@ -382,7 +396,7 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
         raise ValueError(f"K / V must be (ksl[-1], 4, 128), got {tuple(K.shape)}, {tuple(V.shape)}")
     if any(b < a for a, b in zip(qsl, qsl[1:])) or any(b < a for a, b in zip(ksl, ksl[1:])):
         raise ValueError("qsl / ksl must be non-decreasing")
-    kp = kp.to(device=dev, dtype=torch.int32).contiguous()
+    kp = host_to_device(kp, torch.int32, dev).contiguous()
     if kp.shape != (K.shape[0],):
         raise ValueError("kp must be (S,)")
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
@@ -391,7 +405,7 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
         tiles.append(tiles[-1] + (b - a + 31) // 32)   # 32-query tiles, one workgroup per tile and KV head
     if R == 0 or tiles[-1] == 0:
         return out
-    meta = torch.tensor(qsl + ksl + qpos0 + tiles, dtype=torch.int64).to(dev)
+    meta = host_to_device(qsl + ksl + qpos0 + tiles, torch.int64, dev)
     m_qsl, m_ksl = meta[:R + 1], meta[R + 1:2 * R + 2]
     m_pos, m_tiles = meta[2 * R + 2:3 * R + 2], meta[3 * R + 2:]
     _check(L.kv800_hip_prefill(_ptr(q), _ptr(m_qsl), _ptr(m_pos), _ptr(K), _ptr(V), _ptr(kp), _ptr(m_ksl),

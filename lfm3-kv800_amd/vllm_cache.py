@@ -404,9 +404,9 @@ def prefill_quant_inputs(P, q, k, v, qsl, prev, cos_t, sin_t):
     Kc = torch.empty(int(ksl[-1]), 4, 128, dtype=torch.bfloat16, device=dev)
     Vc = torch.empty_like(Kc)
     kv800_hip.history(P, prev, cos_t, sin_t, out=(Kc, Vc), offs=ksl[:-1])
-    pos_new = torch.from_numpy(_ranges(prev, new)).to(dev)
+    pos_new = kv800_hip.host_to_device(_ranges(prev, new), torch.int64, dev)
     Kn = kv800_hip.rope_rows(k[:qsl[-1]].to(torch.bfloat16), pos_new, cos_t, sin_t)
-    idx = torch.from_numpy(_ranges(ksl[:-1] + np.asarray(prev, np.int64), new)).to(dev)
+    idx = kv800_hip.host_to_device(_ranges(ksl[:-1] + np.asarray(prev, np.int64), new), torch.int64, dev)
     Kc.index_copy_(0, idx, Kn)
     Vc.index_copy_(0, idx, v[:qsl[-1]].to(torch.bfloat16))
     kp = torch.from_numpy(_ranges([0] * R, np.asarray(prev) + np.asarray(new)).astype(np.int32))
@@ -435,8 +435,9 @@ def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     # ---- exact rows [lo, prev): element offset of each (position, head) K row through the page table
     xr = np.repeat(rows, nx)
     xp = _ranges(lo, nx)
-    page = P.eoff[torch.from_numpy(xr).to(dev), torch.from_numpy(xp // P.ebs).to(dev)]        # (Sx,) element offsets
-    ko = (page + torch.from_numpy((xp % P.ebs) * P.e_ts).to(dev))[:, None] + torch.arange(4, device=dev) * P.e_hs
+    h2d = lambda a: kv800_hip.host_to_device(a, torch.int64, dev)
+    page = P.eoff[h2d(xr), h2d(xp // P.ebs)]                                      # (Sx,) element offsets
+    ko = (page + h2d((xp % P.ebs) * P.e_ts))[:, None] + torch.arange(4, device=dev) * P.e_hs
     d128 = torch.arange(128, device=dev)
     ef = kv800.flat(P.epool)
     Kx, Vx = ef[ko[..., None] + d128], ef[ko[..., None] + P.e_v + d128]                          # (Sx, 4, 128)
@@ -444,9 +445,10 @@ def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
     if sinks:
         sr = np.repeat(rows, ns)
         st = _ranges(np.zeros(R, np.int64), ns)
-        so = torch.from_numpy(st * 512).to(dev)[:, None] + torch.arange(4, device=dev) * 128
-        Ks = kv800.flat(P.sk)[(P.skoff[torch.from_numpy(sr).to(dev)][:, None] + so)[..., None] + d128]
-        Vs = kv800.flat(P.sv)[(P.svoff[torch.from_numpy(sr).to(dev)][:, None] + so)[..., None] + d128]
+        so = h2d(st * 512)[:, None] + torch.arange(4, device=dev) * 128
+        srd = h2d(sr)
+        Ks = kv800.flat(P.sk)[(P.skoff[srd][:, None] + so)[..., None] + d128]
+        Vs = kv800.flat(P.sv)[(P.svoff[srd][:, None] + so)[..., None] + d128]
     else:
         Ks = Vs = torch.empty(0, 4, 128, dtype=torch.bfloat16, device=dev)
     # ---- per row: sinks, exact rows, new rows, as rows of cat(sinks, exact, new)
@@ -458,10 +460,10 @@ def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
                                                            new)]) if R else np.zeros(0, np.int64)
     kpos = np.concatenate([np.concatenate((np.arange(a), np.arange(l0, n0), np.arange(n0, n0 + c)))
                            for a, l0, n0, c in zip(ns, lo, p0, new)]) if R else np.zeros(0, np.int64)
-    idx = torch.from_numpy(order.astype(np.int64)).to(dev)
+    idx = h2d(order.astype(np.int64))
     Kc = torch.cat((Ks, Kx, k[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
     Vc = torch.cat((Vs, Vx, v[:qsl[-1]].to(torch.bfloat16))).index_select(0, idx)
     if cos_t is not None:
-        Kc = kv800_hip.rope_rows(Kc, torch.from_numpy(kpos).to(dev), cos_t, sin_t)
+        Kc = kv800_hip.rope_rows(Kc, h2d(kpos), cos_t, sin_t)
     return kv800_hip.prefill(q, qsl, prev, Kc, Vc, torch.from_numpy(kpos.astype(np.int32)), ksl, window=kv800.WIN,
                              nsink=kv800.NSINK if sinks else 0)
