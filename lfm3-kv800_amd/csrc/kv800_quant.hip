@@ -529,7 +529,8 @@ __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restri
 // dequantizer's fp32 chain, then bf16: dequantize_blocks, kv800.py:79-92), the others from the exact pages. RoPE is the
 // reference's fp32 kf c + rotate_half(kf) s over the 128-wide tables (cos32 | 1 | cos32 | 1), (sin32 | 0 | sin32 | 0),
 // each product and the sum rounded once, then bf16. Unreadable rows (offsets outside their pool, positions past the
-// rope table) are written as zeros. One workgroup per (256-position tile, row).
+// rope table) are written as zeros. One workgroup per (64-position tile, row): a quarter of a sub-block, so that
+// the V chain (one wave per token at a time) runs at eight waves per SIMD on a long prefill.
 __device__ __forceinline__ void rope8(float (&a)[8], float (&b)[8], const uint16_t* cs, const uint16_t* sn, bool rope) {
   // a = dims d0 .. d0 + 7, b = dims d0 + 64 .. d0 + 71; rope: d0 < 32 (cs / sn the tables' entries d0 ..), else the
   // unrotated dims, for which the table holds cos 1, sin 0
@@ -546,6 +547,7 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float (&x)[8]) {
                     f2bf(x[6]) | (f2bf(x[7]) << 16));
 }
 
+constexpr int HPOS = 64;   // positions per history workgroup (a quarter of a sub-block)
 __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uint16_t* __restrict__ cos_t,
                                                       const uint16_t* __restrict__ sin_t, int64_t rope_rows,
                                                       int64_t qpool_bytes, int64_t epool_elems,
@@ -554,15 +556,16 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
   __shared__ __align__(16) float xbuf[4][4 * VROW];   // per wave: one token's 4 dequantized V rows
   __shared__ float klo_s[512], ksc_s[512];
   const int r = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int n = P.N[r], p0 = blockIdx.x * BLK;
+  const int n = P.N[r], p0 = blockIdx.x * HPOS;
   if (p0 >= n) return;   // uniform over the workgroup
-  const int cnt = min(BLK, n - p0);
+  const int cnt = min(HPOS, n - p0);
+  const int sb = p0 / BLK, to = p0 - sb * BLK;   // the positions' sub-block and the first one's token in it
   const int64_t ob = out_off[r] + p0;
   const bool rot = cos_t != nullptr;
   const int nq = min((int64_t)max(P.NQ[r], 0), P.boff_stride);
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  if ((int)blockIdx.x < nq) {
-    const int64_t base = P.boff[(int64_t)r * P.boff_stride + blockIdx.x];
+  if (sb < nq) {
+    const int64_t base = P.boff[(int64_t)r * P.boff_stride + sb];
     const bool ok = base >= 0 && base + SUB <= qpool_bytes;   // uniform
     const uint8_t* s = P.qpool + (ok ? base : 0);
     if (ok)
@@ -578,7 +581,7 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
         *reinterpret_cast<uint4*>(ko + 64) = zero4;
         continue;
       }
-      const uint2 by = *reinterpret_cast<const uint2*>(s + KC_O + (t * 4 + h) * 32 + (d0 & 31));
+      const uint2 by = *reinterpret_cast<const uint2*>(s + KC_O + ((to + t) * 4 + h) * 32 + (d0 & 31));
       const uint32_t bw[2] = {by.x, by.y};
       const int sa = 2 * (d0 >> 5), sb = sa + 4;   // code fields of dims d0 + e and d0 + 64 + e
       float a[8], b[8];
@@ -606,8 +609,8 @@ __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uin
         continue;
       }
       {
-        const float vsc = f8d(s[VSC_O + t * 2 + (hh >> 1)]), vlo = f8d(s[VLO_O + t * 2 + (hh >> 1)]);
-        const uint8_t* vb = s + VB_O + (t * 4 + hh) * 16;
+        const float vsc = f8d(s[VSC_O + (to + t) * 2 + (hh >> 1)]), vlo = f8d(s[VLO_O + (to + t) * 2 + (hh >> 1)]);
+        const uint8_t* vb = s + VB_O + ((to + t) * 4 + hh) * 16;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int d = 8 * jj + e;
@@ -768,7 +771,7 @@ int kv800_hip_history(const kv800_paged_t* P, int64_t R, int64_t max_n, const ui
   KV800_REQUIRE(P->boff_stride == 0 || (P->qpool && P->boff), "history: quantized rows need qpool and boff");
   KV800_REQUIRE(((uintptr_t)k_out % 16) == 0 && ((uintptr_t)v_out % 16) == 0, "history: outputs must be 16-byte aligned");
   KV800_REQUIRE(R <= 65535, "history: at most 65535 rows per call");
-  const int64_t tiles = (max_n + BLK - 1) / BLK;
+  const int64_t tiles = (max_n + HPOS - 1) / HPOS;
   KV800_REQUIRE(tiles <= 0x7FFFFFFF, "history: max_n too large");
   hipLaunchKernelGGL(history_kernel, dim3((unsigned)tiles, (unsigned)R), dim3(256), 0, (hipStream_t)stream, *P, cos_t,
                      sin_t, rope_rows, qpool_bytes, epool_elems, out_off, k_out, v_out);
