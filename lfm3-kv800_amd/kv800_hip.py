@@ -319,6 +319,8 @@ def history(P, lens, cos_t=None, sin_t=None, out=None, offs=None):
         for b in range(1, R):
             offs[b] = offs[b - 1] + lens[b - 1]
     else:
+        if offs is None:
+            raise ValueError("history: out needs offs, each row's first output row")
         K, V = out
         _need(K, "K", torch.bfloat16, dev); _need(V, "V", torch.bfloat16, dev)
         if K.shape != V.shape or K.dim() != 3 or K.shape[1:] != (4, 128) or not (K.is_contiguous() and

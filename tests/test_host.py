@@ -85,3 +85,17 @@ def test_ranges_helper():
     assert got.tolist() == [5, 6, 7, 100, 101, 7]
     assert vc._ranges([], []).tolist() == []
     assert vc._ranges([3], [0]).tolist() == []
+
+
+def test_host_to_device_on_cpu():
+    """kv800_hip.host_to_device: lists, numpy arrays and tensors become tensors of the asked dtype on the device (on
+    the CPU here; on a GPU the copy goes through pinned memory, asynchronously)."""
+    import numpy as np
+    dev = torch.device("cpu")
+    a = kh.host_to_device([3, 1, 2], torch.int32, dev)
+    assert a.dtype == torch.int32 and a.tolist() == [3, 1, 2]
+    b = kh.host_to_device(np.arange(4, dtype=np.int64), torch.int64, dev)
+    assert b.dtype == torch.int64 and b.tolist() == [0, 1, 2, 3]
+    c = kh.host_to_device(torch.tensor([7, 8], dtype=torch.int64), torch.int32, dev)
+    assert c.dtype == torch.int32 and c.tolist() == [7, 8]
+    assert kh.host_to_device([], torch.int64, dev).numel() == 0
