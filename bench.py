@@ -20,8 +20,9 @@ fields: flush_c2 (config C2, the flush kernel alone), c4 (config
 layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
 sequences), e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens), prefill
 (prefill over compressed history: 8 rows x a 2048-token chunk over 16K-token histories, the attention kernel against
-the MFMA peak), fake_quant (training fake quantization of one layer's K and V) and hbm_copy (a plain 1 GiB device
-copy: the bandwidth the box sustains). Every
+the MFMA peak), fake_quant (training fake quantization of one layer's K and V), hbm_copy (a plain 1 GiB device
+copy: the bandwidth the box sustains) and hbm_read (a 4 GiB streaming read by kv800_hip_read_probe: the read
+bandwidth the part sustains for plain loads, and the decode kernel's achieved bandwidth as a fraction of it). Every
 timed loop runs with the interpreter's garbage collector frozen (frozen_heap). --calib runs a plain copy of known size
 instead (rocprof FETCH/WRITE calibration)."""
 import argparse
@@ -422,6 +423,17 @@ def bench_copy(torch, dev, steps):
     return {"bytes": 2 * (1 << 30), "ms": round(ms, 4), "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+def bench_read(torch, kh, dev, steps):
+    """A 4 GiB streaming read by kv800_hip_read_probe (plain 16-byte loads, 8 in flight per lane, 512 workgroups),
+    HIP events: the read bandwidth the part sustains for the decode kernels' kind of load, beside the 8 TB/s peak."""
+    x = torch.empty(1 << 32, dtype=torch.uint8, device=dev)
+    out = torch.empty(512, dtype=torch.int32, device=dev)
+    ms = events_ms(torch, lambda: kh.read_probe(x, out, 512), steps, 3)
+    gbps = x.numel() / (ms * 1e-3) / 1e9
+    del x, out
+    return {"bytes": 1 << 32, "ms": round(ms, 4), "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4)}
+
+
 def rope_tables(torch, n, dev):
     """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
     inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
@@ -664,9 +676,11 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = c4 = e2e = e2e_398 = prefill = fake_quant = copy = None
+    flush_c2 = c4 = e2e = e2e_398 = prefill = fake_quant = copy = read = None
     if not a.c3_only:
         copy = bench_copy(torch, dev, 10)
+        read = bench_read(torch, kh, dev, 10)
+        read["decode_quant_frac_of_read"] = round(achieved / read["gbps"], 4)
         prefill = bench_prefill(torch, kh, dev, max(3, min(a.steps, 10)), 2)
         torch.cuda.empty_cache()
         fake_quant = bench_fake_quant(torch, kh, dev, extra_steps, 5)
@@ -719,6 +733,7 @@ def main():
         "prefill": prefill,
         "fake_quant": fake_quant,
         "hbm_copy": copy,
+        "hbm_read": read,
     }
     print(json.dumps(res), flush=True)
 

@@ -238,6 +238,12 @@ int kv800_hip_decode_noalloc(const kv800_paged_t* P, const uint16_t* q, int64_t 
                              const uint16_t* sin_t, int64_t rope_rows, const uint32_t* cs2, int64_t qpool_bytes,
                              int64_t epool_elems, int64_t sink_elems, uint16_t* out, int64_t spb, void* stream);
 
+/* Streaming read of bytes (a positive multiple of 16) from buf with `groups` workgroups (8 plain 16-byte loads in
+ * flight per lane), writing one xor word per workgroup to out[0 .. groups). No counterpart in the reference: a
+ * measurement aid, the read bandwidth the part sustains for plain loads, against which bench.py sets the kernels'
+ * achieved bandwidth. */
+int kv800_hip_read_probe(const void* buf, int64_t bytes, uint32_t* out, int64_t groups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

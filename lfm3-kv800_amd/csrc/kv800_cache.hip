@@ -87,6 +87,33 @@ step_meta_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int64_t npag
   lens32[r] = (int32_t)n;
 }
 
+// Streaming-read probe (a measurement aid of bench.py, not part of the cache path): workgroup g reads the 16-byte
+// units g * 2048 + tid + 256 k (k < 8) of the buffer and every gridDim.x * 2048 units after, xor-folds them and writes
+// one word; with 8 loads in flight per lane and two workgroups per CU it reads at what the part sustains for
+// plain (cached) loads.
+typedef uint32_t pv4 __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(256) read_probe_kernel(const pv4* __restrict__ p, int64_t n16,
+                                                         uint32_t* __restrict__ out) {
+  constexpr int U = 8;
+  const int64_t stride = (int64_t)gridDim.x * 256 * U;
+  pv4 acc = {0u, 0u, 0u, 0u};
+  for (int64_t i = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i < n16; i += stride) {
+    pv4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = (i + 256 * u < n16) ? p[i + 256 * u] : pv4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u];
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t x = 0;
+    for (int k = 0; k < 256; ++k) x ^= red[k];
+    out[blockIdx.x] = x;
+  }
+}
+
 }  // namespace
 }  // namespace kv800
 
@@ -161,6 +188,16 @@ int kv800_hip_step_meta(const int32_t* bt, int64_t bt_stride, int64_t npages, co
   hipLaunchKernelGGL(step_meta_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, (hipStream_t)stream, bt,
                      bt_stride, npages, lens, R, ebs, slot, pos, lens32);
   return check_launch("step_meta");
+}
+
+int kv800_hip_read_probe(const void* buf, int64_t bytes, uint32_t* out, int64_t groups, void* stream) {
+  KV800_REQUIRE(buf && out, "read_probe: null pointer");
+  KV800_REQUIRE(bytes >= 16 && bytes % 16 == 0 && ((uintptr_t)buf % 16) == 0,
+                "read_probe: bytes must be a positive multiple of 16 and buf 16-byte aligned");
+  KV800_REQUIRE(groups >= 1 && groups <= 65536, "read_probe: groups must be in [1, 65536]");
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)groups), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const pv4*>(buf), bytes / 16, out);
+  return check_launch("read_probe");
 }
 
 }  // extern "C"

@@ -41,6 +41,7 @@ _VP, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_
 SIGNATURES = {
     "kv800_hip_version": (_I32, []),
     "kv800_hip_last_error": (ctypes.c_char_p, []),
+    "kv800_hip_read_probe": (_I32, [_VP, _I64, _VP, _I64, _VP]),
     "kv800_hip_quantize_blocks": (_I32, [_VP, _VP, _I64, _VP, _VP]),
     "kv800_hip_flush": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _I64, _I64,
                                _VP]),
@@ -413,6 +414,16 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
     _check(L.kv800_hip_prefill(_ptr(q), _ptr(m_qsl), _ptr(m_pos), _ptr(K), _ptr(V), _ptr(kp), _ptr(m_ksl),
                                _ptr(m_tiles), R, tiles[-1], int(window), int(nsink), _ptr(out), _stream(dev)))
     return out
+
+
+def read_probe(buf, out, groups):
+    """Streaming read of the whole of buf (a contiguous device tensor, a multiple of 16 bytes) by kv800_hip_read_probe
+    with `groups` workgroups; out: an int32 device tensor of at least `groups` entries (one xor word each)."""
+    L = ops()
+    if not (buf.is_cuda and out.is_cuda and buf.is_contiguous() and out.numel() >= groups):
+        raise ValueError("read_probe: contiguous device tensors, out with at least `groups` entries")
+    _check(L.kv800_hip_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(out), int(groups),
+                                  _stream(buf.device)))
 
 
 def fake_quant_k(x):

@@ -122,3 +122,22 @@ def test_decode_fp16_weight_range(hip, oracle, step):
     say(f"fp16 weight range: step {step} log2 units per sub-block, alpha {alpha:.4f}")
     got, want = run(hip, oracle, [blocks], q, tail_seed=11)
     check(got, want, f"fp16 weights step {step}")
+
+
+def test_read_probe_reads_every_unit(hip):
+    """kv800_hip_read_probe (bench.py's read-bandwidth measurement): the xor of its per-workgroup words equals the xor
+    of every dword of the buffer, for a buffer that is not a multiple of the grid's stride and for more workgroups
+    than the buffer has strides."""
+    import lfm3_kv800_amd.kv800_hip as kh
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for n16, groups in ((1_000_003, 512), (4097, 64), (1, 8)):
+        x = torch.randint(-2 ** 31, 2 ** 31 - 1, (4 * n16,), generator=g, device="cuda", dtype=torch.int64)
+        x = x.to(torch.int32)
+        out = torch.full((groups,), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+        kh.read_probe(x, out, groups)
+        torch.cuda.synchronize()
+        xs = x.cpu().numpy().view(np.uint32)
+        want = int(np.bitwise_xor.reduce(xs)) if xs.size else 0
+        got = int(np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)))
+        print(f"[gpu-range] read_probe n16={n16} groups={groups}: xor {got:#010x} vs {want:#010x}", flush=True)
+        assert got == want
