@@ -345,7 +345,7 @@ def events_ms(torch, fn, n, warmup):
 
 
 def bench_prefill(torch, kh, dev, steps, warmup):
-    """SURVEY f3, prefill over compressed history (vllm_attn.py:351-402 for quantized layers): PF_R rows, each
+    """Prefill over compressed history (vllm_attn.py:351-402 for quantized layers): PF_R rows, each
     extending a PF_HIST-token history by one PF_NEW-query chunk (the reference's prefill chunk, vllm_attn.py:190-200),
     through vllm_cache.prefill_quant_rows: the history producer (flushed sub-blocks dequantized and rotated to bf16,
     exact rows rotated), the new rows' key RoPE, one flash-attention launch over all rows. The cache is a PagedStore
@@ -395,7 +395,7 @@ FQ_B, FQ_T = 8, 4096                                  # training batch of the fa
 
 
 def bench_fake_quant(torch, kh, dev, steps, warmup):
-    """SURVEY f4, training fake quantization (train.py:82-100): one quantized layer's keys and values of a training
+    """Training fake quantization (train.py:82-100): one quantized layer's keys and values of a training
     batch of FQ_B sequences x FQ_T tokens, float32, 4 KV heads x 128: kv800_hip_fake_quant_k over (B, T / 256, 256,
     512) and kv800_hip_fake_quant_v over (B T, 4, 128), HIP events per launch. Each reads and writes its tensor once;
     V also runs the quantizer's and the dequantizer's fp32 Hadamard chains per token."""
