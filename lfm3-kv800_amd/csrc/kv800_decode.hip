@@ -479,7 +479,7 @@ decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint1
 // The table lookups of one instruction touch 4 tables (one per lane group) whose entries sit in disjoint LDS banks.
 constexpr int QWAVES = 4;
 constexpr float QLAZY = 0.f;   // rescale threshold (log2 units): p <= 2^QLAZY, and p vsc <= 448 stays far below 65,504
-constexpr int64_t BAL_CHUNK = 16, BAL_ROUNDS = 1;   // balanced schedule: sub-blocks per workgroup, most rounds
+constexpr int64_t BAL_CHUNK = 4, BAL_ROUNDS = 1;    // balanced schedule: sub-blocks per workgroup, most rounds
 constexpr int LUT_WORDS = 64 * 64;                     // 64 blocks of 64 dwords: (kind, head, channel quad, channel)
 constexpr int QROW = 132;
 constexpr int VBH = 34;        // staged vb rows per head: 32 + 2 of padding put head h + 2 16 banks away from head h
@@ -1343,7 +1343,10 @@ int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
   // about BAL_CHUNK sub-blocks per workgroup at the batch's largest size B * nqmax (ragged batches hold fewer
   // sub-blocks, and each workgroup then takes proportionally fewer); beyond one round of resident workgroups, whole
   // rounds, at most BAL_ROUNDS (one: longer spans in a single round measured faster than two or three rounds of
-  // shorter ones at 256-400 rows of up to 32K tokens)
+  // shorter ones at 256-400 rows of up to 32K tokens). Small batches are latency chains: at 32K tokens per row,
+  // B = 1 / 8 / 16 / 32 take 89 / 91 / 91 / 93 us at 16 sub-blocks per workgroup and 41 / 45 / 58 / 77 us at 4 (2 per
+  // workgroup: 42 / 58 / 58 / 77, the merge then reading twice the partials); from 64 rows on one round holds more
+  // than 4 per workgroup and the plan is the resident round either way.
   const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK, res = resident_groups();
   *groups = want < 1 ? 1 : want <= res ? want : min((want + res - 1) / res, BAL_ROUNDS) * res;
   return KV800_OK;
