@@ -22,7 +22,8 @@ sequences), e2e_398x32k (the same loop at the reference's published point, 398 s
 (prefill over compressed history: 8 rows x a 2048-token chunk over 16K-token histories, the attention kernel against
 the MFMA peak), fake_quant (training fake quantization of one layer's K and V), hbm_copy (a plain 1 GiB device
 copy: the bandwidth the box sustains) and hbm_read (a 4 GiB streaming read by kv800_hip_read_probe: the read
-bandwidth the part sustains for plain loads, and the decode kernel's achieved bandwidth as a fraction of it). Every
+bandwidth the part sustains for plain loads, and the decode kernel's achieved bandwidth as a fraction of it) and
+decode_small_batch (one decode layer's latency for 1, 8 and 16 rows of 32K tokens). Every
 timed loop runs with the interpreter's garbage collector frozen (frozen_heap). --calib runs a plain copy of known size
 instead (rocprof FETCH/WRITE calibration)."""
 import argparse
@@ -434,6 +435,32 @@ def bench_read(torch, kh, dev, steps):
     return {"bytes": 1 << 32, "ms": round(ms, 4), "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+def decode_small_batches(torch, kh, P, q, cos, sin, sizes=(1, 8, 16)):
+    """Latency of one decode layer for the first B rows of the C3 layer (32,768 tokens each): kv800.decode's default
+    plan, HIP events, median of 200 launches after 100; the small-batch regime of a serving engine, where each
+    workgroup's sub-block chain and not HBM sets the time."""
+    import lfm3_kv800_amd.kv800 as kv
+    s = torch.cuda.current_stream(q.device)
+    res = {}
+    for b in sizes:
+        Pb = kv.Paged(qpool=P.qpool, boff=P.boff[:b].contiguous(), epool=P.epool, eoff=P.eoff[:b].contiguous(),
+                      ebs=P.ebs, e_hs=P.e_hs, e_ts=P.e_ts, e_v=P.e_v, sk=None, sv=None, skoff=None, svoff=None,
+                      N=P.N[:b].contiguous(), NQ=P.NQ[:b].contiguous(), nqmax=P.nqmax, win=0)
+        qb = q[:b].contiguous()
+        for _ in range(100):
+            kh.decode(Pb, qb, cos, sin)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(200)]
+        for e0, e1 in ev:
+            e0.record(s)
+            kh.decode(Pb, qb, cos, sin)
+            e1.record(s)
+        ev[-1][1].synchronize()
+        t = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
+        res[str(b)] = round(t[len(t) // 2], 1)
+    return {"workload": "first B rows of the C3 layer (32,768 tokens each), whole kv800.decode, HIP events, median",
+            "unit": "us", "us": res}
+
+
 def rope_tables(torch, n, dev):
     """(cos, sin) (n, 32) bf16 of LFM3's full-attention layers (theta 1e6, fp32 product, bf16 cast)."""
     inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 128))
@@ -642,6 +669,7 @@ def main():
     out = kh.decode(layers[0], q, cos, sin)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
+    small = decode_small_batches(torch, kh, layers[0], q, cos, sin) if not a.c3_only else None
 
     achieved = QBYTES / (ms_quant * 1e-3) / 1e9
     layer_gbps = ALG_BYTES / (ms_step * 1e-3) / 1e9
@@ -734,6 +762,7 @@ def main():
         "fake_quant": fake_quant,
         "hbm_copy": copy,
         "hbm_read": read,
+        "decode_small_batch": small,
     }
     print(json.dumps(res), flush=True)
 
