@@ -167,6 +167,17 @@ int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos
                       const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off, int64_t R,
                       int64_t ntiles, int64_t window, int64_t nsink, uint16_t* out, void* stream);
 
+/* kv800_hip_prefill with each (query tile, KV head) split over `splits` (1 .. 256) ranges of its key tiles, for
+ * batches of few query tiles over long histories (a short extend chunk, a decode-like row): each split writes the
+ * unnormalised partial (o, m, l) of its queries to part (T x 16 heads x splits x 132 floats, T = qsl[R] the total
+ * query count, part_floats its size), and a second launch merges the splits (log-sum-exp) into out. splits = 1 is
+ * kv800_hip_prefill (part unused). Same arguments and masks otherwise; the same reference attention
+ * (vllm_attn.py:168-211), summed in a different order across the splits. */
+int kv800_hip_prefill_split(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
+                            const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off,
+                            int64_t R, int64_t ntiles, int64_t T, int64_t window, int64_t nsink, int64_t splits,
+                            float* part, int64_t part_floats, uint16_t* out, void* stream);
+
 /* Step bookkeeping in vLLM's page geometry (exact page [4 heads, ebs, K128 | V128] bf16 with element strides s0 (page),
  * s1 (head), s2 (token); quant page = 5 x 51,200-byte sub-blocks per 1280 tokens, qs0 bytes apart). */
 

@@ -88,6 +88,8 @@ __device__ __forceinline__ uint32_t bfpk(float a, float b) {
 // four lanes (two cross-lane steps) and the O rescale moves no data. A tile whose keys all precede the workgroup's
 // first query (and are all in range) needs no mask: in a chunk over a long history, nearly every tile.
 constexpr int PQ = 32;      // queries per workgroup = per interface tile (tile_off counts these)
+constexpr int PPART = 132;  // floats per key-split partial of (query, head): 128 dims of o, m, l, 2 of padding
+constexpr int PMAXSPLIT = 256;
 constexpr int PK = 64;      // keys per LDS tile
 constexpr int KROW = 136;   // K tile row stride (elements): 272 B, rows 4 banks apart for the 16-byte A reads
 constexpr int VROW = 144;   // V tile row stride (elements): 288 B, conflict-free transposed reads
@@ -104,12 +106,23 @@ constexpr float PLAZY = 8.f;   // log2 units a query's running max may lag its s
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int RSRC_WORD3 = 0x00020000;   // raw (untyped, unswizzled) buffer access on gfx9-family parts
 
-// first index in [0, n) with a[index] > x (a ascending)
+// first index in [0, n) with a[index] > x (a ascending), n if none: a 64-way search by the whole wave (lane l probes
+// lo + l step; the count of probes <= x, from a ballot, narrows [lo, hi) 64-fold), so n = 16K entries take three
+// dependent loads instead of fourteen. All 64 lanes must be active; the result is the same in every lane.
 __device__ __forceinline__ int64_t upper(const int32_t* a, int64_t n, int64_t x) {
-  int64_t lo = 0, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if ((int64_t)a[mid] <= x) lo = mid + 1; else hi = mid;
+  const int lane = threadIdx.x & 63;
+  int64_t lo = 0, hi = n;   // the answer lies in [lo, hi]
+  while (hi > lo) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t idx = lo + lane * step;
+    const bool le = idx < hi && (int64_t)a[idx < hi ? idx : lo] <= x;
+    const int c = __popcll(__ballot(le));   // probes 0 .. c - 1 are <= x (a ascending)
+    if (c == 0) return lo;
+    const int64_t last = lo + (int64_t)(c - 1) * step;   // a[last] <= x
+    const int64_t next = lo + (int64_t)c * step;          // the first probe > x, or past hi
+    lo = last + 1;
+    hi = next < hi ? next : hi;
+    if (step == 1) return lo;
   }
   return lo;
 }
@@ -134,18 +147,20 @@ __global__ void __launch_bounds__(256, 2)
 prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, const int64_t* __restrict__ qpos0,
                const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, const int32_t* __restrict__ kp,
                const int64_t* __restrict__ ksl, const int64_t* __restrict__ tile_off, int64_t R, int64_t window,
-               int64_t nsink, float scale_log2, uint16_t* __restrict__ out) {
+               int64_t nsink, float scale_log2, uint16_t* __restrict__ out, int splits, float* __restrict__ part) {
   __shared__ __align__(16) PLds lds;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous run L = [x per + min(x, rem),
-  // ...) of the (g, t) order (t fastest), so the workgroups sharing a row's keys of one KV head share that XCD's L2
+  // ...) of the (g, t, split) order (split fastest, then t), so the workgroups sharing a row's keys of one KV head
+  // share that XCD's L2
   const int nb = (int)gridDim.x, xcd = (int)blockIdx.x & 7, per = nb >> 3, rem = nb & 7;
   const int L = xcd * per + min(xcd, rem) + ((int)blockIdx.x >> 3);
-  const int ntl = nb >> 2;
-  const int g = L / ntl, h = 4 * g + w;
+  const int ntl = nb / (4 * splits);
+  const int g = L / (ntl * splits), h = 4 * g + w;
+  const int lr = L - g * ntl * splits, sp = lr % splits;
   const int col = lane & 15, G = lane >> 4;
   // ---- row of this tile: last i with tile_off[i] <= t
-  const int64_t t = L - g * ntl;
+  const int64_t t = lr / splits;
   int64_t lo = 0, hi = R;
   while (hi - lo > 1) {
     const int64_t mid = (lo + hi) >> 1;
@@ -167,6 +182,8 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     if (kbeg <= sink_end) { kbeg = 0; sink_end = 0; }
   }
   const int n0 = (int)((sink_end + PK - 1) / PK), nt = n0 + (int)((kend - kbeg + PK - 1) / PK);
+  // key split sp of `splits` takes tiles [i0, i1) of the nt (all of them without a split)
+  const int per_sp = (nt + splits - 1) / splits, i0 = min(nt, sp * per_sp), i1 = min(nt, i0 + per_sp);
   // ---- the wave's queries as the B operands of S^T = K . Q^T (query block cq, 4 k-steps of 32 dims)
   bool qok[2];
   int qpos[2];
@@ -226,14 +243,14 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     if (tid < PK) T.kp[tid] = skp;
   };
 
-  if (nt > 0) {
-    fetch(0);
-    store(lds.t[0]);
+  if (i0 < i1) {
+    fetch(i0);
+    store(lds.t[i0 & 1]);
   }
   __syncthreads();
-  for (int i = 0; i < nt; ++i) {
+  for (int i = i0; i < i1; ++i) {
     const PTile& T = lds.t[i & 1];
-    if (i + 1 < nt) fetch(i + 1);
+    if (i + 1 < i1) fetch(i + 1);
     // ---- S^T = K . Q^T: 4 blocks of 16 keys x 2 blocks of 16 queries
     f4 sc[2][4];
 #pragma unroll
@@ -319,14 +336,22 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
       }
     }
     // the next tile into the other buffer, whose last reads (tile i - 1) ended at the previous barrier
-    if (i + 1 < nt) store(lds.t[(i + 1) & 1]);
+    if (i + 1 < i1) store(lds.t[(i + 1) & 1]);
     __syncthreads();
   }
-  // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query 16 cq + col
+  // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query 16 cq + col. With a key split, the
+  // unnormalised partial (o, m, l) of (query, head, split) instead: PPART floats, o relative to 2^m
 #pragma unroll
   for (int cq = 0; cq < 2; ++cq) {
     const float l = sum4rows(lsum[cq]);
     if (!qok[cq]) continue;
+    if (part) {
+      float* pp = part + (((q0 + 16 * cq + col) * 16 + h) * splits + sp) * PPART;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *reinterpret_cast<f4*>(pp + 16 * j + 4 * G) = o[cq][j];
+      if (G == 0) { pp[128] = m[cq]; pp[129] = l; }
+      continue;
+    }
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     uint16_t* dst = out + ((q0 + 16 * cq + col) * 16 + h) * 128 + 4 * G;
 #pragma unroll
@@ -335,6 +360,53 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
       *reinterpret_cast<u2v*>(dst + 16 * j) = v2;
     }
   }
+}
+
+// ---------------------------------------------------------------- key-split merge
+// One wave per (query, head). Lanes read the splits' (m, l) in parallel: M = max m_s and L = sum l_s 2^(m_s - M) by
+// wave reductions; then lane holds dims 2 lane, 2 lane + 1 and sums o_s 2^(m_s - M) over the splits, eight loads in
+// flight; out = bf16(O / L) (a split without keys has l = 0 and o = 0).
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) x = fmaxf(x, __shfl_xor(x, k, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) x += __shfl_xor(x, k, 64);
+  return x;
+}
+__global__ void __launch_bounds__(256)
+prefill_merge_kernel(const float* __restrict__ part, int64_t pairs, int splits, uint16_t* __restrict__ out) {
+  const int64_t pr = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pr >= pairs) return;   // uniform over the wave
+  const int lane = threadIdx.x & 63;
+  const float* pp = part + pr * splits * PPART;
+  float M = -INFINITY;
+  for (int s = lane; s < splits; s += 64) M = fmaxf(M, pp[s * PPART + 128]);
+  M = wave_max(M);
+  float Ls = 0.f;
+  for (int s = lane; s < splits; s += 64) Ls += __builtin_amdgcn_exp2f(pp[s * PPART + 128] - M) * pp[s * PPART + 129];
+  Ls = wave_sum(Ls);
+  float o0 = 0.f, o1 = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float mv[8];
+    float2 av[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int sk = s0 + k < splits ? s0 + k : s0;   // past the last split: a repeat, weighted 0 below
+      mv[k] = s0 + k < splits ? pp[sk * PPART + 128] : -INFINITY;
+      av[k] = *reinterpret_cast<const float2*>(pp + sk * PPART + 2 * lane);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float wgt = __builtin_amdgcn_exp2f(mv[k] - M);
+      o0 += wgt * av[k].x;
+      o1 += wgt * av[k].y;
+    }
+  }
+  const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+  *reinterpret_cast<uint32_t*>(out + pr * 128 + 2 * lane) = bfpk(o0 * inv, o1 * inv);
 }
 
 }  // namespace
@@ -356,20 +428,42 @@ int kv800_hip_rope_rows(const uint16_t* k, const int64_t* pos, int64_t S, const 
   return check_launch("rope_rows");
 }
 
-int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
-                      const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off, int64_t R,
-                      int64_t ntiles, int64_t window, int64_t nsink, uint16_t* out, void* stream) {
-  KV800_REQUIRE(R >= 0 && ntiles >= 0, "prefill: negative R or tile count");
+int kv800_hip_prefill_split(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
+                            const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off,
+                            int64_t R, int64_t ntiles, int64_t T, int64_t window, int64_t nsink, int64_t splits,
+                            float* part, int64_t part_floats, uint16_t* out, void* stream) {
+  KV800_REQUIRE(R >= 0 && ntiles >= 0 && T >= 0, "prefill: negative R, tile count or query count");
   if (R == 0 || ntiles == 0) return KV800_OK;
   KV800_REQUIRE(q && qsl && qpos0 && K && V && kp && ksl && tile_off && out, "prefill: null pointer");
   KV800_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 &&
                 ((uintptr_t)out % 8) == 0, "prefill: q, K, V need 16-byte and out 8-byte alignment");
   KV800_REQUIRE(window >= 0 && nsink >= 0, "prefill: negative window or sink count");
-  KV800_REQUIRE(ntiles < (1ll << 29), "prefill: too many query tiles");
+  KV800_REQUIRE(splits >= 1 && splits <= PMAXSPLIT, "prefill: splits must be in [1, %d]", PMAXSPLIT);
+  KV800_REQUIRE(ntiles * 4 * splits < (1ll << 31), "prefill: too many query tiles x splits");
+  KV800_REQUIRE(ntiles <= (T + PQ - 1) / PQ + R, "prefill: more query tiles than T queries can hold");
+  if (splits > 1) {
+    KV800_REQUIRE(part && ((uintptr_t)part % 16) == 0, "prefill: a key split needs a 16-byte aligned part buffer");
+    KV800_REQUIRE(part_floats >= T * 16 * splits * PPART, "prefill: part holds %lld floats, the split needs %lld",
+                  (long long)part_floats, (long long)(T * 16 * splits * PPART));
+  }
   const float scale_log2 = 0.088388347648318440f * 1.4426950408889634f;   // 128^-0.5 * log2(e)
-  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)ntiles * 4), dim3(256), 0, (hipStream_t)stream, q, qsl, qpos0, K, V,
-                     kp, ksl, tile_off, R, window, nsink, scale_log2, out);
-  return check_launch("prefill");
+  hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)(ntiles * 4 * splits)), dim3(256), 0, (hipStream_t)stream, q, qsl,
+                     qpos0, K, V, kp, ksl, tile_off, R, window, nsink, scale_log2, out, (int)splits,
+                     splits > 1 ? part : (float*)nullptr);
+  int rc = check_launch("prefill");
+  if (rc != KV800_OK || splits == 1 || T == 0) return rc;
+  const int64_t pairs = T * 16;
+  hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, (hipStream_t)stream, part,
+                     pairs, (int)splits, out);
+  return check_launch("prefill_merge");
+}
+
+int kv800_hip_prefill(const uint16_t* q, const int64_t* qsl, const int64_t* qpos0, const uint16_t* K,
+                      const uint16_t* V, const int32_t* kp, const int64_t* ksl, const int64_t* tile_off, int64_t R,
+                      int64_t ntiles, int64_t window, int64_t nsink, uint16_t* out, void* stream) {
+  KV800_REQUIRE(ntiles < (1ll << 29), "prefill: too many query tiles");
+  return kv800_hip_prefill_split(q, qsl, qpos0, K, V, kp, ksl, tile_off, R, ntiles, ntiles * PQ, window, nsink, 1,
+                                 nullptr, 0, out, stream);
 }
 
 }  // extern "C"

@@ -71,6 +71,8 @@ SIGNATURES = {
     "kv800_hip_history": (_I32, [ctypes.POINTER(Paged), _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP]),
     "kv800_hip_rope_rows": (_I32, [_VP, _VP, _I64, _VP, _VP, _I64, _VP, _VP]),
     "kv800_hip_prefill": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _VP]),
+    "kv800_hip_prefill_split": (_I32, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64,
+                                        _VP, _I64, _VP, _VP]),
     "kv800_hip_fake_quant_k": (_I32, [_VP, _I64, _I64, _VP, _VP]),
     "kv800_hip_flush_latency": (_I32, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _VP, _I64, _I64, _I64, _VP, _VP,
                                        _I64, _I64, _VP]),
@@ -380,11 +382,25 @@ def rope_rows(k, pos, cos_t, sin_t):
     return out
 
 
-def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
-    """Prefill attention of ragged rows (kv800_hip_prefill): row r's queries q[qsl[r]:qsl[r+1]] ((T, 16, 128) bf16) at
-    positions qpos0[r], qpos0[r] + 1, ... over keys / values K, V[ksl[r]:ksl[r+1]] ((S, 4, 128) bf16) at positions kp
-    (S,) (ascending within a row). qsl / ksl / qpos0: host sequences (R + 1, R + 1, R). Mask: kp <= query position,
-    and with window > 0 also kp > position - window or kp < nsink. Returns (T, 16, 128) bf16."""
+PREFILL_SPLIT_BELOW = 256   # workgroups (query tiles x 4 KV heads) under which the key range is split
+PREFILL_SPLIT_TARGET = 512  # workgroups a split grid aims at (two per CU)
+
+
+def prefill_splits(tiles, max_key_tiles):
+    """Key splits of one prefill launch: 1 when its tiles x 4 workgroups nearly fill the GPU, else enough for about
+    PREFILL_SPLIT_TARGET workgroups, with at least two 64-key tiles per split and at most 64 splits."""
+    w = 4 * tiles
+    if w >= PREFILL_SPLIT_BELOW or max_key_tiles < 4:
+        return 1
+    return int(max(1, min(64, -(-PREFILL_SPLIT_TARGET // w), max_key_tiles // 2)))
+
+
+def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0, splits=None):
+    """Prefill attention of ragged rows (kv800_hip_prefill_split): row r's queries q[qsl[r]:qsl[r+1]] ((T, 16, 128)
+    bf16) at positions qpos0[r], qpos0[r] + 1, ... over keys / values K, V[ksl[r]:ksl[r+1]] ((S, 4, 128) bf16) at
+    positions kp (S,) (ascending within a row). qsl / ksl / qpos0: host sequences (R + 1, R + 1, R). Mask: kp <= query
+    position, and with window > 0 also kp > position - window or kp < nsink. splits: key splits per (query tile, KV
+    head) (default prefill_splits: few query tiles over long rows are split and merged). Returns (T, 16, 128) bf16."""
     L = ops()
     dev = q.device
     q, K, V = q.contiguous(), K.contiguous(), V.contiguous()
@@ -408,11 +424,17 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0):
         tiles.append(tiles[-1] + (b - a + 31) // 32)   # 32-query tiles, one workgroup per tile and KV head
     if R == 0 or tiles[-1] == 0:
         return out
+    if splits is None:
+        splits = prefill_splits(tiles[-1], max(-(-(b - a) // 64) for a, b in zip(ksl, ksl[1:])))
+    splits = int(splits)
+    T = qsl[-1]
+    part = torch.empty(T * 16 * splits * 132 if splits > 1 else 0, dtype=torch.float32, device=dev)
     meta = host_to_device(qsl + ksl + qpos0 + tiles, torch.int64, dev)
     m_qsl, m_ksl = meta[:R + 1], meta[R + 1:2 * R + 2]
     m_pos, m_tiles = meta[2 * R + 2:3 * R + 2], meta[3 * R + 2:]
-    _check(L.kv800_hip_prefill(_ptr(q), _ptr(m_qsl), _ptr(m_pos), _ptr(K), _ptr(V), _ptr(kp), _ptr(m_ksl),
-                               _ptr(m_tiles), R, tiles[-1], int(window), int(nsink), _ptr(out), _stream(dev)))
+    _check(L.kv800_hip_prefill_split(_ptr(q), _ptr(m_qsl), _ptr(m_pos), _ptr(K), _ptr(V), _ptr(kp), _ptr(m_ksl),
+                                     _ptr(m_tiles), R, tiles[-1], T, int(window), int(nsink), splits,
+                                     _ptr(part) if splits > 1 else None, part.numel(), _ptr(out), _stream(dev)))
     return out
 
 

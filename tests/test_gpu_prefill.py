@@ -122,6 +122,56 @@ def check_quant_rows(oracle, prev, new, seed):
     say(f"{R} rows: worst max-abs {worst:.3e}")
 
 
+def test_prefill_key_splits(hip, oracle):
+    """kv800_hip_prefill_split: the same rows with the key range of every (query tile, KV head) split 1, 2, 5, 24 and
+    64 ways (partials merged by log-sum-exp): each against float64 at the bar, and each within 4e-3 of the unsplit
+    kernel (a split rescales its probabilities by its own running max before their bf16 rounding, so single outputs
+    move by a few bf16 steps of the row's magnitude, not of their own)."""
+    from lfm3_kv800_amd import vllm_cache as vc
+    import lfm3_kv800_amd.kv800_hip as kh
+    rng = np.random.RandomState(19)
+    prev, new = [3000, 700, 0], [5, 40, 3]
+    lens = [p + t for p, t in zip(prev, new)]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    cos, sin = oracle.rope_tables(max(lens) + 8)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), prev, ebs=64, shuffle_seed=19)
+    P = upload(case)
+    q = oracle.randn_bf16(rng, (sum(new), 16, 128))
+    qsl = np.concatenate([[0], np.cumsum(new)]).astype(np.int64)
+    kn = np.concatenate([K[b][prev[b]:] for b in range(3)])
+    vn = np.concatenate([V[b][prev[b]:] for b in range(3)])
+    args = vc.prefill_quant_inputs(P, to_dev_bf16(q), to_dev_bf16(kn), to_dev_bf16(vn), qsl, prev, to_dev_bf16(cos),
+                                   to_dev_bf16(sin))
+    want = []
+    for b in range(3):
+        n0, n = prev[b], lens[b]
+        kb, vb = history_np(oracle, K[b], V[b], n0)
+        kb = np.concatenate([kb, K[b][n0:n]]); vb = np.concatenate([vb, V[b][n0:n]])
+        Kr = np.repeat(oracle.bf16_to_f32(rope_np(oracle, kb, np.arange(n), cos, sin)).astype(np.float64), 4, axis=1)
+        Vf = np.repeat(oracle.bf16_to_f32(vb).astype(np.float64), 4, axis=1)
+        qf = oracle.bf16_to_f32(q[qsl[b]:qsl[b + 1]]).astype(np.float64)
+        sc = np.einsum("thd,shd->hts", qf, Kr) * 128 ** -0.5
+        sc = np.where(np.arange(n)[None, None, :] <= np.arange(n0, n)[None, :, None], sc, -np.inf)
+        w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
+        want.append(np.einsum("hts,shd->thd", w, Vf))
+    want = np.concatenate(want)
+    base = None
+    for splits in (1, 2, 5, 24, 64):
+        say("prefill key splits", splits)
+        out = kh.prefill(*args, window=0, splits=splits)
+        o = torch.from_numpy(bits_of(out).view(np.int16)).view(torch.bfloat16).float().numpy()
+        d = np.abs(o - want)
+        say(f"splits {splits}: max-abs {d.max():.3e} mean-abs {d.mean():.3e}")
+        assert np.isfinite(o).all() and d.max() < MAX_ABS and d.mean() < MEAN_ABS, (splits, d.max(), d.mean())
+        if base is None:
+            base = o
+        dd = float(np.abs(o - base).max())
+        say(f"splits {splits}: max |split - unsplit| {dd:.3e}")
+        assert dd <= 4e-3, (splits, dd)
+    assert kh.prefill_splits(3, 48) > 1                                   # the default for these rows splits
+
+
 def test_prefill_quant_rows(hip, oracle):
     """Extend rows of a quantized layer: queries at positions n0 .. n-1 over the compressed history + new rows, against
     a float64 attention over the reference's assembled keys / values."""
