@@ -332,6 +332,20 @@ PF_R, PF_HIST, PF_NEW = 8, 16384, 2048                # prefill rows, history to
 MFMA_BF16_PEAK = 2500.0                               # TFLOP/s, MI355X dense bf16 / fp16
 
 
+def median_us(torch, fn, n, warmup=10):
+    """Median duration (us) of fn() over n calls, one HIP event pair per call on the current stream."""
+    for _ in range(warmup):
+        fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    ev[-1][1].synchronize()
+    t = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
+    return round(t[len(t) // 2], 1)
+
+
 def events_ms(torch, fn, n, warmup):
     """Average duration of fn() over n calls, one HIP event pair per call on the current stream, after warmup calls."""
     for _ in range(warmup):
@@ -384,12 +398,22 @@ def bench_prefill(torch, kh, dev, steps, warmup):
     pairs = PF_R * (PF_NEW * PF_HIST + PF_NEW * (PF_NEW + 1) // 2)      # (query, visible key) pairs, causal
     flop = pairs * 16 * 4 * 128
     tflops = flop / (ms_k * 1e-3) / 1e12
+    # a short extend chunk: row 0 alone with 16 new queries over its 16K history (the key-split path), HIP events
+    # around the attention call (its host preparation included), median of 50
+    import lfm3_kv800_amd.kv800 as kv
+    P1 = kv.Paged(qpool=P.qpool, boff=P.boff[:1].contiguous(), epool=P.epool, eoff=P.eoff[:1].contiguous(), ebs=P.ebs,
+                  e_hs=P.e_hs, e_ts=P.e_ts, e_v=P.e_v, sk=None, sv=None, skoff=None, svoff=None,
+                  N=P.N[:1].contiguous(), NQ=P.NQ[:1].contiguous(), nqmax=P.nqmax, win=0)
+    args1 = vc.prefill_quant_inputs(P1, q[:16], k[:16], v[:16], [0, 16], [PF_HIST], cos, sin)
+    short = median_us(torch, lambda: kh.prefill(*args1, window=0), 50)
     return {"workload": f"f3: prefill over compressed history, {PF_R} rows x {PF_NEW}-token chunk over "
                         f"{PF_HIST}-token histories ({(PF_HIST - 128) // 256} flushed sub-blocks each), "
                         "PagedStore geometry, N(0,1) q/K/V",
             "ms": round(ms, 4), "tok_s": round(T / (ms * 1e-3), 1), "attention_kernel_ms": round(ms_k, 4),
             "attention_flop": flop, "tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK, 4),
-            "bound": "mfma"}
+            "bound": "mfma",
+            "short_chunk_us": {"workload": f"1 row x 16 queries over a {PF_HIST}-token history (key-split path)",
+                               "attention_call_us": short}}
 
 
 FQ_B, FQ_T = 8, 4096                                  # training batch of the fake-quant measurement
