@@ -529,8 +529,10 @@ __global__ void __launch_bounds__(256) fake_quant_v_kernel(const float* __restri
 // dequantizer's fp32 chain, then bf16: dequantize_blocks, kv800.py:79-92), the others from the exact pages. RoPE is the
 // reference's fp32 kf c + rotate_half(kf) s over the 128-wide tables (cos32 | 1 | cos32 | 1), (sin32 | 0 | sin32 | 0),
 // each product and the sum rounded once, then bf16. Unreadable rows (offsets outside their pool, positions past the
-// rope table) are written as zeros. One workgroup per (64-position tile, row): a quarter of a sub-block, so that
-// the V chain (one wave per token at a time) runs at eight waves per SIMD on a long prefill.
+// rope table) are written as zeros. One workgroup per (hpos-position tile, row): hpos = 64, a quarter of a sub-block,
+// so that the V chain (one wave per token at a time) runs at eight waves per SIMD on a long prefill, or 16 or 4 when
+// 64 gives fewer than 1,024 workgroups (a single row). hpos divides 256, so a tile never straddles a sub-block; the
+// outputs do not depend on it.
 __device__ __forceinline__ void rope8(float (&a)[8], float (&b)[8], const uint16_t* cs, const uint16_t* sn, bool rope) {
   // a = dims d0 .. d0 + 7, b = dims d0 + 64 .. d0 + 71; rope: d0 < 32 (cs / sn the tables' entries d0 ..), else the
   // unrotated dims, for which the table holds cos 1, sin 0
@@ -547,18 +549,21 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float (&x)[8]) {
                     f2bf(x[6]) | (f2bf(x[7]) << 16));
 }
 
-constexpr int HPOS = 64;   // positions per history workgroup (a quarter of a sub-block)
+// positions per history workgroup: a quarter of a sub-block, cut by 4 (down to 4 positions, one token per wave)
+// while the rows give fewer than four workgroups per CU (a single long row: the V chain then runs at four waves per
+// SIMD instead of one)
+constexpr int HPOS = 64, HPOS_MIN = 4, HPOS_MIN_GROUPS = 1024;
 __global__ void __launch_bounds__(256) history_kernel(kv800_paged_t P, const uint16_t* __restrict__ cos_t,
                                                       const uint16_t* __restrict__ sin_t, int64_t rope_rows,
                                                       int64_t qpool_bytes, int64_t epool_elems,
                                                       const int64_t* __restrict__ out_off, uint16_t* __restrict__ kout,
-                                                      uint16_t* __restrict__ vout) {
+                                                      uint16_t* __restrict__ vout, int hpos) {
   __shared__ __align__(16) float xbuf[4][4 * VROW];   // per wave: one token's 4 dequantized V rows
   __shared__ float klo_s[512], ksc_s[512];
   const int r = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int n = P.N[r], p0 = blockIdx.x * HPOS;
+  const int n = P.N[r], p0 = blockIdx.x * hpos;
   if (p0 >= n) return;   // uniform over the workgroup
-  const int cnt = min(HPOS, n - p0);
+  const int cnt = min(hpos, n - p0);
   const int sb = p0 / BLK, to = p0 - sb * BLK;   // the positions' sub-block and the first one's token in it
   const int64_t ob = out_off[r] + p0;
   const bool rot = cos_t != nullptr;
@@ -771,10 +776,12 @@ int kv800_hip_history(const kv800_paged_t* P, int64_t R, int64_t max_n, const ui
   KV800_REQUIRE(P->boff_stride == 0 || (P->qpool && P->boff), "history: quantized rows need qpool and boff");
   KV800_REQUIRE(((uintptr_t)k_out % 16) == 0 && ((uintptr_t)v_out % 16) == 0, "history: outputs must be 16-byte aligned");
   KV800_REQUIRE(R <= 65535, "history: at most 65535 rows per call");
-  const int64_t tiles = (max_n + HPOS - 1) / HPOS;
+  int hpos = HPOS;
+  while (hpos > HPOS_MIN && (max_n + hpos - 1) / hpos * R < HPOS_MIN_GROUPS) hpos /= 4;
+  const int64_t tiles = (max_n + hpos - 1) / hpos;
   KV800_REQUIRE(tiles <= 0x7FFFFFFF, "history: max_n too large");
   hipLaunchKernelGGL(history_kernel, dim3((unsigned)tiles, (unsigned)R), dim3(256), 0, (hipStream_t)stream, *P, cos_t,
-                     sin_t, rope_rows, qpool_bytes, epool_elems, out_off, k_out, v_out);
+                     sin_t, rope_rows, qpool_bytes, epool_elems, out_off, k_out, v_out, hpos);
   return check_launch("history");
 }
 

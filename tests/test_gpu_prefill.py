@@ -55,12 +55,15 @@ def history_np(oracle, K, V, n):
     return kb, vb
 
 
-def test_history_bitexact(hip, oracle):
+# the launch takes 64 positions per workgroup, or 16 / 4 when that leaves fewer than 1,024 workgroups: the first set
+# runs at 4 (578 tiles x 5 rows), the single 16K row at 16 (1,025 tiles), the four rows at 64 (257 tiles x 4)
+@pytest.mark.parametrize("lens", [[50, 384, 640, 1000, 2311], [16400], [16400, 300, 9000, 16390]],
+                         ids=["tiles4", "tiles16", "tiles64"])
+def test_history_bitexact(hip, oracle, lens):
     rng = np.random.RandomState(5)
-    lens = [50, 384, 640, 1000, 2311]
     K = [oracle.randn_bf16(rng, (n, 4, 128), offset=rng.standard_normal((1, 4, 128))) for n in lens]
     V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
-    cos, sin = oracle.rope_tables(2400)
+    cos, sin = oracle.rope_tables(max(lens) + 16)
     case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, ebs=64, shuffle_seed=3)
     P = upload(case)
     say("history", lens)
