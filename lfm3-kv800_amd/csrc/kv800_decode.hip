@@ -18,7 +18,8 @@
 //                       grid: one per (row, KV head), its 4 waves taking turns over the chunks): sinks + exact
 //                       positions in 32-token chunks (loads one chunk ahead), QK and PV on bf16 MFMA; the fused
 //                       variant also merges the quantized splits of its rows.
-//   decode_merge_kernel one workgroup per row b: LSE merge + in-register FWHT (staged path).
+//   decode_merge_kernel one workgroup per (row, query head): LSE merge of the partials (shared out over 16 lane
+//                       groups, then combined), in-register FWHT, bf16 out.
 #include <math.h>
 
 #include <mutex>
@@ -1056,10 +1057,17 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 
 
 // ---------------------------------------------------------------- split merge
+// One workgroup per (row b, query head hq). The row's quantized partials are shared out over 16 lane groups (group k
+// takes partials k, k + 16, ..., up to four per memory round trip) and each group keeps a running (M, L, x) of its
+// share; wave 0 then combines the 16 states from LDS with the exact partial, applies the FWHT and writes the head's
+// 128 outputs. A row with many partials (a small batch cut into many slices) waits on one or two round trips instead
+// of one per four partials.
 __global__ void __launch_bounds__(256)
 decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
                     Sched S, uint16_t* __restrict__ out) {
-  const int b = blockIdx.x, tid = threadIdx.x, r = tid >> 4, l16 = tid & 15;
+  __shared__ float gm[16], gl[16];
+  __shared__ __align__(16) float gx[16][128];
+  const int b = blockIdx.x, hq = blockIdx.y, tid = threadIdx.x, k = tid >> 4, l16 = tid & 15;
   // row b's quantized partials: slots first .. first + ns - 1 (and slot extra); its exact partial: slot xs
   int64_t first = (int64_t)b * (ns + 1), xs = first + ns, extra = -1;
   if (S.groups > 0) {
@@ -1075,40 +1083,22 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     }
     xs = (int64_t)S.groups + S.B + b;
   }
-  const int64_t r0 = first * 16 + r;   // row of the first quantized partial; the next adds 16
-  // one pass with a running max: each batch of 4 partials (m, l, acc) is requested together, the exact partial with
-  // the first batch, so the row waits on one memory round trip per batch
-  const int64_t xrow = xs * 16 + r;
-  float M = mo[xrow];
-  const float xl = lo[xrow];
-  const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
-  const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
-  const float Mx = M;
-  float Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, xe[8];
-  const bool anyq = ns > 0 || extra >= 0;
-  if (extra >= 0) {   // the entering workgroup's partial, folded first
-    const int64_t row = extra * 16 + r;
-    const float me = mo[row], le = lo[row];
-    const float4 e0 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
-    const float4 e1 = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
-    M = fmaxf(M, me);
-    const float wgt = exp2f(me - M);
-    const float a[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-    Ls = wgt * le;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xq[e] = wgt * a[e];
-  }
-  for (int s0 = 0; s0 < ns; s0 += 4) {   // quantized splits
+  // partial j < nt: slot first + j for j < ns, the entering workgroup's slot for j = ns
+  const int nt = ns + (extra >= 0 ? 1 : 0);
+  auto row_of = [&](int j) { return ((j < ns) ? first + j : extra) * 16 + hq; };
+  float M = NEG_BIG, Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j0 = k; j0 < nt; j0 += 64) {   // group k: partials j0, j0 + 16, j0 + 32, j0 + 48
     float mv[4], lv[4];
     float4 a0[4], a1[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool in = s0 + k < ns;
-      const int64_t row = r0 + 16 * (in ? s0 + k : 0);
-      mv[k] = in ? mo[row] : NEG_BIG;
-      lv[k] = lo[row];
-      a0[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
-      a1[k] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
+    for (int i = 0; i < 4; ++i) {
+      const int j = j0 + 16 * i;
+      const bool in = j < nt;
+      const int64_t row = row_of(in ? j : j0);   // past the end: a repeat of partial j0, weighted 0 below
+      mv[i] = in ? mo[row] : NEG_BIG;
+      lv[i] = lo[row];
+      a0[i] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16);
+      a1[i] = *reinterpret_cast<const float4*>(ao + row * 128 + 8 * l16 + 4);
     }
     const float Mn = fmaxf(fmaxf(M, fmaxf(mv[0], mv[1])), fmaxf(mv[2], mv[3]));
     const float al = exp2f(M - Mn);   // rescales what the earlier batches added
@@ -1117,14 +1107,41 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) xq[e] *= al;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float wgt = exp2f(mv[k] - M);   // 0 for the padding entries
-      const float a[8] = {a0[k].x, a0[k].y, a0[k].z, a0[k].w, a1[k].x, a1[k].y, a1[k].z, a1[k].w};
-      Ls += wgt * lv[k];
+    for (int i = 0; i < 4; ++i) {
+      const float wgt = exp2f(mv[i] - M);   // 0 for the padding entries
+      const float a[8] = {a0[i].x, a0[i].y, a0[i].z, a0[i].w, a1[i].x, a1[i].y, a1[i].z, a1[i].w};
+      Ls += wgt * lv[i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
     }
   }
+  if (l16 == 0) { gm[k] = M; gl[k] = Ls; }
+  *reinterpret_cast<float4*>(&gx[k][8 * l16]) = make_float4(xq[0], xq[1], xq[2], xq[3]);
+  *reinterpret_cast<float4*>(&gx[k][8 * l16 + 4]) = make_float4(xq[4], xq[5], xq[6], xq[7]);
+  __syncthreads();
+  if (tid >= 64) return;   // wave 0 finishes (its four lane groups alike; group 0 writes)
+  // the exact partial and the 16 group states, relative to the largest max
+  const int64_t xrow = xs * 16 + hq;
+  const float Mx = mo[xrow], xl = lo[xrow];
+  const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
+  const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
+  M = Mx;
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) M = fmaxf(M, gm[kk]);
+  Ls = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) xq[e] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    const float wgt = exp2f(gm[kk] - M);   // 0 for groups without partials (their state is zero anyway)
+    Ls += wgt * gl[kk];
+    const float4 c0 = *reinterpret_cast<const float4*>(&gx[kk][8 * l16]);
+    const float4 c1 = *reinterpret_cast<const float4*>(&gx[kk][8 * l16 + 4]);
+    const float a[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
+  }
+  float xe[8];
   {   // exact partial
     const float wgt = exp2f(Mx - M);
     Ls += wgt * xl;
@@ -1132,18 +1149,19 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) xe[e] = wgt * a[e];
   }
+  const bool anyq = nt > 0;
   if (anyq) {   // y = H x, d = 8 l16 + e: three in-lane stages, four across the 16-lane group
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
+    for (int kk = 0; kk < 3; ++kk)
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (!(e & (1 << k))) {
-          const float a = xq[e], c = xq[e | (1 << k)];
-          xq[e] = a + c; xq[e | (1 << k)] = a - c;
+        if (!(e & (1 << kk))) {
+          const float a = xq[e], c = xq[e | (1 << kk)];
+          xq[e] = a + c; xq[e | (1 << kk)] = a - c;
         }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int msk = 1 << k;
+    for (int kk = 0; kk < 4; ++kk) {
+      const int msk = 1 << kk;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float pv = __shfl_xor(xq[e], msk);
@@ -1161,7 +1179,8 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     y1 = Ls > 0.f ? y1 / Ls : 0.f;
     o[e >> 1] = f2bf(y0) | (f2bf(y1) << 16);
   }
-  *reinterpret_cast<uint4*>(out + ((int64_t)b * 16 + r) * 128 + 8 * l16) = make_uint4(o[0], o[1], o[2], o[3]);
+  if (k == 0)
+    *reinterpret_cast<uint4*>(out + ((int64_t)b * 16 + hq) * 128 + 8 * l16) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -1297,7 +1316,7 @@ int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, in
   if (B == 0) return KV800_OK;
   KV800_REQUIRE(mo && lo && ao && out, "decode_merge: null pointer");
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns,
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B, 16), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns,
                      Sched{nullptr, 0, (int)B, 0}, out);
   return check_launch("decode_merge");
 }
@@ -1427,7 +1446,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
                          scale, &X, S, stream)) != KV800_OK)
     return rc;
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, S,
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B, 16), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, S,
                      out);
   return check_launch("decode_merge");
 }
