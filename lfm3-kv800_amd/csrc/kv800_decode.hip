@@ -1359,14 +1359,15 @@ int64_t kv800_hip_decode_workspace_balanced(int64_t B, int64_t groups, int64_t r
 
 int kv800_hip_plan_balanced(int64_t B, int64_t nqmax, int64_t* groups) {
   KV800_REQUIRE(B >= 0 && nqmax >= 0 && groups, "plan_balanced: bad arguments");
-  // about BAL_CHUNK sub-blocks per workgroup at the batch's largest size B * nqmax (ragged batches hold fewer
-  // sub-blocks, and each workgroup then takes proportionally fewer); beyond one round of resident workgroups, whole
-  // rounds, at most BAL_ROUNDS (one: longer spans in a single round measured faster than two or three rounds of
-  // shorter ones at 256-400 rows of up to 32K tokens). Small batches are latency chains: at 32K tokens per row,
-  // B = 1 / 8 / 16 / 32 take 89 / 91 / 91 / 93 us at 16 sub-blocks per workgroup and 41 / 45 / 58 / 77 us at 4 (2 per
-  // workgroup: 42 / 58 / 58 / 77, the merge then reading twice the partials); from 64 rows on one round holds more
-  // than 4 per workgroup and the plan is the resident round either way.
-  const int64_t want = (B * nqmax + BAL_CHUNK - 1) / BAL_CHUNK, res = resident_groups();
+  // about BAL_CHUNK sub-blocks per workgroup at the batch's largest size T = B * nqmax (ragged batches hold fewer
+  // sub-blocks, and each workgroup then takes proportionally fewer), or 1 while T fills at most half a round of
+  // resident workgroups and 2 while T / 2 fills at most one; beyond one round, whole rounds, at most BAL_ROUNDS (one:
+  // longer spans in a single round measured faster than two or three rounds of shorter ones at 256-400 rows of up to
+  // 32K tokens). Small batches are latency chains: at 32K tokens per row, B = 1 / 2 / 4 / 8 rows take
+  // 19.2 / 23.0 / 30.0 / 34.9 us at 1 sub-block per workgroup, 23.2 / 23.2 / 25.7 / 35.0 at 2, 32.4 / 32.8 / 32.8 /
+  // 34.6 at 4 (89-91 us at 16); from 16 rows on one round holds 4 or more per workgroup.
+  const int64_t T = B * nqmax, res = resident_groups();
+  const int64_t want = T <= res / 2 ? T : (T + 1) / 2 <= res ? (T + 1) / 2 : (T + BAL_CHUNK - 1) / BAL_CHUNK;
   *groups = want < 1 ? 1 : want <= res ? want : min((want + res - 1) / res, BAL_ROUNDS) * res;
   return KV800_OK;
 }
