@@ -158,7 +158,8 @@ int kv800_hip_rope_rows(const uint16_t* k, const int64_t* pos, int64_t S, const 
 /* Prefill / extend attention of R ragged rows, replacing the reference's prefill attention (vllm_attn.py:168-211 with
  * the masks of 176-184): row r has queries q[qsl[r], qsl[r+1]) ((T, 16, 128) bf16, post-RoPE) at positions
  * qpos0[r] + 0, 1, ... and keys / values K, V[ksl[r], ksl[r+1]) ((S, 4, 128) bf16, rotated as the layer stores them for
- * attention) at positions kp (int32, ascending within a row); query head h reads KV head h / 4. A key is kept when
+ * attention) at positions kp (int32, ascending within a row; kp = NULL: key j of a row is at position j, the order in
+ * which quantized layers assemble history and new rows); query head h reads KV head h / 4. A key is kept when
  * kp <= the query's position and, with window > 0, kp > position - window or kp < nsink (nsink 4 for window + sinks
  * layers, 0 for sliding layers; window 0 for quantized layers). Scale 128^-0.5, fp32 scores and softmax, bf16
  * probabilities times bf16 V with fp32 accumulation, bf16 out (T, 16, 128). tile_off (R + 1, int64) is the prefix sum of

@@ -7,7 +7,8 @@
 //                     rounded to bf16 -- the same value, bit for bit, dims without a frequency included.
 //   prefill_kernel    flash attention of R ragged rows. Row i has queries q[qsl[i], qsl[i+1]) (T, 16 heads, 128) at the
 //                     consecutive positions qpos0[i], qpos0[i] + 1, ... and keys / values K, V[ksl[i], ksl[i+1])
-//                     (S, 4 KV heads, 128) at the ascending positions kp; query head h reads KV head h / 4. A key is
+//                     (S, 4 KV heads, 128) at the ascending positions kp (kp = null: key j of a row at position
+//                     j, as quantized layers assemble them); query head h reads KV head h / 4. A key is
 //                     kept when kp <= query position and, with window > 0, kp > query position - window or kp < nsink
 //                     (the quantized, window + sinks and sliding masks of vllm_attn.py:168-184). fp32 scores and
 //                     online softmax, bf16 probabilities for the P.V product, fp32 accumulation, bf16 out.
@@ -106,10 +107,11 @@ constexpr float PLAZY = 8.f;   // log2 units a query's running max may lag its s
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int RSRC_WORD3 = 0x00020000;   // raw (untyped, unswizzled) buffer access on gfx9-family parts
 
-// first index in [0, n) with a[index] > x (a ascending), n if none: a 64-way search by the whole wave (lane l probes
-// lo + l step; the count of probes <= x, from a ballot, narrows [lo, hi) 64-fold), so n = 16K entries take three
-// dependent loads instead of fourteen. All 64 lanes must be active; the result is the same in every lane.
+// first index in [0, n) with a[index] > x (a ascending; a = null: a[i] = i), n if none: a 64-way search by the whole
+// wave (lane l probes lo + l step; the count of probes <= x, from a ballot, narrows [lo, hi) 64-fold), so n = 16K
+// entries take three dependent loads instead of fourteen. All 64 lanes must be active; the result is the same in every lane.
 __device__ __forceinline__ int64_t upper(const int32_t* a, int64_t n, int64_t x) {
+  if (!a) return x < 0 ? 0 : (x + 1 < n ? x + 1 : n);   // positions = indices 0 .. n - 1
   const int lane = threadIdx.x & 63;
   int64_t lo = 0, hi = n;   // the answer lies in [lo, hi]
   while (hi > lo) {
@@ -171,7 +173,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
   const int nq = (int)min((int64_t)PQ, qsl[row + 1] - q0);
   const int64_t p0 = qpos0[row] + (q0 - qsl[row]);
   const int64_t ks = ksl[row], S = ksl[row + 1] - ks;
-  const int32_t* kpr = kp + ks;
+  const int32_t* kpr = kp ? kp + ks : nullptr;   // null: key j of the row at position j
 
   // ---- key ranges: [0, sink_end) and [kbeg, kend)
   const int64_t kend = upper(kpr, S, p0 + nq - 1);
@@ -227,7 +229,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
       sk[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
       sv[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
     }
-    if (tid < PK) skp = (k0 + tid < r1) ? kpr[k0 + tid] : 0x7FFFFFFF;
+    if (tid < PK) skp = (k0 + tid < r1) ? (kpr ? kpr[k0 + tid] : (int32_t)(k0 + tid)) : 0x7FFFFFFF;
   };
   auto store = [&](PTile& T) {
 #pragma unroll
@@ -434,7 +436,7 @@ int kv800_hip_prefill_split(const uint16_t* q, const int64_t* qsl, const int64_t
                             float* part, int64_t part_floats, uint16_t* out, void* stream) {
   KV800_REQUIRE(R >= 0 && ntiles >= 0 && T >= 0, "prefill: negative R, tile count or query count");
   if (R == 0 || ntiles == 0) return KV800_OK;
-  KV800_REQUIRE(q && qsl && qpos0 && K && V && kp && ksl && tile_off && out, "prefill: null pointer");
+  KV800_REQUIRE(q && qsl && qpos0 && K && V && ksl && tile_off && out, "prefill: null pointer");
   KV800_REQUIRE(((uintptr_t)q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 &&
                 ((uintptr_t)out % 8) == 0, "prefill: q, K, V need 16-byte and out 8-byte alignment");
   KV800_REQUIRE(window >= 0 && nsink >= 0, "prefill: negative window or sink count");

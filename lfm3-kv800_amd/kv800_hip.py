@@ -398,7 +398,8 @@ def prefill_splits(tiles, max_key_tiles):
 def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0, splits=None):
     """Prefill attention of ragged rows (kv800_hip_prefill_split): row r's queries q[qsl[r]:qsl[r+1]] ((T, 16, 128)
     bf16) at positions qpos0[r], qpos0[r] + 1, ... over keys / values K, V[ksl[r]:ksl[r+1]] ((S, 4, 128) bf16) at
-    positions kp (S,) (ascending within a row). qsl / ksl / qpos0: host sequences (R + 1, R + 1, R). Mask: kp <= query
+    positions kp (S,) (ascending within a row; None: key j of a row at position j). qsl / ksl / qpos0: host sequences
+    (R + 1, R + 1, R). Mask: kp <= query
     position, and with window > 0 also kp > position - window or kp < nsink. splits: key splits per (query tile, KV
     head) (default prefill_splits: few query tiles over long rows are split and merged). Returns (T, 16, 128) bf16."""
     L = ops()
@@ -415,9 +416,10 @@ def prefill(q, qsl, qpos0, K, V, kp, ksl, window=0, nsink=0, splits=None):
         raise ValueError(f"K / V must be (ksl[-1], 4, 128), got {tuple(K.shape)}, {tuple(V.shape)}")
     if any(b < a for a, b in zip(qsl, qsl[1:])) or any(b < a for a, b in zip(ksl, ksl[1:])):
         raise ValueError("qsl / ksl must be non-decreasing")
-    kp = host_to_device(kp, torch.int32, dev).contiguous()
-    if kp.shape != (K.shape[0],):
-        raise ValueError("kp must be (S,)")
+    if kp is not None:
+        kp = host_to_device(kp, torch.int32, dev).contiguous()
+        if kp.shape != (K.shape[0],):
+            raise ValueError("kp must be (S,)")
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=dev)
     tiles = [0]
     for a, b in zip(qsl, qsl[1:]):

@@ -393,24 +393,26 @@ def prefill_quant_rows(P, q, k, v, qsl, prev, cos_t, sin_t):
 
 def prefill_quant_inputs(P, q, k, v, qsl, prev, cos_t, sin_t):
     """The arguments of prefill_quant_rows' attention launch, (q, qsl, prev, K, V, key positions, key row starts):
-    the rows' keys (history, then new rows) and values assembled as prefill_quant_rows describes."""
+    the rows' keys (history, then new rows) and values assembled as prefill_quant_rows describes. The key positions
+    are None: key j of a row is at position j."""
     dev = q.device
     prev, qsl = [int(x) for x in prev], [int(x) for x in qsl]
-    R = len(prev)
     new = [b - a for a, b in zip(qsl, qsl[1:])]
+    T = qsl[-1]
     # key order: row 0's history, row 0's new rows, row 1's history, ...; the history launch writes each row's history
     # in place, the new rows (rotated) follow by one index_copy_ each for K and V
     ksl = np.concatenate(([0], np.cumsum(np.asarray(prev) + np.asarray(new)))).astype(np.int64)
     Kc = torch.empty(int(ksl[-1]), 4, 128, dtype=torch.bfloat16, device=dev)
     Vc = torch.empty_like(Kc)
     kv800_hip.history(P, prev, cos_t, sin_t, out=(Kc, Vc), offs=ksl[:-1])
-    pos_new = kv800_hip.host_to_device(_ranges(prev, new), torch.int64, dev)
-    Kn = kv800_hip.rope_rows(k[:qsl[-1]].to(torch.bfloat16), pos_new, cos_t, sin_t)
-    idx = kv800_hip.host_to_device(_ranges(ksl[:-1] + np.asarray(prev, np.int64), new), torch.int64, dev)
+    # the new rows' positions and their key indices, in one copy
+    pi = kv800_hip.host_to_device(np.concatenate((_ranges(prev, new), _ranges(ksl[:-1] + np.asarray(prev, np.int64),
+                                                                              new))), torch.int64, dev)
+    pos_new, idx = pi[:T], pi[T:]
+    Kn = kv800_hip.rope_rows(k[:T].to(torch.bfloat16), pos_new, cos_t, sin_t)
     Kc.index_copy_(0, idx, Kn)
-    Vc.index_copy_(0, idx, v[:qsl[-1]].to(torch.bfloat16))
-    kp = torch.from_numpy(_ranges([0] * R, np.asarray(prev) + np.asarray(new)).astype(np.int32))
-    return q, qsl, prev, Kc, Vc, kp, ksl
+    Vc.index_copy_(0, idx, v[:T].to(torch.bfloat16))
+    return q, qsl, prev, Kc, Vc, None, ksl   # key positions: the index within the row (kp = None)
 
 
 def prefill_window_rows(P, q, k, v, qsl, prev, cos_t, sin_t):

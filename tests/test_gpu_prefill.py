@@ -159,6 +159,12 @@ def test_prefill_key_splits(hip, oracle):
         w = np.exp(sc - sc.max(-1, keepdims=True)); w /= w.sum(-1, keepdims=True)
         want.append(np.einsum("hts,shd->thd", w, Vf))
     want = np.concatenate(want)
+    # the assembled rows carry no position array (key j of a row is at position j): the same output, bit for bit, as
+    # the explicit positions
+    kp = torch.from_numpy(np.concatenate([np.arange(n) for n in lens]).astype(np.int32))
+    assert args[5] is None
+    explicit = kh.prefill(*args[:5], kp, args[6], window=0, splits=1)
+    assert torch.equal(explicit.view(torch.int16), kh.prefill(*args, window=0, splits=1).view(torch.int16))
     base = None
     for splits in (1, 2, 5, 24, 64):
         say("prefill key splits", splits)
