@@ -352,6 +352,38 @@ def test_decode_stages_and_merge(hip, oracle):
     assert torch.equal(fused, out)
 
 
+def test_decode_merge_many_partials(hip, oracle):
+    """The merge with more partials per row than its 16 lane groups take in one memory round trip (the fixed grid at
+    one sub-block per split: 77 and 33 quantized partials), against the oracle's combine of the same partials; then
+    single long rows through the balanced plan, which cuts a batch that fills under half a resident round into one
+    sub-block per workgroup (a 32K row: 127 slices)."""
+    rng = np.random.RandomState(43)
+    lens = [20000, 8600]
+    K = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    V = [oracle.randn_bf16(rng, (n, 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (2, 16, 128))
+    cos, sin = oracle.rope_tables(max(lens) + 1)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, shuffle_seed=43)
+    say("decode merge of many partials", lens)
+    P = upload(case)
+    out, MO, LO, AO, ns = hip.decode_parts(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin), spb=1)
+    assert ns == 77
+    merged = oracle.combine(MO.cpu().numpy(), LO.cpu().numpy(), AO.cpu().numpy(), ns)
+    close(bits_of(out), merged, "HIP merge of 77 partials vs oracle combine")
+    close(bits_of(out), oracle.decode_f32(case, q, cos, sin), "77 splits vs oracle")
+    res = hip.plan_balanced(64, 127)                     # one round of resident workgroups
+    assert hip.plan_balanced(1, 127) == 127 and hip.plan_balanced(2, 127) == 254
+    assert hip.plan_balanced(4, 127) == (508 + 1) // 2 and hip.plan_balanced(16, 127) == min(res, 508)
+    n = 32768
+    K1 = oracle.randn_bf16(rng, (1, n, 4, 128)); V1 = oracle.randn_bf16(rng, (1, n, 4, 128))
+    q1 = oracle.randn_bf16(rng, (1, 16, 128))
+    cos, sin = oracle.rope_tables(n + 1)
+    case1 = oracle.build_paged(lambda b, p0, p1: (K1[b, p0:p1], V1[b, p0:p1]), [n], ebs=128, shuffle_seed=44)
+    say("decode one 32K row, plan", hip.plan_balanced(1, int(case1.nqmax)))
+    out1 = hip.decode(upload(case1), to_dev_bf16(q1), to_dev_bf16(cos), to_dev_bf16(sin))
+    close(bits_of(out1), oracle.decode_f32(case1, q1, cos, sin), "one 32K row, one sub-block per workgroup")
+
+
 def test_decode_full_size_all_rows(hip, oracle):
     """config C3 at full size (64 x 32,768, permuted tables): cache built on the GPU by the HIP quantizer,
     decoded by the HIP kernels; every row is decoded again by the oracle from the downloaded pages (the strict bar), and
