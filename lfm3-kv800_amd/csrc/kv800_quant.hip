@@ -7,9 +7,10 @@
 //     code = clamp(rne((x - f32(lo8)) / max(f32(sc8), 1e-8)), 0, 3) with IEEE division;
 //   * V: y = f32(v) @ H per (token, head) as the sequential fma chain over k = 0..127 that torch-CPU's sgemm
 //     evaluates for this shape, then per (token, 2-head group) lo8 / sc8 and 1-bit codes the same way.
-// One workgroup (8 waves) quantizes one 256-token sub-block of all 4 KV heads; the input is gathered straight from
-// the exact pages (paged flush) or from dense (M, 256, 4, 128) tensors, and the 51,200-byte result is written
-// through the quant block table, so a flush is one launch with no host loop and no intermediate copies.
+// Workgroups of 8 waves quantize one 256-token sub-block: its K per head, its V per token range; the input is
+// gathered straight from the exact pages (paged flush) or from dense (M, 256, 4, 128) tensors, and the 51,200-byte
+// result is written through the quant block table, so a flush is one launch with no host loop and no intermediate
+// copies.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -96,7 +97,9 @@ struct QuantLds {                  // K path: per-wave min / max partials, then 
   float col_den[512];
 };
 
-// K codes and scales of one sub-block: per (head, channel) min / max over its 256 tokens (8 waves x 32 tokens).
+// K codes and scales of one sub-block, all 4 heads in one workgroup: per (head, channel) min / max over its 256
+// tokens (8 waves x 32 tokens). The latency flush uses it (one workgroup per sub-block's K); the throughput grids
+// take the per-head form below, which reads each row once.
 template <typename Src, int KG = 4>
 __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -175,6 +178,104 @@ __device__ void quantize_k(const Src& src, uint8_t* __restrict__ out, char* lds)
           *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + h) * 32 + 8 * q) = make_uint2(d0, d1);
         }
       }
+    }
+  }
+}
+
+// K codes and scales of one head hh of one sub-block, its 256 token rows read once: lane (g, c) of wave w holds the
+// 8 channels 8 c .. 8 c + 7 of the tokens 32 i + 4 w + g (i = 0..7) in registers through both passes (min / max, then
+// codes), so each row is fetched from memory once (the all-heads pass above reads its rows twice). Min / max across
+// the 4 token rows of a wave by permlane swaps, across the 8 waves through LDS.
+struct QuantLds1 {
+  float red_min[QW][128];
+  float red_max[QW][128];
+  float col_lo[128];
+  float col_den[128];
+};
+__device__ __forceinline__ float min4rows(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max4rows(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <typename Src>
+__device__ void quantize_k1(const Src& src, uint8_t* __restrict__ out, char* lds, int hh) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15, c0 = 8 * c16;
+  QuantLds1& S = *reinterpret_cast<QuantLds1*>(lds);
+  constexpr int NT = BLK / 32;   // tokens per lane
+  uint4 kx[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) kx[i] = *reinterpret_cast<const uint4*>(src.krow(32 * i + 4 * w + g, hh) + c0);
+  {
+    float mn[8], mx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { mn[e] = INFINITY; mx[e] = -INFINITY; }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      __builtin_amdgcn_sched_barrier(0);   // one token row at a time
+      const uint32_t wd[4] = {kx[i].x, kx[i].y, kx[i].z, kx[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+        mn[e] = fminf(mn[e], x);
+        mx[e] = fmaxf(mx[e], x);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __builtin_amdgcn_sched_barrier(0);
+      mn[e] = min4rows(mn[e]);
+      mx[e] = max4rows(mx[e]);
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { S.red_min[w][c0 + e] = mn[e]; S.red_max[w][c0 + e] = mx[e]; }
+    }
+  }
+  __syncthreads();
+  if (tid < 128) {
+    float lo = S.red_min[0][tid], hi = S.red_max[0][tid];
+#pragma unroll
+    for (int ww = 1; ww < QW; ++ww) { lo = fminf(lo, S.red_min[ww][tid]); hi = fmaxf(hi, S.red_max[ww][tid]); }
+    const uint32_t lo8 = f8e(lo);
+    const uint32_t sc8 = f8e(clamp_min_1e8(__fdiv_rn(__fsub_rn(hi, lo), 3.0f)));
+    out[KLO_O + hh * 128 + tid] = (uint8_t)lo8;
+    out[KSC_O + hh * 128 + tid] = (uint8_t)sc8;
+    S.col_lo[tid] = f8d(lo8);
+    S.col_den[tid] = clamp_min_1e8(f8d(sc8));
+  }
+  __syncthreads();
+  // the rows stay packed across the passes: their unpacked floats are formed again here, not kept from the first
+  // pass (64 registers instead of 32)
+#pragma unroll
+  for (int i = 0; i < NT; ++i) asm volatile("" : "+v"(kx[i].x), "+v"(kx[i].y), "+v"(kx[i].z), "+v"(kx[i].w));
+  float lof[8], den[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { lof[e] = S.col_lo[c0 + e]; den[e] = S.col_den[c0 + e]; }
+  const int p = c16 >> 2, q = c16 & 3;   // plane of these 8 channels, byte quarter 8q .. 8q + 7
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    __builtin_amdgcn_sched_barrier(0);   // one token row at a time
+    const uint32_t wd[4] = {kx[i].x, kx[i].y, kx[i].z, kx[i].w};
+    uint32_t d0 = 0, d1 = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (e & 1) ? bf2f_hi(wd[e >> 1]) : bf2f_lo(wd[e >> 1]);
+      const uint32_t code = kcode(__fsub_rn(x, lof[e]), den[e]) << (2 * p);
+      if (e < 4) d0 |= code << (8 * e); else d1 |= code << (8 * (e - 4));
+    }
+    // the 4 planes of these bytes sit in the lanes 4, 8, 12 apart within the 16-lane row
+    d0 |= row_ror(d0, 4); d1 |= row_ror(d1, 4);
+    d0 |= row_ror(d0, 8); d1 |= row_ror(d1, 8);
+    if (p == 0) {
+      const int t = 32 * i + 4 * w + g;
+      *reinterpret_cast<uint2*>(out + KC_O + (t * 4 + hh) * 32 + 8 * q) = make_uint2(d0, d1);
     }
   }
 }
@@ -324,15 +425,18 @@ __device__ void quantize_v(const Src& src, uint8_t* __restrict__ out, int t0, ch
   }
 }
 
-// A quantize grid holds, per sub-block, one K workgroup (all 256 tokens per (head, channel)) followed in the grid by
-// VSPLIT V workgroups (V is independent per token). Both passes fit 64 VGPRs and 39 KB of LDS, so 8 waves per SIMD run
-// and the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup i < units is the K pass of unit i;
-// i >= units is the V pass of unit (i - units) / VSPLIT, token range (i - units) % VSPLIT.
+// A quantize grid holds, per sub-block, 4 K workgroups (one per head: all 256 tokens per channel, each row read once)
+// followed in the grid by VSPLIT V workgroups (V is independent per token). Both passes fit 72 VGPRs and 39 KB of LDS,
+// so 7 waves per SIMD run and the K workgroups' memory latency overlaps the V workgroups' fma chains. Workgroup
+// i < 4 units is the K pass of unit i / 4, head i % 4; i >= 4 units is the V pass of unit (i - 4 units) / VSPLIT, token
+// range (i - 4 units) % VSPLIT.
 constexpr int QLDS_BYTES = (int)sizeof(QuantLds) > VLDS_BYTES ? (int)sizeof(QuantLds) : VLDS_BYTES;
+static_assert(sizeof(QuantLds1) <= (size_t)QLDS_BYTES, "per-head K pass LDS");
 
+// kpass: part = the head of the per-head K pass; else the V token range
 template <typename Src>
 __device__ __forceinline__ void quantize_part(const Src& src, uint8_t* __restrict__ out, char* lds, bool kpass, int part) {
-  if (kpass) quantize_k(src, out, lds);
+  if (kpass) quantize_k1(src, out, lds, part);
   else quantize_v<VTPW>(src, out, part * VTOK, lds);
 }
 
@@ -341,9 +445,9 @@ __global__ void __launch_bounds__(QTHREADS) quantize_dense_kernel(const uint16_t
                                                                    uint8_t* __restrict__ out, int64_t M) {
   __shared__ __align__(16) char lds[QLDS_BYTES];
   const int64_t i = blockIdx.x;
-  const bool kpass = i < M;
-  const int64_t m = kpass ? i : (i - M) / VSPLIT;
-  quantize_part(DenseSrc{k, v, m}, out + m * SUB, lds, kpass, kpass ? 0 : (int)((i - M) % VSPLIT));
+  const bool kpass = i < 4 * M;
+  const int64_t m = kpass ? i / 4 : (i - 4 * M) / VSPLIT;
+  quantize_part(DenseSrc{k, v, m}, out + m * SUB, lds, kpass, kpass ? (int)(i % 4) : (int)((i - 4 * M) % VSPLIT));
 }
 
 __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restrict__ ep, const int64_t* __restrict__ eoff,
@@ -355,8 +459,8 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
   __shared__ __align__(16) char lds[QLDS_BYTES];
   __shared__ int64_t rowtab[BLK];
   const int64_t units = R * max_new, i = blockIdx.x;
-  const bool kpass = i < units;
-  const int64_t unit = kpass ? i : (i - units) / VSPLIT;
+  const bool kpass = i < 4 * units;
+  const int64_t unit = kpass ? i / 4 : (i - 4 * units) / VSPLIT;
   const int64_t r = unit / max_new;
   const int j = nq_prev[r] + (int)(unit % max_new);
   if (j >= nq_new[r]) return;   // uniform over the workgroup
@@ -364,7 +468,7 @@ __global__ void __launch_bounds__(QTHREADS) flush_kernel(const uint16_t* __restr
   uint8_t* dst = qpool + qbt[r * qs + tok0 / bsq] * qs0 + ((tok0 % bsq) / BLK) * SUB;
   PagedSrc src{ep, eoff + r * es, ebs, e_hs, e_ts, e_v, tok0};
   src.prepare(rowtab);
-  quantize_part(src, dst, lds, kpass, kpass ? 0 : (int)((i - units) % VSPLIT));
+  quantize_part(src, dst, lds, kpass, kpass ? (int)(i % 4) : (int)((i - 4 * units) % VSPLIT));
 }
 
 // ---------------------------------------------------------------- latency-oriented flush (decode steps)
@@ -685,10 +789,10 @@ int kv800_hip_quantize_blocks(const uint16_t* k, const uint16_t* v, int64_t M, u
   KV800_REQUIRE(M >= 0, "quantize_blocks: M = %lld < 0", (long long)M);
   if (M == 0) return KV800_OK;
   KV800_REQUIRE(k && v && out, "quantize_blocks: null pointer");
-  KV800_REQUIRE(M * (1 + VSPLIT) <= 0x7FFFFFFF, "quantize_blocks: M = %lld too large", (long long)M);
+  KV800_REQUIRE(M * (4 + VSPLIT) <= 0x7FFFFFFF, "quantize_blocks: M = %lld too large", (long long)M);
   KV800_REQUIRE(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && ((uintptr_t)out % 8) == 0,
                 "quantize_blocks: k / v must be 16-byte aligned and out 8-byte aligned");
-  hipLaunchKernelGGL(quantize_dense_kernel, dim3((unsigned)(M * (1 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream, k,
+  hipLaunchKernelGGL(quantize_dense_kernel, dim3((unsigned)(M * (4 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream, k,
                      v, out, M);
   return check_launch("quantize_blocks");
 }
@@ -704,8 +808,8 @@ int kv800_hip_flush(const uint16_t* epool, const int64_t* eoff, int64_t eoff_str
   KV800_REQUIRE(ebs > 0 && bsq > 0 && bsq % BLK == 0, "flush: ebs must be > 0 and bsq a positive multiple of 256");
   KV800_REQUIRE(e_hs % 8 == 0 && e_ts % 8 == 0 && e_v % 8 == 0 && ((uintptr_t)epool % 16) == 0,
                 "flush: exact-pool strides must be multiples of 8 elements and the pool 16-byte aligned");
-  KV800_REQUIRE(R * max_new * (1 + VSPLIT) <= 0x7FFFFFFF, "flush: grid too large");
-  hipLaunchKernelGGL(flush_kernel, dim3((unsigned)(R * max_new * (1 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream,
+  KV800_REQUIRE(R * max_new * (4 + VSPLIT) <= 0x7FFFFFFF, "flush: grid too large");
+  hipLaunchKernelGGL(flush_kernel, dim3((unsigned)(R * max_new * (4 + VSPLIT))), dim3(QTHREADS), 0, (hipStream_t)stream,
                      epool, eoff, eoff_stride, ebs, e_hs, e_ts, e_v, qpool, qbt, qbt_stride, bsq, qs0, nq_prev, nq_new, R,
                      (int)max_new);
   return check_launch("flush");
