@@ -18,8 +18,9 @@
 //                       grid: one per (row, KV head), its 4 waves taking turns over the chunks): sinks + exact
 //                       positions in 32-token chunks (loads one chunk ahead), QK and PV on bf16 MFMA; the fused
 //                       variant also merges the quantized splits of its rows.
-//   decode_merge_kernel one workgroup per (row, query head): LSE merge of the partials (shared out over 16 lane
-//                       groups, then combined), in-register FWHT, bf16 out.
+//   decode_merge_kernel 1, 4 or 16 query heads of a row per workgroup: LSE merge of the partials (a row's many
+//                       partials shared out over up to 16 lane groups per head, then combined), in-register FWHT,
+//                       bf16 out.
 #include <math.h>
 
 #include <mutex>
@@ -1057,17 +1058,21 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
 
 
 // ---------------------------------------------------------------- split merge
-// One workgroup per (row b, query head hq). The row's quantized partials are shared out over 16 lane groups (group k
-// takes partials k, k + 16, ..., up to four per memory round trip) and each group keeps a running (M, L, x) of its
-// share; wave 0 then combines the 16 states from LDS with the exact partial, applies the FWHT and writes the head's
-// 128 outputs. A row with many partials (a small batch cut into many slices) waits on one or two round trips instead
-// of one per four partials.
+// HPW query heads of row b per workgroup (grid (B, 16 / HPW)), SG = 16 / HPW lane groups of 16 per head: the row's
+// quantized partials are shared out over a head's SG groups (group k takes partials k, k + SG, ..., four per memory
+// round trip), each keeping a running (M, L, x) of its share; with SG > 1 the first group of each head combines the
+// states from LDS. Then the exact partial, the FWHT across the group's 16 lanes and the head's 128 bf16 outputs. Many
+// partials per row (a small batch cut into many slices) take SG = 16, so a row waits on one or two round trips
+// instead of one per four partials; large batches with a few partials per row take HPW = 16, one workgroup per row.
+template <int HPW>
 __global__ void __launch_bounds__(256)
 decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, const float* __restrict__ ao, int ns,
                     Sched S, uint16_t* __restrict__ out) {
-  __shared__ float gm[16], gl[16];
-  __shared__ __align__(16) float gx[16][128];
-  const int b = blockIdx.x, hq = blockIdx.y, tid = threadIdx.x, k = tid >> 4, l16 = tid & 15;
+  constexpr int SG = 16 / HPW;
+  __shared__ float gm[SG > 1 ? 16 : 1], gl[SG > 1 ? 16 : 1];
+  __shared__ __align__(16) float gx[SG > 1 ? 16 : 1][128];
+  const int b = blockIdx.x, tid = threadIdx.x, r16 = tid >> 4, l16 = tid & 15;
+  const int hl = r16 / SG, k = r16 % SG, hq = (int)blockIdx.y * HPW + hl;
   // row b's quantized partials: slots first .. first + ns - 1 (and slot extra); its exact partial: slot xs
   int64_t first = (int64_t)b * (ns + 1), xs = first + ns, extra = -1;
   if (S.groups > 0) {
@@ -1087,12 +1092,12 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
   const int nt = ns + (extra >= 0 ? 1 : 0);
   auto row_of = [&](int j) { return ((j < ns) ? first + j : extra) * 16 + hq; };
   float M = NEG_BIG, Ls = 0.f, xq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int j0 = k; j0 < nt; j0 += 64) {   // group k: partials j0, j0 + 16, j0 + 32, j0 + 48
+  for (int j0 = k; j0 < nt; j0 += 4 * SG) {   // group k: partials j0, j0 + SG, j0 + 2 SG, j0 + 3 SG
     float mv[4], lv[4];
     float4 a0[4], a1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j = j0 + 16 * i;
+      const int j = j0 + SG * i;
       const bool in = j < nt;
       const int64_t row = row_of(in ? j : j0);   // past the end: a repeat of partial j0, weighted 0 below
       mv[i] = in ? mo[row] : NEG_BIG;
@@ -1115,35 +1120,45 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
       for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
     }
   }
-  if (l16 == 0) { gm[k] = M; gl[k] = Ls; }
-  *reinterpret_cast<float4*>(&gx[k][8 * l16]) = make_float4(xq[0], xq[1], xq[2], xq[3]);
-  *reinterpret_cast<float4*>(&gx[k][8 * l16 + 4]) = make_float4(xq[4], xq[5], xq[6], xq[7]);
-  __syncthreads();
-  if (tid >= 64) return;   // wave 0 finishes (its four lane groups alike; group 0 writes)
-  // the exact partial and the 16 group states, relative to the largest max
+  if (SG > 1) {   // the head's SG group states, combined by its first group
+    if (l16 == 0) { gm[r16] = M; gl[r16] = Ls; }
+    *reinterpret_cast<float4*>(&gx[r16][8 * l16]) = make_float4(xq[0], xq[1], xq[2], xq[3]);
+    *reinterpret_cast<float4*>(&gx[r16][8 * l16 + 4]) = make_float4(xq[4], xq[5], xq[6], xq[7]);
+    __syncthreads();
+    if (k != 0) return;   // whole 16-lane rows leave; the FWHT below stays within each remaining row
+    M = NEG_BIG;
+#pragma unroll
+    for (int kk = 0; kk < SG; ++kk) M = fmaxf(M, gm[hl * SG + kk]);
+    Ls = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xq[e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < SG; ++kk) {
+      const int rr = hl * SG + kk;
+      const float wgt = exp2f(gm[rr] - M);   // 0 for groups without partials (their state is zero anyway)
+      Ls += wgt * gl[rr];
+      const float4 c0 = *reinterpret_cast<const float4*>(&gx[rr][8 * l16]);
+      const float4 c1 = *reinterpret_cast<const float4*>(&gx[rr][8 * l16 + 4]);
+      const float a[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
+    }
+  }
+  // the exact partial, relative to the larger max
   const int64_t xrow = xs * 16 + hq;
   const float Mx = mo[xrow], xl = lo[xrow];
   const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
   const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
-  M = Mx;
+  const float Mt = fmaxf(M, Mx);
+  {
+    const float al = exp2f(M - Mt);
+    Ls *= al;
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) M = fmaxf(M, gm[kk]);
-  Ls = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) xq[e] = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < 16; ++kk) {
-    const float wgt = exp2f(gm[kk] - M);   // 0 for groups without partials (their state is zero anyway)
-    Ls += wgt * gl[kk];
-    const float4 c0 = *reinterpret_cast<const float4*>(&gx[kk][8 * l16]);
-    const float4 c1 = *reinterpret_cast<const float4*>(&gx[kk][8 * l16 + 4]);
-    const float a[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xq[e] += wgt * a[e];
+    for (int e = 0; e < 8; ++e) xq[e] *= al;
   }
   float xe[8];
-  {   // exact partial
-    const float wgt = exp2f(Mx - M);
+  {
+    const float wgt = exp2f(Mx - Mt);
     Ls += wgt * xl;
     const float a[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
 #pragma unroll
@@ -1179,8 +1194,28 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     y1 = Ls > 0.f ? y1 / Ls : 0.f;
     o[e >> 1] = f2bf(y0) | (f2bf(y1) << 16);
   }
-  if (k == 0)
-    *reinterpret_cast<uint4*>(out + ((int64_t)b * 16 + hq) * 128 + 8 * l16) = make_uint4(o[0], o[1], o[2], o[3]);
+  *reinterpret_cast<uint4*>(out + ((int64_t)b * 16 + hq) * 128 + 8 * l16) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Heads per merge workgroup for about p partials per row. Whole decode, same process, HIP events (balanced plan; C3
+// rows of 32K for B <= 64, 4K-token rows above): B = 1 / 8 / 16 / 64 / 128 / 256 / 398 rows (127 / 64 / 32 / 8 / 4 /
+// 2 / 1-2 partials a row) 18.8 / 34.8 / 47.4 / 142 / 56.6 / 100.1 / 154.1 us with 1 head per workgroup, 22.8 / 36.8 /
+// 47.2 / 136.5 / 54.4 / 97.4 / 148.8 with 4, 35.9 / 44.1 / 51.1 / 139.9 / 53.7 / 95.3 / 145.8 with 16.
+int merge_hpw(int64_t p) { return p >= 16 ? 1 : p >= 6 ? 4 : 16; }
+
+// Launches the merge with hpw (1, 4 or 16) heads per workgroup.
+int launch_merge(const float* mo, const float* lo, const float* ao, int ns, const Sched& S, int64_t B, uint16_t* out,
+                 void* stream, int hpw) {
+  if (hpw == 16)
+    hipLaunchKernelGGL(decode_merge_kernel<16>, dim3((unsigned)B, 1), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, ns,
+                       S, out);
+  else if (hpw == 4)
+    hipLaunchKernelGGL(decode_merge_kernel<4>, dim3((unsigned)B, 4), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, ns,
+                       S, out);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<1>, dim3((unsigned)B, 16), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, ns,
+                       S, out);
+  return check_launch("decode_merge");
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -1316,9 +1351,7 @@ int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, in
   if (B == 0) return KV800_OK;
   KV800_REQUIRE(mo && lo && ao && out, "decode_merge: null pointer");
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B, 16), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns,
-                     Sched{nullptr, 0, (int)B, 0}, out);
-  return check_launch("decode_merge");
+  return launch_merge(mo, lo, ao, (int)ns, Sched{nullptr, 0, (int)B, 0}, B, out, stream, merge_hpw(ns + 1));
 }
 
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows) {
@@ -1447,9 +1480,8 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
                          scale, &X, S, stream)) != KV800_OK)
     return rc;
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)B, 16), dim3(256), 0, (hipStream_t)stream, mo, lo, ao, (int)ns, S,
-                     out);
-  return check_launch("decode_merge");
+  return launch_merge(mo, lo, ao, (int)ns, S, B, out, stream,
+                      merge_hpw(S.groups ? (S.groups + B - 1) / B + 1 : ns + 1));   // partials per row, about
 }
 
 int kv800_hip_decode(const kv800_paged_t* P, const uint16_t* q, int64_t B, const uint16_t* cos_t,
