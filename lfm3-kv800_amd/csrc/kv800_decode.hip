@@ -1073,8 +1073,14 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
   __shared__ __align__(16) float gx[SG > 1 ? 16 : 1][128];
   const int b = blockIdx.x, tid = threadIdx.x, r16 = tid >> 4, l16 = tid & 15;
   const int hl = r16 / SG, k = r16 % SG, hq = (int)blockIdx.y * HPW + hl;
-  // row b's quantized partials: slots first .. first + ns - 1 (and slot extra); its exact partial: slot xs
-  int64_t first = (int64_t)b * (ns + 1), xs = first + ns, extra = -1;
+  // row b's exact partial: slot xs, requested first (its slot needs no table); its quantized partials: slots
+  // first .. first + ns - 1 (and slot extra)
+  const int64_t xs = S.groups > 0 ? (int64_t)S.groups + S.B + b : (int64_t)b * (ns + 1) + ns;
+  const int64_t xrow = xs * 16 + hq;
+  const float Mx = mo[xrow], xl = lo[xrow];
+  const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
+  const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
+  int64_t first = (int64_t)b * (ns + 1), extra = -1;
   if (S.groups > 0) {
     const int cut = S.pre[S.B + 1];
     if (cut < 0) {   // row-wise: row b's slices are workgroups [pre[b], pre[b + 1]), one partial each
@@ -1086,7 +1092,6 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
       ns = nb > 0 ? (st + nb - 1) / C - (int)first + 1 : 0;
       if (nb > 0 && st % C != 0) extra = (int64_t)S.groups + b;     // the one that entered it from an earlier row
     }
-    xs = (int64_t)S.groups + S.B + b;
   }
   // partial j < nt: slot first + j for j < ns, the entering workgroup's slot for j = ns
   const int nt = ns + (extra >= 0 ? 1 : 0);
@@ -1145,10 +1150,6 @@ decode_merge_kernel(const float* __restrict__ mo, const float* __restrict__ lo, 
     }
   }
   // the exact partial, relative to the larger max
-  const int64_t xrow = xs * 16 + hq;
-  const float Mx = mo[xrow], xl = lo[xrow];
-  const float4 xa0 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16);
-  const float4 xa1 = *reinterpret_cast<const float4*>(ao + xrow * 128 + 8 * l16 + 4);
   const float Mt = fmaxf(M, Mx);
   {
     const float al = exp2f(M - Mt);
