@@ -41,7 +41,6 @@ constexpr float NEG_BIG = -1e30f;
 constexpr float LAZY = 8.f;   // log2 units a tile max may exceed the running max before the state is rescaled
 
 __device__ __forceinline__ uint32_t hbits(h2 x) { return __builtin_bit_cast(uint32_t, x); }
-__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 __device__ __forceinline__ h8 pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   u4v v = {a, b, c, d};
   return __builtin_bit_cast(h8, v);
@@ -1323,7 +1322,7 @@ int kv800_hip_decode_quant_sized(const uint16_t* q, const uint8_t* qpool, int64_
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, int64_t spb, float scale,
                                  void* stream) {
   return launch_quant(q, qpool, qpool_bytes, boff, boff_stride, nq, cs2, rope_rows, mo, lo, ao, B, ns, spb, scale,
-                      nullptr, Sched{nullptr, 0, (int)B, 0}, stream);
+                      nullptr, Sched{nullptr, 0, (int)B, 0, 0}, stream);
 }
 
 int kv800_hip_decode_quant(const uint16_t* q, const uint8_t* qpool, const int64_t* boff, int64_t boff_stride,
@@ -1352,7 +1351,7 @@ int kv800_hip_decode_merge(const float* mo, const float* lo, const float* ao, in
   if (B == 0) return KV800_OK;
   KV800_REQUIRE(mo && lo && ao && out, "decode_merge: null pointer");
   KV800_REQUIRE(((uintptr_t)ao % 16) == 0 && ((uintptr_t)out % 16) == 0, "decode_merge: ao / out must be 16-byte aligned");
-  return launch_merge(mo, lo, ao, (int)ns, Sched{nullptr, 0, (int)B, 0}, B, out, stream, merge_hpw(ns + 1));
+  return launch_merge(mo, lo, ao, (int)ns, Sched{nullptr, 0, (int)B, 0, 0}, B, out, stream, merge_hpw(ns + 1));
 }
 
 int64_t kv800_hip_decode_workspace(int64_t B, int64_t ns, int64_t rope_rows) {
@@ -1437,7 +1436,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   }
   // spb > 0: fixed (row, split) grid of spb sub-blocks per split; spb == 0: balanced schedule with the library's group
   // count; spb < 0: balanced schedule with -spb groups
-  Sched S{nullptr, 0, (int)B, (int)nqmax};
+  Sched S{nullptr, 0, (int)B, (int)nqmax, 0};
   int64_t ns, sp, slots;
   if (spb > 0) {
     sp = spb;
