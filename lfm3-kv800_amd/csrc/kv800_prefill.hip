@@ -24,9 +24,10 @@
 // statistics of a query live in the four lanes l % 16 and are combined with two cross-lane steps, and the O rescale
 // (lazy: only when a query's running max grows by more than PLAZY) needs no data movement. P^T's B operand is the
 // lane's 8 probabilities of keys 4 G + i and 16 + 4 G + i (G = l / 16) of each 32-key half, the key order in which
-// the transposed reads deliver V^T. The tiles are double-buffered in LDS (the next tile's loads, through a buffer
-// resource whose reads past the row's keys return zeros, are in flight while the current one is multiplied; one
-// barrier per tile), and a tile whose keys are all in range and precede the workgroup's first query is not masked.
+// the transposed reads deliver V^T. The tiles are double-buffered in LDS and loaded straight into it (buffer loads
+// with the lds modifier, through a buffer resource whose reads past the row's keys return zeros; the next tile's
+// loads are in flight while the current one is multiplied, one barrier per tile), and a tile whose keys are all in
+// range and precede the workgroup's first query is not masked.
 // Key tiles outside [first key a query of the workgroup can see, last key not in its future] are skipped: for window
 // layers only the sink keys and the keys of the window are read.
 // The grid is one workgroup per (KV head, 32-query tile), numbered so that each XCD runs whole (KV head, row) runs of
@@ -80,8 +81,9 @@ __device__ __forceinline__ uint32_t bfpk(float a, float b) {
 // computes query head 4 g + w for its 32 queries as two column blocks of 16. Every workgroup of the grid has work (a
 // grid whose idle workgroups sat at every other index put all the work on half the XCDs under round-robin dispatch),
 // and the workgroups of one (KV head, row) run on one XCD, in order, so the row's key tiles are read once into that
-// XCD's L2 for its 64 query tiles. Keys come in tiles of 64, staged in LDS as K and V rows and
-// double-buffered: the next tile's loads are in flight while the current one is multiplied, one barrier per tile. Per
+// XCD's L2 for its 64 query tiles. Keys come in tiles of 64, loaded into LDS as K and V rows by LDS-direct loads (no
+// register staging) and double-buffered: the next tile's loads are in flight while the current one is multiplied, one
+// barrier per tile. Per
 // wave and tile on f32_16x16x32_bf16: S^T = K . Q^T (keys x queries: 4 key blocks x 2 query blocks x 4 k-steps, every
 // K operand read once for both query blocks) and O^T += V^T . P^T (8 dim blocks x 2 query blocks x 2 k-steps; the
 // V^T operand is read from the V rows by two ds_read_b64_tr_b16, in the key order of the lane's own probabilities,
@@ -92,17 +94,17 @@ constexpr int PQ = 32;      // queries per workgroup = per interface tile (tile_
 constexpr int PPART = 132;  // floats per key-split partial of (query, head): 128 dims of o, m, l, 2 of padding
 constexpr int PMAXSPLIT = 256;
 constexpr int PK = 64;      // keys per LDS tile
-constexpr int KROW = 136;   // K tile row stride (elements): 272 B, rows 4 banks apart for the 16-byte A reads
-constexpr int VROW = 144;   // V tile row stride (elements): 288 B, conflict-free transposed reads
 
+// a tile as staged by LDS-direct loads: K and V rows of 256 bytes, unpadded, their 16-byte pieces permuted within
+// each row so that the operand reads spread over the banks: piece p of key row j at piece p ^ (j & 15) (K: 16 rows
+// read at one piece per instruction) and p ^ 2 (j & 7) (V: 32-byte pairs of pieces, 4 rows per 16 lanes)
 struct alignas(16) PTile {
-  uint16_t k[PK * KROW];
-  uint16_t v[PK * VROW];
+  uint16_t k[PK * 128];
+  uint16_t v[PK * 128];
   int32_t kp[PK];
 };
-struct alignas(16) PLds {
-  PTile t[2];
-};
+__device__ __forceinline__ int kswz(int j, int p) { return p ^ (j & 15); }
+__device__ __forceinline__ int vswz(int j, int p) { return p ^ (2 * (j & 7)); }
 constexpr float PLAZY = 8.f;   // log2 units a query's running max may lag its scores (p <= 2^8 in bf16)
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int RSRC_WORD3 = 0x00020000;   // raw (untyped, unswizzled) buffer access on gfx9-family parts
@@ -150,7 +152,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
                const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, const int32_t* __restrict__ kp,
                const int64_t* __restrict__ ksl, const int64_t* __restrict__ tile_off, int64_t R, int64_t window,
                int64_t nsink, float scale_log2, uint16_t* __restrict__ out, int splits, float* __restrict__ part) {
-  __shared__ __align__(16) PLds lds;
+  __shared__ PTile tA, tB;   // two buffers as two objects: a read of one is not held for the other's loads
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous run L = [x per + min(x, rem),
   // ...) of the (g, t, split) order (split fastest, then t), so the workgroups sharing a row's keys of one KV head
@@ -211,9 +213,8 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     if (i < n0) { k0 = (int64_t)i * PK; r1 = sink_end; }
     else { k0 = kbeg + (int64_t)(i - n0) * PK; r1 = kend; }
   };
-  u4v sk[4], sv[4];            // the next tile's K and V rows in flight
-  int32_t skp = 0;
-  auto fetch = [&](int i) {
+  int32_t skp = 0;             // the next tile's key positions (lanes < 64), stored with the tile's last reads done
+  auto fetch = [&](int i, PTile& T) {
     int64_t k0, r1;
     range_of(i, k0, r1);
     // the tile's K and V rows as buffers (base and size in SGPRs): a read past the row's S keys returns zeros, so every
@@ -223,36 +224,29 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
                                                         RSRC_WORD3);
     const rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(V + (ks + k0) * 512), (short)0, nbytes,
                                                         RSRC_WORD3);
+    // LDS-direct: instruction r of wave w fills key rows 16 r + 4 w .. + 3 (1 KB, lane l at byte 16 l); lane l
+    // fetches the global piece that belongs in its slot
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int c = tid + 256 * r, j = c >> 4, part = c & 15, off = j * 1024 + g * 256 + 16 * part;
-      sk[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-      sv[r] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+      const int j = 16 * r + 4 * w + (lane >> 4), qs = lane & 15;
+      const int base = j * 1024 + g * 256;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&T.k[(16 * r + 4 * w) * 128],
+                                               16, base + 16 * kswz(j, qs), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&T.v[(16 * r + 4 * w) * 128],
+                                               16, base + 16 * vswz(j, qs), 0, 0, 0);
     }
     if (tid < PK) skp = (k0 + tid < r1) ? (kpr ? kpr[k0 + tid] : (int32_t)(k0 + tid)) : 0x7FFFFFFF;
-  };
-  auto store = [&](PTile& T) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + 256 * r, j = c >> 4, part = c & 15;
-      *reinterpret_cast<u4v*>(&T.k[j * KROW + 8 * part]) = sk[r];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + 256 * r, j = c >> 4, part = c & 15;
-      *reinterpret_cast<u4v*>(&T.v[j * VROW + 8 * part]) = sv[r];
-    }
-    if (tid < PK) T.kp[tid] = skp;
+    // the loads write T behind the compiler's view of the buffer: its address escapes here
+    asm volatile("" ::"s"((uint32_t)(uintptr_t)&T) : "memory");
   };
 
   if (i0 < i1) {
-    fetch(i0);
-    store(lds.t[i0 & 1]);
+    fetch(i0, tA);
+    if (tid < PK) tA.kp[tid] = skp;
   }
   __syncthreads();
-  for (int i = i0; i < i1; ++i) {
-    const PTile& T = lds.t[i & 1];
-    if (i + 1 < i1) fetch(i + 1);
+  auto step = [&](int i, const PTile& T, PTile& Nx) {
+    if (i + 1 < i1) fetch(i + 1, Nx);
     // ---- S^T = K . Q^T: 4 blocks of 16 keys x 2 blocks of 16 queries
     f4 sc[2][4];
 #pragma unroll
@@ -260,7 +254,7 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
       f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u4v a = *reinterpret_cast<const u4v*>(&T.k[(nb * 16 + col) * KROW + 32 * s + 8 * G]);
+        const u4v a = *reinterpret_cast<const u4v*>(&T.k[(nb * 16 + col) * 128 + 8 * kswz(col, 4 * s + G)]);
         a0 = mfma_bf(a, qb[0][s], a0);
         a1 = mfma_bf(a, qb[1][s], a1);
       }
@@ -318,17 +312,18 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
     }
     // ---- O^T += V^T . P^T: 2 halves of 32 keys x 8 blocks of 16 dims x 2 query blocks. A = V^T (row = dim; K = the
     // half's keys 4 G .. 4 G + 3 and 16 + 4 G .. + 3, whose probabilities the lane holds) by two transposed reads
-    const int vrow = 4 * G + (col >> 2), vcol = 4 * (col & 3);
+    const int vrow = 4 * G + (col >> 2);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const u4v b0 = {pb[0][2 * hh][0], pb[0][2 * hh][1], pb[0][2 * hh + 1][0], pb[0][2 * hh + 1][1]};
       const u4v b1 = {pb[1][2 * hh][0], pb[1][2 * hh][1], pb[1][2 * hh + 1][0], pb[1][2 * hh + 1][1]};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        const int vo = 8 * vswz(vrow, 2 * j + ((col >> 1) & 1)) + 4 * (col & 1);   // rows vrow and vrow + 16 alike
         const s4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow) * VROW + 16 * j + vcol]));
+            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow) * 128 + vo]));
         const s4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow + 16) * VROW + 16 * j + vcol]));
+            (lds_s4*)const_cast<uint16_t*>(&T.v[(32 * hh + vrow + 16) * 128 + vo]));
         const u4v a = {__builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 0, 1)),
                        __builtin_bit_cast(uint32_t, __builtin_shufflevector(t0, t0, 2, 3)),
                        __builtin_bit_cast(uint32_t, __builtin_shufflevector(t1, t1, 0, 1)),
@@ -337,9 +332,14 @@ prefill_kernel(const uint16_t* __restrict__ q, const int64_t* __restrict__ qsl, 
         o[1][j] = mfma_bf(a, b1, o[1][j]);
       }
     }
-    // the next tile into the other buffer, whose last reads (tile i - 1) ended at the previous barrier
-    if (i + 1 < i1) store(lds.t[(i + 1) & 1]);
+    // the next tile's positions into its buffer, whose last reads (tile i - 1) ended at the previous barrier; the
+    // barrier waits for the tile's LDS-direct loads
+    if (i + 1 < i1 && tid < PK) Nx.kp[tid] = skp;
     __syncthreads();
+  };
+  for (int i = i0; i < i1; i += 2) {
+    step(i, tA, tB);
+    if (i + 1 < i1) step(i + 1, tB, tA);
   }
   // ---- normalise and write: lane holds dims 16 j + 4 G + 0..3 of query 16 cq + col. With a key split, the
   // unnormalised partial (o, m, l) of (query, head, split) instead: PPART floats, o relative to 2^m
