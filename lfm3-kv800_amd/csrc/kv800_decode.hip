@@ -90,9 +90,9 @@ __global__ void rope_table_kernel(const uint16_t* __restrict__ cos_t, const uint
 }
 
 // ---------------------------------------------------------------- exact tail + sinks
-// A workgroup of 4 waves takes NH KV heads of one row b (query rows 4 h .. 4 h + 3 of head h): NH = 4, one wave per
-// head; NH = 1, the 4 waves take the head's 32-token chunks in turn (wave w: chunks w, w + 4, ...) and merge their
-// states at the end. The tokens are the row's sinks, then its exact positions. Both products run on MFMA
+// A workgroup takes one KV head h of one row b (query rows 4 h .. 4 h + 3): with NW = 4 waves, the waves take the
+// head's 32-token chunks in turn (wave w: chunks w, w + 4, ...) and merge their states at the end; with NW = 1, its
+// one wave takes every chunk. The tokens are the row's sinks, then its exact positions. Both products run on MFMA
 // f32_16x16x32_bf16 with a 32-token chunk as two 16-token tiles u; lane (g, n) = (lane / 16, lane % 16):
 // - QK: A = the tile's K rows (row n = token 16 u + n; k-step s = dims 32 s + 8 g .. + 7), B = q (column n < 8 =
 //   query row n % 4, zero above). The RoPE pairs (j, j + 64), j < 32, are rotated in fp32 and rounded to bf16 by one
@@ -112,13 +112,15 @@ constexpr int XCH = 32;                // tokens per chunk
 constexpr int XPG = 64;                // page-table entries of the row kept in LDS (later pages are read from memory)
 constexpr int XVROW = 144;             // bf16 per staged V row: 128 + 16 padding spreads a tile's rows over the banks
 constexpr int XTROW = 132;             // floats per row of the end-of-row column dump
-struct XLds {
+template <int NW>                      // NW waves per workgroup
+struct XLdsT {
   int64_t pg[XPG];                     // element offsets of the row's exact pages, from page lo_e / ebs on
-  uint16_t v[4][XCH][XVROW];           // each wave's copy of its chunk's V rows; at the end its columns and (m, l)
-  u4v qb[4][4][64];                    // each wave's QK B operand: k-step s of lane l in qb[w][s][l]
-  float fm[4][4], fl[4][4];            // NH = 1: each wave's m and l of rows 0..3
-  float facc[4][4][128];               // NH = 1: each wave's accumulators of rows 0..3
+  uint16_t v[NW][XCH][XVROW];          // each wave's copy of its chunk's V rows; at the end its columns and (m, l)
+  u4v qb[NW][4][64];                   // each wave's QK B operand: k-step s of lane l in qb[w][s][l]
+  float fm[NW][4], fl[NW][4];          // 4 waves on one head: each wave's m and l of rows 0..3
+  float facc[NW][4][128];              // 4 waves on one head: each wave's accumulators of rows 0..3
 };
+typedef XLdsT<4> XLds;
 static_assert(sizeof(float) * (8 * XTROW + 8) <= sizeof(uint16_t) * XCH * XVROW, "column dump must fit the V copy");
 struct XChunk {                        // one chunk's data in registers; lane (g, r): token 16 u + r of tile u
   u4v k[2][4];                         // K dims 32 s + 8 g .. + 7
@@ -140,17 +142,17 @@ __device__ __forceinline__ f4 mfma_bf(b8 a, b8 b, f4 c) { return __builtin_amdgc
 // MERGE = false: writes the exact partial (m, l, acc) of the heads' rows into partial slot xslot.
 // MERGE = true : instead merges it with the ns quantized partials of those rows (slots b (ns + 1) + s, written before
 //                on the same stream) and writes the bf16 output rows, as decode_merge_kernel does for all 16 rows.
-template <int NH, bool MERGE>
-__device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, const kv800_paged_t& P,
+template <bool MERGE, int NW>
+__device__ __forceinline__ void exact_row(XLdsT<NW>& X, const int b, const int h0, const kv800_paged_t& P,
                                           const uint16_t* __restrict__ q,
                                           const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t,
                                           int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                                           float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao,
                                           int ns, int64_t xslot, float scale, int nsink, uint16_t* __restrict__ out) {
-  static_assert(NH == 1 || NH == 4, "a workgroup takes one KV head or all four");
-  constexpr int WPH = 4 / NH;          // waves per head
+  static_assert(NW == 1 || NW == 4, "a workgroup of 1 or 4 waves takes one KV head");
+  constexpr int WPH = NW;              // waves per head
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
-  const int hl = w / WPH, ph = w % WPH, h = h0 + hl;   // head slot, chunk phase, KV head
+  const int ph = w, h = h0;            // chunk phase, KV head
   const int n = P.N[b];
   int lo_e = P.NQ[b] * BLK;
   if (P.win > 0) lo_e = max(lo_e, n - (int)P.win);
@@ -407,7 +409,7 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
       *reinterpret_cast<uint32_t*>(out + ((int64_t)b * 16 + h * 4 + r) * 128 + dd) = f2bf(y0) | (f2bf(y1) << 16);
     }
   };
-  if constexpr (NH == 4) {
+  if constexpr (WPH == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) emit(r, mr[r], Lr[r], ar[r][0], ar[r][1]);
   } else {   // the 4 waves' states of each row, merged by wave r for row r
@@ -420,10 +422,10 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
     const int r = w;
     float M = NEG_BIG;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, X.fm[ww][r]);
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, X.fm[ww][r]);
     float L = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
+    for (int ww = 0; ww < NW; ++ww) {
       const float sc = exp2f(X.fm[ww][r] - M);
       const float2 a = *reinterpret_cast<const float2*>(&X.facc[ww][r][dd]);
       L += sc * X.fl[ww][r];
@@ -434,25 +436,23 @@ __device__ __forceinline__ void exact_row(XLds& X, const int b, const int h0, co
   }
 }
 
-// KV heads per workgroup of the exact-tail workgroups of the quantized grid, which must finish early to free their CUs
-// for the split work. The standalone partial-writing variant uses the tails' split, so its partials are bit-identical
-// to the ones the quantized grid computes in-grid. The fused exact kernel (window layers) takes NH = 1 while the 4 B
-// workgroups of that split fit one round of resident workgroups (more waves per row's chunks) and NH = 4 beyond
-// (one workgroup per row: fewer, longer workgroups keep more of the pool streaming per CU). MI355X, window 256 + 4
-// sinks at 32K: B = 64 / 96 / 128 take 14.0 / 19.0 / 19.6 us with NH = 1 and 25.1 / 25.3 / 25.3 us with NH = 4;
-// B = 160 / 192 / 256 / 398 take 27.1 / 28.6 / 33.3 / 50.2 us with NH = 1 and 25.4 / 25.5 / 27.4 / 45.7 us with NH = 4.
-constexpr int XNH_TAIL = 1;
-
-template <int NH, bool MERGE>
-__global__ void __launch_bounds__(256)
+// The exact-tail workgroups of the quantized grid take NW = 4 (a tail must finish early to free its CU for the split
+// work); the standalone partial-writing variant does the same, so its partials are bit-identical to the ones the
+// quantized grid computes in-grid. The fused exact kernel (window layers) takes NW = 4 while its 4 B workgroups fit
+// one round of resident workgroups (more waves on each head's chunks) and NW = 1 beyond: 4 B one-wave workgroups,
+// up to 8 resident per CU, spread the (row, head) streams over the CUs in units of one stream. MI355X, window 256 + 4
+// sinks at 32K: B = 64 / 96 / 128 take 14.0 / 19.0 / 19.6 us with NW = 4; B = 192 / 256 / 320 / 398 take 23.5 /
+// 25.5 / 33.1 / 42.6 us with NW = 1, against 23.5 / 25.5 / 42.2 / 43.4 us with one 4-wave workgroup per row (one
+// wave per head), whose 398 workgroups left 142 CUs with two rows and the rest with one.
+template <bool MERGE, int NW>
+__global__ void __launch_bounds__(64 * NW)
 decode_exact_kernel(kv800_paged_t P, const uint16_t* __restrict__ q, const uint16_t* __restrict__ cos_t,
                     const uint16_t* __restrict__ sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                     float* __restrict__ mo, float* __restrict__ lo_out, float* __restrict__ ao, int ns, float scale,
                     int nsink, uint16_t* __restrict__ out) {
-  __shared__ XLds X;
-  constexpr int G = 4 / NH;   // workgroups per row
-  const int b = blockIdx.x / G;
-  exact_row<NH, MERGE>(X, b, (blockIdx.x % G) * NH, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
+  __shared__ XLdsT<NW> X;
+  const int b = blockIdx.x / 4;   // 4 workgroups per row, one per KV head
+  exact_row<MERGE, NW>(X, b, blockIdx.x % 4, P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo,
                         lo_out, ao, ns, (int64_t)b * (ns + 1) + ns, scale, nsink, out);
 }
 
@@ -960,9 +960,8 @@ decode_quant_kernel(const uint16_t* __restrict__ q, const uint8_t* __restrict__ 
   __shared__ __align__(16) char lds_raw[QLDS_BYTES];
   const int nwork = (int)gridDim.x - X.nexact;
   if ((int)blockIdx.x >= nwork) {
-    constexpr int G = 4 / XNH_TAIL;   // workgroups per row
-    const int xb = (int)blockIdx.x - nwork, b = xb / G;
-    exact_row<XNH_TAIL, false>(*reinterpret_cast<XLds*>(lds_raw), b, (xb % G) * XNH_TAIL, X.P, q, X.cos_t,
+    const int xb = (int)blockIdx.x - nwork, b = xb / 4;   // 4 workgroups per row, one per KV head
+    exact_row<false, 4>(*reinterpret_cast<XLds*>(lds_raw), b, xb % 4, X.P, q, X.cos_t,
                                X.sin_t, X.rope_rows, X.epool_elems, X.sink_elems, mo, lo_out, ao, ns,
                                X.xs0 + b * X.xst, scale, X.nsink, nullptr);
     return;
@@ -1239,25 +1238,26 @@ int check_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t
   return KV800_OK;
 }
 
-// Launches decode_exact_kernel; with out != null the fused variant that also merges the quantized splits and writes
-// the bf16 rows, with nh (1 or 4) KV heads per workgroup.
+// Launches decode_exact_kernel, one workgroup per (row, KV head); with out != null the fused variant that also merges
+// the quantized splits and writes the bf16 rows, with nw (1 or 4) waves per workgroup (the partial-writing variant
+// always takes 4, as the quantized grid's tails do).
 int launch_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
                  int64_t rope_rows, int64_t epool_elems, int64_t sink_elems, float* mo, float* lo, float* ao, int64_t B,
-                 int64_t ns, float scale, uint16_t* out, int nh, void* stream) {
+                 int64_t ns, float scale, uint16_t* out, int nw, void* stream) {
   if (B == 0) return KV800_OK;
   int nsink = 0, rc;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &nsink)) != KV800_OK) return rc;
-  if (!out) nh = XNH_TAIL;
-  KV800_REQUIRE(nh == 1 || nh == 4, "decode_exact: 1 or 4 KV heads per workgroup");
-  const unsigned grid = (unsigned)(B * (4 / nh));
-  if (out && nh == 4)
-    hipLaunchKernelGGL((decode_exact_kernel<4, true>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
+  if (!out) nw = 4;
+  KV800_REQUIRE(nw == 1 || nw == 4, "decode_exact: 1 or 4 waves per workgroup");
+  const unsigned grid = (unsigned)(B * 4);
+  if (out && nw == 1)
+    hipLaunchKernelGGL((decode_exact_kernel<true, 1>), dim3(grid), dim3(64), 0, (hipStream_t)stream, *P, q, cos_t,
                        sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
   else if (out)
-    hipLaunchKernelGGL((decode_exact_kernel<1, true>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
+    hipLaunchKernelGGL((decode_exact_kernel<true, 4>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q, cos_t,
                        sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink, out);
   else
-    hipLaunchKernelGGL((decode_exact_kernel<XNH_TAIL, false>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q,
+    hipLaunchKernelGGL((decode_exact_kernel<false, 4>), dim3(grid), dim3(256), 0, (hipStream_t)stream, *P, q,
                        cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, (int)ns, scale, nsink,
                        (uint16_t*)nullptr);
   return check_launch(out ? "decode_exact_merge" : "decode_exact");
@@ -1336,7 +1336,7 @@ int kv800_hip_decode_exact_sized(const kv800_paged_t* P, const uint16_t* q, cons
                                  const uint16_t* sin_t, int64_t rope_rows, int64_t epool_elems, int64_t sink_elems,
                                  float* mo, float* lo, float* ao, int64_t B, int64_t ns, float scale, void* stream) {
   return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, ns, scale, nullptr,
-                      XNH_TAIL, stream);
+                      4, stream);
 }
 
 int kv800_hip_decode_exact(const kv800_paged_t* P, const uint16_t* q, const uint16_t* cos_t, const uint16_t* sin_t,
@@ -1430,8 +1430,8 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
     float* mo = (float*)ws;
     float* lo = (float*)(ws + align256(B * 16 * 4));
     float* ao = (float*)(ws + 2 * align256(B * 16 * 4));
-    const int nh = 4 * B <= resident_groups() ? 1 : 4;
-    return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, 0, scale, out, nh,
+    const int nw = 4 * B <= resident_groups() ? 4 : 1;
+    return launch_exact(P, q, cos_t, sin_t, rope_rows, epool_elems, sink_elems, mo, lo, ao, B, 0, scale, out, nw,
                         stream);
   }
   // spb > 0: fixed (row, split) grid of spb sub-blocks per split; spb == 0: balanced schedule with the library's group
@@ -1472,7 +1472,7 @@ int kv800_hip_decode_sized(const kv800_paged_t* P, const uint16_t* q, int64_t B,
   // quantized work and the exact tail in one grid, then the merge
   ExactArgs X{};
   X.P = *P; X.cos_t = cos_t; X.sin_t = sin_t; X.rope_rows = rope_rows; X.epool_elems = epool_elems;
-  X.sink_elems = sink_elems; X.nexact = (int)(B * (4 / XNH_TAIL));
+  X.sink_elems = sink_elems; X.nexact = (int)(B * 4);
   X.xs0 = S.groups ? B + S.groups : ns;
   X.xst = S.groups ? 1 : ns + 1;
   if ((rc = check_exact(P, q, cos_t, sin_t, epool_elems, mo, lo, ao, B, ns, out, &X.nsink)) != KV800_OK) return rc;
