@@ -275,6 +275,27 @@ def test_decode_shuffled_ragged(hip, oracle, win):
         close(bits_of(out), want, f"ragged win={win} spb={spb} groups={groups}")
 
 
+@pytest.mark.parametrize("B", [128, 129])
+def test_decode_window_either_side_of_one_wave_switch(hip, oracle, B):
+    """Window + sinks layer at the two batch sizes either side of the exact kernel's switch from 4-wave workgroups per
+    (row, KV head) to one-wave workgroups (4 B workgroups against one resident round, 512 on MI355X): ragged rows
+    (empty-window, sink-only and just-full rows among them), shuffled pages, every row against the oracle."""
+    rng = np.random.RandomState(400 + B)
+    lens = rng.randint(1, 700, size=B)
+    lens[:5] = [1, 4, 5, 260, 261]
+    K = [oracle.randn_bf16(rng, (int(n), 4, 128), offset=rng.standard_normal((1, 4, 128))) for n in lens]
+    V = [oracle.randn_bf16(rng, (int(n), 4, 128)) for n in lens]
+    q = oracle.randn_bf16(rng, (B, 16, 128), scale=1.5)
+    cos, sin = oracle.rope_tables(704)
+    case = oracle.build_paged(lambda b, p0, p1: (K[b][p0:p1], V[b][p0:p1]), lens, win=256, ebs=128,
+                              shuffle_seed=B)
+    say("decode window", B, "rows")
+    P = upload(case)
+    want = oracle.decode_f32(case, q, cos, sin)
+    out = hip.decode(P, to_dev_bf16(q), to_dev_bf16(cos), to_dev_bf16(sin))
+    close(bits_of(out), want, f"window B={B}")
+
+
 def test_decode_many_rows_few_groups(hip, oracle):
     """Balanced schedule with few workgroups over 150 ragged rows: a single workgroup (one slice per row), slices that
     start and end inside rows, rows without quantized sub-blocks between them."""
