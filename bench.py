@@ -13,7 +13,8 @@ whatever --warmup says: the C3 layer steps and the C3 kernel launches each at le
 GPU time (warm_up; the JSON records what ran), 200 flushes for C2, 20 steps for C4.
 Inputs are resident in HBM; two cache copies (2 x 450 MB, above the 256 MB MALL) alternate between steps. Prints one
 JSON line. roofline: the quantized-split kernel's algorithmic bytes (NQ * 51,200 per sequence) over its average
-duration, one HIP event pair per launch on its own stream; traffic from the committed rocprofv3 counter summary;
+launch duration, K launches back to back between one HIP event pair on their own stream; traffic from the
+committed rocprofv3 counter summary;
 cpu_baseline: a pure-torch CPU restatement of the reference's torch_decode.py on a sample of the same rows (the C
 oracle's time beside it). Extra
 fields: flush_c2 (config C2, the flush kernel alone), c4 (config 4, one decode step of all 6 attention
