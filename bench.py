@@ -4,7 +4,8 @@ tables), 16 query heads over 4 KV heads x 128 (the reference format's head shape
 32 / 8 / 64).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--c3-only] [--calib]
-                    [--c2-only | --c4-only | --prefill-only | --e2e-only [--e2e-which both|256|398] [--e2e-steps S]]
+                    [--c2-only | --c4-only | --prefill-only | --window-only | --e2e-only [--e2e-which both|256|398]
+                     [--e2e-steps S]]
 
 A step = one kv800.decode call over one layer (the quantized-split grid with the exact tail, then the split merge).
 Warm-up: the GPU reaches its sustained-load clocks only after tens of milliseconds of work (the first 50 C3 kernel
@@ -21,7 +22,8 @@ fields: flush_c2 (config C2, the flush kernel alone), c4 (config
 layers over 398 ragged sequences), e2e (config 5, greedy decode tok/s of an LFM3-shaped model over 256
 sequences), e2e_398x32k (the same loop at the reference's published point, 398 sequences of 32K tokens), prefill
 (prefill over compressed history: 8 rows x a 2048-token chunk over 16K-token histories, the attention kernel against
-the MFMA peak), fake_quant (training fake quantization of one layer's K and V), hbm_copy (a plain 1 GiB device
+the MFMA peak), fake_quant (training fake quantization of one layer's K and V), window_398 (one window + sinks layer
+of 398 rows at 32K context against the HBM peak), hbm_copy (a plain 1 GiB device
 copy: the bandwidth the box sustains) and hbm_read (a 4 GiB streaming read by kv800_hip_read_probe: the read
 bandwidth the part sustains for plain loads, and the decode kernel's achieved bandwidth as a fraction of it) and
 decode_small_batch (one decode layer's latency for 1, 8 and 16 rows of 32K tokens). Every
@@ -420,6 +422,60 @@ def bench_prefill(torch, kh, dev, steps, warmup):
 FQ_B, FQ_T = 8, 4096                                  # training batch of the fake-quant measurement
 
 
+WIN_R, WIN_W, WIN_SINKS = 398, 256, 4      # a window + sinks layer (LFM3 layers 2 / 18) at 398 rows of 32K context
+
+
+def bench_window(torch, kh, dev, steps, warmup):
+    """One window + sinks layer (vllm_attn.py:34: the last 256 positions and the 4 sinks) of 398 rows at 32,768 tokens
+    through the fused HIP decode (NQ = 0): 128-token exact pages in vLLM geometry, shuffled, N(0,1) K / V / sinks /
+    q. kv800_hip_decode_sized is called directly with its buffers allocated once, the K launches back to back between
+    one HIP event pair; 2,048 algorithmic bytes per (visible token, layer)."""
+    import ctypes
+    import lfm3_kv800_amd.kv800 as kv
+    g = torch.Generator(device=dev).manual_seed(61)
+    ebs, pages = 128, N_CTX // 128
+    lo = (N_CTX - WIN_W) // ebs
+    npg = WIN_R * (pages - lo)
+    eoff = torch.zeros(WIN_R, pages, dtype=torch.int64, device=dev)
+    eoff[:, lo:] = torch.randperm(npg, generator=g, device=dev).view(WIN_R, pages - lo) * (4 * ebs * 256)
+    epool = torch.randn(npg, 4, ebs, 256, generator=g, device=dev).to(torch.bfloat16)
+    sk = torch.randn(WIN_R, WIN_SINKS, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    sv = torch.randn(WIN_R, WIN_SINKS, 4, 128, generator=g, device=dev).to(torch.bfloat16)
+    so = torch.arange(WIN_R, device=dev, dtype=torch.int64) * (WIN_SINKS * 4 * 128)
+    P = kv.Paged(qpool=None, boff=None, epool=epool, eoff=eoff, ebs=ebs, e_hs=ebs * 256, e_ts=256, e_v=128, sk=sk,
+                 sv=sv, skoff=so, svoff=so.clone(), N=torch.full((WIN_R,), N_CTX, dtype=torch.int32, device=dev),
+                 NQ=torch.zeros(WIN_R, dtype=torch.int32, device=dev), nqmax=0, win=WIN_W)
+    q = torch.randn(WIN_R, 16, 128, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = rope_tables(torch, N_CTX + 64, dev)
+    assert torch.isfinite(kh.decode(P, q, cos, sin).float()).all()
+    L = kh.ops()
+    st, qbytes, eelems, selems = kh.paged_struct(P, WIN_R)
+    wsb = int(L.kv800_hip_decode_workspace(WIN_R, 0, 0))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    out = torch.empty(WIN_R, 16, 128, dtype=torch.bfloat16, device=dev)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def call():
+        rc = L.kv800_hip_decode_sized(ctypes.byref(st), ptr(q), WIN_R, ptr(cos), ptr(sin), cos.shape[0], None, qbytes,
+                                      eelems, selems, ptr(out), ptr(ws), wsb, 0, stream)
+        assert rc == 0, L.kv800_hip_last_error()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with frozen_heap():
+        for _ in range(warmup):
+            call()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    byt = WIN_R * (WIN_W + WIN_SINKS) * 2048
+    return {"workload": f"window + sinks layer ({WIN_W} + {WIN_SINKS} tokens) of {WIN_R} rows at {N_CTX} tokens, one "
+                        "workgroup of one wave per (row, KV head)", "us": round(us, 2), "bytes": byt,
+            "gbps": round(byt / (us * 1e-6) / 1e9, 1), "hbm_frac": round(byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_fake_quant(torch, kh, dev, steps, warmup):
     """Training fake quantization (train.py:82-100): one quantized layer's keys and values of a training
     batch of FQ_B sequences x FQ_T tokens, float32, 4 KV heads x 128: kv800_hip_fake_quant_k over (B, T / 256, 256,
@@ -586,6 +642,7 @@ def main():
     ap.add_argument("--c2-only", action="store_true", help="only the C2 flush (counter passes of the flush kernel)")
     ap.add_argument("--c4-only", action="store_true", help="only the C4 step; prints its record")
     ap.add_argument("--prefill-only", action="store_true", help="only the prefill workload; prints its record")
+    ap.add_argument("--window-only", action="store_true", help="only the 398-row window layer; prints its record")
     ap.add_argument("--e2e-steps", type=int, default=128)
     ap.add_argument("--e2e-which", choices=("both", "256", "398"), default="both",
                     help="with --e2e-only: the 256-sequence loop, the 398 x 32K one, or both")
@@ -612,6 +669,11 @@ def main():
 
     if a.c2_only:
         print(json.dumps({"flush_c2": bench_flush_c2(torch, kh, dev, a.steps, a.warmup)}), flush=True)
+        return
+
+    if a.window_only:
+        print(json.dumps({"window_398": bench_window(torch, kh, dev, max(a.steps, 20), max(a.warmup, 200))}),
+              flush=True)
         return
 
     if a.prefill_only:
@@ -737,7 +799,7 @@ def main():
     del layers, structs
     torch.cuda.empty_cache()
     extra_steps = max(5, min(a.steps, 20))
-    flush_c2 = c4 = e2e = e2e_398 = prefill = fake_quant = copy = read = None
+    flush_c2 = c4 = e2e = e2e_398 = prefill = fake_quant = copy = read = window = None
     if not a.c3_only:
         copy = bench_copy(torch, dev, 10)
         read = bench_read(torch, kh, dev, 10)
@@ -745,6 +807,8 @@ def main():
         prefill = bench_prefill(torch, kh, dev, max(3, min(a.steps, 10)), 2)
         torch.cuda.empty_cache()
         fake_quant = bench_fake_quant(torch, kh, dev, extra_steps, 5)
+        torch.cuda.empty_cache()
+        window = bench_window(torch, kh, dev, max(a.steps, 20), 200)
         torch.cuda.empty_cache()
         flush_c2 = bench_flush_c2(torch, kh, dev, extra_steps, 200)
         torch.cuda.empty_cache()
@@ -794,6 +858,7 @@ def main():
         "e2e_398x32k": e2e_398,
         "prefill": prefill,
         "fake_quant": fake_quant,
+        "window_398": window,
         "hbm_copy": copy,
         "hbm_read": read,
         "decode_small_batch": small,
